@@ -1,0 +1,324 @@
+"""ctypes binding of libhelrm_hip.so with the interface of Orion's Lattigo
+backend (orion/backend/lattigo/bindings.py:104-796): the same method names,
+argument conversion (Python lists -> C arrays, floats -> c_float) and
+{Data, Length} array results freed through FreeCArray.
+
+Orion selects a backend object in Scheme.setup_backend
+(orion/core/orion.py:100-126) and calls `setup_bindings(params)` on it; a
+`HipLibrary` is a drop-in for `LattigoLibrary` there.  Errors raise
+`HipError` with the library's message instead of aborting the process.
+"""
+import ctypes
+
+import numpy as np
+
+from . import library_path
+
+
+class HipError(RuntimeError):
+    pass
+
+
+class ArrayResultInt(ctypes.Structure):
+    _fields_ = [("Data", ctypes.POINTER(ctypes.c_int)), ("Length", ctypes.c_ulong)]
+
+
+class ArrayResultFloat(ctypes.Structure):
+    _fields_ = [("Data", ctypes.POINTER(ctypes.c_float)), ("Length", ctypes.c_ulong)]
+
+
+class ArrayResultUInt64(ctypes.Structure):
+    _fields_ = [("Data", ctypes.POINTER(ctypes.c_ulonglong)), ("Length", ctypes.c_ulonglong)]
+
+
+_ARRAY_TYPES = (ArrayResultInt, ArrayResultFloat, ArrayResultUInt64)
+
+
+class HipFunction:
+    """Wraps one C entry point: converts arguments as LattigoFunction does
+    (orion/backend/lattigo/bindings.py:9-97) and turns the -1 / empty-array
+    failure convention into HipError."""
+
+    lib = None
+
+    def __init__(self, func, argtypes, restype, checked=True):
+        self.func = func
+        self.func.argtypes = argtypes
+        self.func.restype = restype
+        self.checked = checked
+
+    def __call__(self, *args):
+        c_args = []
+        for arg in args:
+            typ = self.func.argtypes[len(c_args)]
+            c_arg = self._to_c(arg, typ)
+            if isinstance(c_arg, tuple):
+                c_args.extend(c_arg)
+            else:
+                c_args.append(c_arg)
+        res = self.func(*c_args)
+        if isinstance(res, _ARRAY_TYPES):
+            if not res.Data:
+                if self.checked and HipFunction.lib is not None:
+                    msg = HipFunction.lib.GetLastError().decode()
+                    if msg:
+                        raise HipError(msg)
+                return []
+            n = int(res.Length)
+            if isinstance(res, ArrayResultFloat):
+                out = np.ctypeslib.as_array(res.Data, shape=(n,)).astype(np.float64).tolist()
+            else:
+                out = [int(res.Data[i]) for i in range(n)]
+            HipFunction.lib.FreeCArray(ctypes.cast(res.Data, ctypes.c_void_p))
+            return out
+        if self.checked and self.func.restype is ctypes.c_int and res == -1:
+            raise HipError(HipFunction.lib.GetLastError().decode())
+        return res
+
+    @staticmethod
+    def _to_c(arg, typ):
+        if isinstance(arg, bool):
+            return ctypes.c_int(int(arg))
+        if isinstance(arg, (int, np.integer)) and typ in (ctypes.c_int, ctypes.c_ulong, ctypes.c_ulonglong, ctypes.c_uint64):
+            return typ(int(arg))
+        if isinstance(arg, float) and typ is ctypes.c_double:
+            return ctypes.c_double(arg)
+        if isinstance(arg, float):
+            return ctypes.c_float(arg)
+        if isinstance(arg, str):
+            return arg.encode("utf-8")
+        if isinstance(arg, np.ndarray):
+            if typ == ctypes.POINTER(ctypes.c_float):
+                a = np.ascontiguousarray(arg, dtype=np.float32)
+                return (a.ctypes.data_as(typ), len(a))
+            if typ == ctypes.POINTER(ctypes.c_int):
+                a = np.ascontiguousarray(arg, dtype=np.int32)
+                return (a.ctypes.data_as(typ), len(a))
+        if isinstance(arg, (list, tuple)):
+            if typ == ctypes.POINTER(ctypes.c_int):
+                return ((ctypes.c_int * len(arg))(*arg), len(arg))
+            if typ == ctypes.POINTER(ctypes.c_float):
+                a = np.ascontiguousarray(np.asarray(arg, dtype=np.float32))
+                return (a.ctypes.data_as(typ), len(a))
+            if typ == ctypes.POINTER(ctypes.c_uint64):
+                return ((ctypes.c_uint64 * len(arg))(*arg), len(arg))
+            raise ValueError("unexpected list argument type")
+        return arg
+
+
+_c = ctypes
+_I = _c.c_int
+_PI = _c.POINTER(_c.c_int)
+_PF = _c.POINTER(_c.c_float)
+_PU64 = _c.POINTER(_c.c_uint64)
+
+# name -> (argtypes, restype); argtypes follow orion/backend/lattigo/bindings.py
+_SIGNATURES = {
+    # scheme
+    "NewScheme": ([_I, _PI, _I, _PI, _I, _I, _I, _c.c_char_p, _c.c_char_p, _c.c_char_p], _I),
+    "DeleteScheme": ([], _I),
+    "NewSchemeWithModuli": ([_I, _PU64, _I, _PU64, _I, _I, _I, _c.c_uint64], _I),
+    "SetSchemeSeed": ([_c.c_uint64], None),
+    "GeneratePrimes": ([_I, _PI, _I, _PI, _I, _PU64, _PU64], _I),
+    "GetLastError": ([], _c.c_char_p),
+    # keys
+    "NewKeyGenerator": ([], _I),
+    "GenerateSecretKey": ([], _I),
+    "GeneratePublicKey": ([], _I),
+    "GenerateRelinearizationKey": ([], _I),
+    "GenerateEvaluationKeys": ([], _I),
+    # encoder
+    "NewEncoder": ([], _I),
+    "Encode": ([_PF, _I, _I, _c.c_ulong], _I),
+    "Decode": ([_I], ArrayResultFloat),
+    "DecodeDouble": ([_I, _c.POINTER(_c.c_double), _I], _I),
+    # encryptor
+    "NewEncryptor": ([], _I),
+    "NewDecryptor": ([], _I),
+    "Encrypt": ([_I], _I),
+    "Decrypt": ([_I], _I),
+    "SetEncryptionCounter": ([_c.c_uint64], _I),
+    # evaluator
+    "NewEvaluator": ([], _I),
+    "AddRotationKey": ([_I], _I),
+    "Rotate": ([_I, _I], _I),
+    "RotateNew": ([_I, _I], _I),
+    "Conjugate": ([_I], _I),
+    "ConjugateNew": ([_I], _I),
+    "Rescale": ([_I], _I),
+    "RescaleNew": ([_I], _I),
+    "AddPlaintext": ([_I, _I], _I),
+    "AddPlaintextNew": ([_I, _I], _I),
+    "SubPlaintext": ([_I, _I], _I),
+    "SubPlaintextNew": ([_I, _I], _I),
+    "AddCiphertext": ([_I, _I], _I),
+    "AddCiphertextNew": ([_I, _I], _I),
+    "SubCiphertext": ([_I, _I], _I),
+    "SubCiphertextNew": ([_I, _I], _I),
+    # linear transforms
+    "NewLinearTransformEvaluator": ([], _I),
+    "GenerateLinearTransform": ([_PI, _I, _PF, _I, _I, _c.c_float, _c.c_char_p], _I),
+    "EvaluateLinearTransform": ([_I, _I], _I),
+    "GetLinearTransformRotationKeys": ([_I], ArrayResultInt),
+    "GenerateLinearTransformRotationKey": ([_I], _I),
+    "DeleteLinearTransform": ([_I], _I),
+    "RemoveRotationKeys": ([], _I),
+    # tensors
+    "DeletePlaintext": ([_I], _I),
+    "DeleteCiphertext": ([_I], _I),
+    "GetPlaintextScale": ([_I], _c.c_ulong),
+    "GetCiphertextScale": ([_I], _c.c_ulong),
+    "GetCiphertextScaleDouble": ([_I], _c.c_double),
+    "GetPlaintextScaleDouble": ([_I], _c.c_double),
+    "SetPlaintextScale": ([_I, _c.c_ulong], _I),
+    "SetCiphertextScale": ([_I, _c.c_ulong], _I),
+    "GetPlaintextLevel": ([_I], _I),
+    "GetCiphertextLevel": ([_I], _I),
+    "GetPlaintextSlots": ([_I], _I),
+    "GetCiphertextSlots": ([_I], _I),
+    "GetCiphertextDegree": ([_I], _I),
+    "GetModuliChain": ([], ArrayResultUInt64),
+    "GetAuxModuliChain": ([], ArrayResultUInt64),
+    "GetLivePlaintexts": ([], ArrayResultInt),
+    "GetLiveCiphertexts": ([], ArrayResultInt),
+    "FreeCArray": ([_c.c_void_p], None),
+    # raw residues / measurement
+    "ExportCiphertext": ([_I, _PU64, _c.c_size_t, _I], _I),
+    "ImportCiphertext": ([_PU64, _I, _c.c_double, _I], _I),
+    "ExportPlaintext": ([_I, _PU64, _c.c_size_t, _I], _I),
+    "ImportPlaintext": ([_PU64, _I, _c.c_double, _I], _I),
+    "ExportGaloisKey": ([_c.c_uint64, _PU64, _c.c_size_t], _I),
+    "ExportSecretKey": ([_c.POINTER(_c.c_int64), _c.c_size_t], _I),
+    "ExportLinearTransformDiagonal": ([_I, _I, _PU64, _c.c_size_t], _I),
+    "GetLinearTransformInfo": ([_I, _PI, _I], _I),
+    "GetSchemeInfo": ([_PI, _I], _I),
+    "Synchronize": ([], _I),
+    "GetStream": ([], _c.c_void_p),
+    "KernelTimingEnable": ([_I], _I),
+    "KernelTimingGet": ([_c.c_char_p, _c.POINTER(_c.c_long), _c.POINTER(_c.c_double)], _I),
+    "GetMemoryStats": ([_PU64, _PU64, _PU64], _I),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_lib_handle = None
+
+
+def load_library():
+    """dlopen libhelrm_hip.so once (raises if it has not been built)."""
+    global _lib_handle
+    if _lib_handle is None:
+        _lib_handle = ctypes.CDLL(library_path())
+        HipFunction.lib = _lib_handle
+        _lib_handle.GetLastError.restype = ctypes.c_char_p
+        _lib_handle.GetLastError.argtypes = []
+        _lib_handle.FreeCArray.argtypes = [ctypes.c_void_p]
+        _lib_handle.FreeCArray.restype = None
+    return _lib_handle
+
+
+class HipLibrary:
+    """Drop-in for orion.backend.lattigo.bindings.LattigoLibrary."""
+
+    # EvaluateLinearTransform returns an un-rescaled ciphertext, as Lattigo's
+    # (orion/backend/python/lt_evaluator.py:268-273 reads this flag).
+    lt_output_prerescaled = False
+
+    def __init__(self):
+        self.lib = load_library()
+        for name, (argtypes, restype) in _SIGNATURES.items():
+            setattr(self, name, HipFunction(getattr(self.lib, name), list(argtypes), restype))
+
+    # orion/backend/lattigo/bindings.py:127-138
+    def setup_bindings(self, orion_params):
+        self.setup_scheme(orion_params)
+
+    # orion/backend/lattigo/bindings.py:140-187
+    def setup_scheme(self, orion_params):
+        logn = orion_params.get_logn()
+        logq = orion_params.get_logq()
+        logp = orion_params.get_logp()
+        logscale = orion_params.get_logscale()
+        h = orion_params.get_hamming_weight()
+        ringtype = orion_params.get_ringtype()
+        keys_path = orion_params.get_keys_path()
+        io_mode = orion_params.get_io_mode()
+        seed = getattr(orion_params, "get_seed", lambda: None)()
+        if seed is not None:
+            self.SetSchemeSeed(int(seed))
+        self.NewScheme(logn, list(logq), list(logp), logscale, h, ringtype, keys_path, io_mode)
+
+    # -- helpers for parity checks and benchmarks (numpy views of raw residues)
+    def export_ciphertext(self, ct_id, coeff=False):
+        level = self.GetCiphertextLevel(ct_id)
+        n = 1 << self._logn()
+        buf = np.zeros((2, level + 1, n), dtype=np.uint64)
+        self.ExportCiphertext(ct_id, buf.ctypes.data_as(_PU64), buf.size, int(coeff))
+        return buf
+
+    def import_ciphertext(self, data, level, scale, coeff=False):
+        data = np.ascontiguousarray(data, dtype=np.uint64)
+        return self.ImportCiphertext(data.ctypes.data_as(_PU64), level, float(scale), int(coeff))
+
+    def export_plaintext(self, pt_id, coeff=False):
+        level = self.GetPlaintextLevel(pt_id)
+        n = 1 << self._logn()
+        buf = np.zeros((level + 1, n), dtype=np.uint64)
+        self.ExportPlaintext(pt_id, buf.ctypes.data_as(_PU64), buf.size, int(coeff))
+        return buf
+
+    def import_plaintext(self, data, level, scale, coeff=False):
+        data = np.ascontiguousarray(data, dtype=np.uint64)
+        return self.ImportPlaintext(data.ctypes.data_as(_PU64), level, float(scale), int(coeff))
+
+    def export_galois_key(self, galel):
+        L = len(self.GetModuliChain())
+        K = len(self.GetAuxModuliChain())
+        n = 1 << self._logn()
+        dnum = (L + K - 1) // K
+        buf = np.zeros((dnum, 2, L + K, n), dtype=np.uint64)
+        self.ExportGaloisKey(int(galel), buf.ctypes.data_as(_PU64), buf.size)
+        return buf
+
+    def export_secret_key(self):
+        n = 1 << self._logn()
+        buf = np.zeros(n, dtype=np.int64)
+        self.ExportSecretKey(buf.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), n)
+        return buf
+
+    def export_lt_diagonal(self, lt_id, diag, level):
+        K = len(self.GetAuxModuliChain())
+        n = 1 << self._logn()
+        buf = np.zeros((level + 1 + K, n), dtype=np.uint64)
+        self.ExportLinearTransformDiagonal(lt_id, int(diag), buf.ctypes.data_as(_PU64), buf.size)
+        return buf
+
+    def lt_info(self, lt_id):
+        out = (ctypes.c_int * 4)()
+        self.GetLinearTransformInfo(lt_id, out, 4)
+        return {"N1": out[0], "giant": out[1], "baby": out[2], "plaintexts": out[3]}
+
+    def decode_double(self, pt_id):
+        n = 1 << (self._logn() - 1)
+        buf = np.zeros(n, dtype=np.float64)
+        self.DecodeDouble(pt_id, buf.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), n)
+        return buf
+
+    def kernel_time(self, name):
+        cnt = ctypes.c_long(0)
+        tot = ctypes.c_double(0.0)
+        self.KernelTimingGet(name, ctypes.byref(cnt), ctypes.byref(tot))
+        return int(cnt.value), float(tot.value)
+
+    def memory_stats(self):
+        a, b, c = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        self.GetMemoryStats(ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
+        return {"live": a.value, "cached": b.value, "peak": c.value}
+
+    def scheme_info(self):
+        out = (ctypes.c_int * 6)()
+        self.GetSchemeInfo(out, 6)
+        return {"logN": out[0], "L": out[1], "K": out[2], "dnum": out[3], "logscale": out[4], "h": out[5]}
+
+    def _logn(self):
+        return self.scheme_info()["logN"]

@@ -1,0 +1,84 @@
+// kernels.h -- launch interface of kernels.hip (internal to the library).
+#pragma once
+#include "hipckks.h"
+
+struct NttTables {
+  const ModC* mods;
+  const u64 *w, *wp, *iw, *iwp;  // [mod][N] bit-reversed psi powers and Shoup companions
+  const u64 *ninv, *ninvp;       // [mod]
+};
+
+struct BConvSrc {
+  u64 q, hinv, hinvp;  // source modulus, (S/s_i)^-1 mod s_i and its Shoup companion
+  double qd;           // (double)q
+};
+struct BConvTable {
+  BConvSrc src[HCK_MAXSRC];
+  const u64* hat;  // [nmod][ns]   (S/s_i mod t) * R mod t  (Montgomery form)
+  const u64* vS;   // [nmod][ns+1] v*S mod t
+  int rows_per_block;
+};
+
+struct KeyMacArgs {
+  const u64* digits;       // [dn][nqp][N] (per batch if digits_per_batch)
+  size_t dig_bstride;
+  int digits_per_batch;
+  const u64* const* key;   // per batch: [dnum][2][L+K][N] Montgomery form
+  const uint32_t* const* perm;  // per batch (nullptr: identity)
+  const u64* add0;         // Q rows added to part 0 before the gather (mode 1)
+  u64 *out0, *out1;
+  size_t out_bstride;
+  const ModC* mods;
+  int N, l, L, K, nqp, dn;
+};
+
+struct GiantAccArgs {
+  const u64* digits;  // [ng][dn][nqp][N]
+  size_t dig_bstride;
+  const u64* const* key;       // [ng]
+  const uint32_t* const* perm; // [ng]
+  const int* tg;               // giant-group index into T per key-switched group
+  int ng;
+  const u64* T;                // [ngroups][2][nqp][N]
+  size_t T_gstride, T_pstride;
+  int t_zero;                  // index of the rotation-0 group in T, or -1
+  u64 *out0, *out1;            // QP accumulators [nqp][N]
+  const ModC* mods;
+  int N, l, L, K, nqp, dn;
+};
+
+struct DiagMacArgs {
+  const u64* diag;        // [np][lt_level+1+K][N] Montgomery form
+  size_t diag_stride;
+  const u64* R;           // hoisted rotations [slot][2][nqp][N]
+  size_t R_bstride, R_pstride;
+  const u64* pc;          // P*c0, P*c1 : [2][l+1][N]
+  size_t pc_pstride;
+  const int* baby_is_zero;  // [nbaby]
+  const int* baby_slot;     // [nbaby]
+  const uint64_t* gmask;    // [ng] bit b: baby b present in group g
+  const int* gpidx;         // [ng] first plaintext index of group g
+  u64* T;                   // [ng][2][nqp][N]
+  size_t T_gstride, T_pstride;
+  const ModC* mods;
+  int N, l, L, K, nqp, lt_level, ng, nbaby, b0, nb_chunk;
+};
+
+void launch_ntt(u64* data, size_t bstride, int batch, RowMap rm, int logN, bool forward, const NttTables& tw, hipStream_t st);
+void launch_add(u64* out, const u64* a, const u64* b, size_t bstride, int batch, RowMap rm, const ModC* mods, int N, bool sub, hipStream_t st);
+void launch_mul_const(u64* out, const u64* in, size_t bstride, int batch, RowMap rm, const u64* cw, const u64* cwp, const ModC* mods, int N, hipStream_t st);
+void launch_mont_mul(u64* out, size_t obstride, const u64* a, size_t abstride, const u64* bR, size_t bbstride, int batch, RowMap rm, const ModC* mods, int N, bool acc, hipStream_t st);
+void launch_mont_convert(u64* data, size_t bstride, int batch, RowMap rm, const ModC* mods, int N, bool to, hipStream_t st);
+void launch_permute(u64* out, const u64* in, size_t bstride, int batch, int rows, const uint32_t* perm, int N, hipStream_t st);
+void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable& tab, u64* out, size_t out_bstride, int batch, const RowList& rl, const ModC* mods, int N, bool force_v0, hipStream_t st);
+void launch_moddown_combine(u64* out, size_t o_bstride, const u64* x, size_t x_bstride, const u64* ext, size_t e_bstride, const u64* add, size_t a_bstride, int add_batches, const uint32_t* perm, const u64* pinv, const u64* pinvp, int qrows, int batch, const ModC* mods, int N, hipStream_t st);
+void launch_keymac(const KeyMacArgs& a, int batch, hipStream_t st);
+void launch_giant_acc(const GiantAccArgs& a, hipStream_t st);
+void launch_diag_mac(const DiagMacArgs& a, hipStream_t st);
+void launch_rescale_spread(u64* t, const u64* u, int l, u64 half, const ModC* mods, int N, hipStream_t st);
+void launch_rescale_combine(u64* out, const u64* x, const u64* t, int l, const u64* inv, const u64* invp, const ModC* mods, int N, hipStream_t st);
+void launch_sample_uniform(u64* out, RowMap rm, u64 seed, u64 stream, const ModC* mods, int N, hipStream_t st);
+void launch_sample_cbd(u64* out, RowMap rm, u64 seed, u64 stream, const ModC* mods, int N, bool add, hipStream_t st);
+void launch_signed_rows(u64* out, RowMap rm, const int8_t* v, const ModC* mods, int N, hipStream_t st);
+void launch_gk_combine(u64* b, const u64* a, const u64* soR, const u64* sR, int own0, int own1, const u64* pmod, int rows, const ModC* mods, int N, hipStream_t st);
+void launch_encode_residues(u64* out, RowMap rm, const u64* rec, const ModC* mods, int N, hipStream_t st);

@@ -1,0 +1,516 @@
+// kernels.hip -- gfx950 kernels of the CKKS backend.  Integer RNS arithmetic
+// on the VALU (64-bit words, 128-bit lazy accumulation, one Montgomery REDC
+// per output word); no MFMA: this is modular arithmetic, not a float
+// contraction.  Every kernel is launched on the scheme's stream by the
+// wrappers at the bottom of this file.
+#include "hipckks.h"
+#include "kernels.h"
+
+// ---------------------------------------------------------------------------
+// Negacyclic NTT.  One LDS tile of E = 2^logE words per workgroup.  A
+// "contiguous" pass covers butterfly distances t < E on E consecutive words;
+// a "strided" pass covers the large distances on R rows x TC columns
+// (column stride C = N/R).  Forward: Cooley-Tukey, distances N/2 .. 1,
+// twiddle psi_rev[N/(2t) + j/(2t)].  Inverse: Gentleman-Sande, distances
+// 1 .. N/2, twiddle psi_inv_rev[N/(2t) + j/(2t)], then N^-1.
+// ---------------------------------------------------------------------------
+constexpr int NTT_THREADS = 512;
+
+template <bool FWD, bool STRIDED>
+__global__ __launch_bounds__(NTT_THREADS) void ntt_pass_kernel(
+    u64* __restrict__ data, size_t bstride, RowMap rm, int logN, int logE, int logR,
+    int lt_first, int lt_last, int scale_last, NttTables tw) {
+  extern __shared__ u64 sm[];
+  const int N = 1 << logN, E = 1 << logE;
+  const int row = rm.row(blockIdx.y);
+  const int m = rm.mod(row);
+  const u64 q = tw.mods[m].q;
+  u64* poly = data + (size_t)blockIdx.z * bstride + (size_t)row * N;
+  const u64* W = (FWD ? tw.w : tw.iw) + (size_t)m * N;
+  const u64* Wp = (FWD ? tw.wp : tw.iwp) + (size_t)m * N;
+  const int logTC = logE - logR;
+  const int logC = logN - logR;
+  const int TC = 1 << logTC;
+  size_t base = 0;
+  if (STRIDED) base = (size_t)blockIdx.x * TC; else base = (size_t)blockIdx.x * E;
+  for (int e = threadIdx.x; e < E; e += NTT_THREADS) {
+    size_t g = STRIDED ? base + (e & (TC - 1)) + ((size_t)(e >> logTC) << logC) : base + e;
+    sm[e] = poly[g];
+  }
+  __syncthreads();
+  const int step = FWD ? -1 : 1;
+  for (int lt = lt_first;; lt += step) {
+    const int t = 1 << lt;
+    for (int p = threadIdx.x; p < (E >> 1); p += NTT_THREADS) {
+      int e1; size_t glob;
+      if (STRIDED) {
+        int ltk = lt - logC;
+        int c = p & (TC - 1), kk = p >> logTC;
+        int k = ((kk >> ltk) << (ltk + 1)) | (kk & ((1 << ltk) - 1));
+        e1 = (k << logTC) | c;
+        glob = base + c + ((size_t)k << logC);
+      } else {
+        int j = ((p >> lt) << (lt + 1)) | (p & (t - 1));
+        e1 = j;
+        glob = base + j;
+      }
+      const int e2 = e1 + (STRIDED ? (t >> logC) << logTC : t);
+      const size_t wi = (size_t)(N >> (lt + 1)) + (glob >> (lt + 1));
+      const u64 w = W[wi], wp = Wp[wi];
+      u64 U = sm[e1], V = sm[e2];
+      if (FWD) {
+        V = shoup_mul(V, w, wp, q);
+        sm[e1] = add_mod(U, V, q);
+        sm[e2] = sub_mod(U, V, q);
+      } else {
+        sm[e1] = add_mod(U, V, q);
+        sm[e2] = shoup_mul(sub_mod(U, V, q), w, wp, q);
+      }
+    }
+    __syncthreads();
+    if (lt == lt_last) break;
+  }
+  const u64 ni = tw.ninv[m], nip = tw.ninvp[m];
+  for (int e = threadIdx.x; e < E; e += NTT_THREADS) {
+    size_t g = STRIDED ? base + (e & (TC - 1)) + ((size_t)(e >> logTC) << logC) : base + e;
+    u64 v = sm[e];
+    if (scale_last) v = shoup_mul(v, ni, nip, q);
+    poly[g] = v;
+  }
+}
+
+void launch_ntt(u64* data, size_t bstride, int batch, RowMap rm, int logN, bool forward,
+                const NttTables& tw, hipStream_t st) {
+  const int N = 1 << logN;
+  const int logE = logN < 12 ? logN : 12;
+  const int E = 1 << logE;
+  const int rows = rm.nact();
+  if (rows <= 0 || batch <= 0) return;
+  const size_t shm = (size_t)E * sizeof(u64);
+  if (logN <= logE) {
+    dim3 grid(1, rows, batch);
+    if (forward)
+      hipLaunchKernelGGL((ntt_pass_kernel<true, false>), grid, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, 0, logN - 1, 0, 0, tw);
+    else
+      hipLaunchKernelGGL((ntt_pass_kernel<false, false>), grid, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, 0, 0, logN - 1, 1, tw);
+    return;
+  }
+  // two passes: strided pass owns the logR largest distances
+  const int logR = logN / 2;
+  const int logC = logN - logR;
+  dim3 gridS(N >> logE, rows, batch), gridC(N >> logE, rows, batch);
+  if (forward) {
+    hipLaunchKernelGGL((ntt_pass_kernel<true, true>), gridS, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, logR, logN - 1, logC, 0, tw);
+    hipLaunchKernelGGL((ntt_pass_kernel<true, false>), gridC, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, 0, logC - 1, 0, 0, tw);
+  } else {
+    hipLaunchKernelGGL((ntt_pass_kernel<false, false>), gridC, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, 0, 0, logC - 1, 0, tw);
+    hipLaunchKernelGGL((ntt_pass_kernel<false, true>), gridS, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, logR, logC, logN - 1, 1, tw);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Element-wise kernels over (coefficient, row, batch)
+// ---------------------------------------------------------------------------
+__global__ void add_rows_kernel(u64* __restrict__ out, const u64* __restrict__ a, const u64* __restrict__ b,
+                                size_t bstride, RowMap rm, const ModC* __restrict__ mods, int N, int sub) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  int row = rm.row(blockIdx.y);
+  u64 q = mods[rm.mod(row)].q;
+  size_t o = (size_t)blockIdx.z * bstride + (size_t)row * N + x;
+  out[o] = sub ? sub_mod(a[o], b[o], q) : add_mod(a[o], b[o], q);
+}
+void launch_add(u64* out, const u64* a, const u64* b, size_t bstride, int batch, RowMap rm, const ModC* mods, int N, bool sub, hipStream_t st) {
+  if (rm.nact() <= 0 || batch <= 0) return;
+  hipLaunchKernelGGL(add_rows_kernel, dim3(N / 256, rm.nact(), batch), dim3(256), 0, st, out, a, b, bstride, rm, mods, N, sub ? 1 : 0);
+}
+
+// out = in * c_row (per-row constant in Shoup form, indexed by modulus)
+__global__ void mul_const_kernel(u64* __restrict__ out, const u64* __restrict__ in, size_t bstride, RowMap rm,
+                                 const u64* __restrict__ cw, const u64* __restrict__ cwp, const ModC* __restrict__ mods, int N) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  int row = rm.row(blockIdx.y);
+  int m = rm.mod(row);
+  size_t o = (size_t)blockIdx.z * bstride + (size_t)row * N + x;
+  out[o] = shoup_mul(in[o], cw[m], cwp[m], mods[m].q);
+}
+void launch_mul_const(u64* out, const u64* in, size_t bstride, int batch, RowMap rm, const u64* cw, const u64* cwp,
+                      const ModC* mods, int N, hipStream_t st) {
+  if (rm.nact() <= 0 || batch <= 0) return;
+  hipLaunchKernelGGL(mul_const_kernel, dim3(N / 256, rm.nact(), batch), dim3(256), 0, st, out, in, bstride, rm, cw, cwp, mods, N);
+}
+
+// out = a * bR * R^-1 (b stored in Montgomery form); optional accumulate
+__global__ void mont_mul_kernel(u64* __restrict__ out, const u64* __restrict__ a, size_t abstride,
+                                const u64* __restrict__ bR, size_t bbstride, size_t obstride, RowMap rm,
+                                const ModC* __restrict__ mods, int N, int acc) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  int row = rm.row(blockIdx.y);
+  ModC mc = mods[rm.mod(row)];
+  u64 r = mont_mul(a[(size_t)blockIdx.z * abstride + (size_t)row * N + x], bR[(size_t)blockIdx.z * bbstride + (size_t)row * N + x], mc.q, mc.qinv);
+  size_t o = (size_t)blockIdx.z * obstride + (size_t)row * N + x;
+  out[o] = acc ? add_mod(out[o], r, mc.q) : r;
+}
+void launch_mont_mul(u64* out, size_t obstride, const u64* a, size_t abstride, const u64* bR, size_t bbstride, int batch,
+                     RowMap rm, const ModC* mods, int N, bool acc, hipStream_t st) {
+  if (rm.nact() <= 0 || batch <= 0) return;
+  hipLaunchKernelGGL(mont_mul_kernel, dim3(N / 256, rm.nact(), batch), dim3(256), 0, st, out, a, abstride, bR, bbstride, obstride, rm, mods, N, acc ? 1 : 0);
+}
+
+// v -> v*R mod q (to Montgomery form) or v*R^-1 (from), in place
+__global__ void mont_convert_kernel(u64* __restrict__ data, size_t bstride, RowMap rm, const ModC* __restrict__ mods, int N, int to) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  int row = rm.row(blockIdx.y);
+  ModC mc = mods[rm.mod(row)];
+  size_t o = (size_t)blockIdx.z * bstride + (size_t)row * N + x;
+  u64 v = data[o];
+  data[o] = to ? mont_mul(v, mc.r2, mc.q, mc.qinv) : redc(v, 0, mc.q, mc.qinv);
+}
+void launch_mont_convert(u64* data, size_t bstride, int batch, RowMap rm, const ModC* mods, int N, bool to, hipStream_t st) {
+  if (rm.nact() <= 0 || batch <= 0) return;
+  hipLaunchKernelGGL(mont_convert_kernel, dim3(N / 256, rm.nact(), batch), dim3(256), 0, st, data, bstride, rm, mods, N, to ? 1 : 0);
+}
+
+// out[row][i] = in[row][perm[i]]
+__global__ void permute_kernel(u64* __restrict__ out, const u64* __restrict__ in, size_t bstride, int rows, const uint32_t* __restrict__ perm, int N) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  size_t o = (size_t)blockIdx.z * bstride + (size_t)blockIdx.y * N;
+  out[o + i] = in[o + perm[i]];
+}
+void launch_permute(u64* out, const u64* in, size_t bstride, int batch, int rows, const uint32_t* perm, int N, hipStream_t st) {
+  if (rows <= 0 || batch <= 0) return;
+  hipLaunchKernelGGL(permute_kernel, dim3(N / 256, rows, batch), dim3(256), 0, st, out, in, bstride, rows, perm, N);
+}
+
+// ---------------------------------------------------------------------------
+// RNS basis extension (exact, float64 overflow count as Lattigo ModUpExact):
+//   y_i = x_i * (S/s_i)^-1 mod s_i;  v = (u64) sum_i (double)y_i/(double)s_i
+//   out_t = sum_i y_i * (S/s_i mod t) - v*S mod t
+// One thread per coefficient; the source residues stay in registers and
+// every destination row is produced from them (read ns, write nd words).
+// ---------------------------------------------------------------------------
+template <int MAXS>
+__global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, size_t in_bstride, int ns,
+                                                    BConvTable tab, u64* __restrict__ out, size_t out_bstride,
+                                                    RowList rl, const ModC* __restrict__ mods, int N, int force_v0) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  const u64* inb = in + (size_t)blockIdx.z * in_bstride;
+  u64* outb = out + (size_t)blockIdx.z * out_bstride;
+  u64 y[MAXS];
+  double vf = 0.0;
+#pragma unroll
+  for (int i = 0; i < MAXS; i++) {
+    if (i < ns) {
+      const BConvSrc s = tab.src[i];
+      y[i] = shoup_mul(inb[(size_t)i * N + x], s.hinv, s.hinvp, s.q);
+      vf += (double)y[i] / s.qd;
+    }
+  }
+  const int v = force_v0 ? 0 : (int)(u64)vf;
+  const int r0 = blockIdx.y * tab.rows_per_block;
+  int r1 = r0 + tab.rows_per_block;
+  if (r1 > rl.n) r1 = rl.n;
+  for (int r = r0; r < r1; r++) {
+    const int m = rl.mod[r];
+    const ModC mc = mods[m];
+    const u64* h = tab.hat + (size_t)m * ns;
+    u64 lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < MAXS; i++)
+      if (i < ns) mac_lazy(lo, hi, y[i], h[i], mc.q);
+    u64 res = redc(lo, hi, mc.q, mc.qinv);
+    res = sub_mod(res, tab.vS[(size_t)m * (ns + 1) + v], mc.q);
+    outb[(size_t)rl.row[r] * N + x] = res;
+  }
+}
+void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable& tab, u64* out, size_t out_bstride, int batch,
+                  const RowList& rl, const ModC* mods, int N, bool force_v0, hipStream_t st) {
+  if (rl.n <= 0 || batch <= 0) return;
+  BConvTable t = tab;
+  t.rows_per_block = 8;
+  int ny = (rl.n + t.rows_per_block - 1) / t.rows_per_block;
+  dim3 grid(N / 256, ny, batch);
+  if (ns <= 8)
+    hipLaunchKernelGGL((bconv_kernel<8>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, force_v0 ? 1 : 0);
+  else if (ns <= 16)
+    hipLaunchKernelGGL((bconv_kernel<16>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, force_v0 ? 1 : 0);
+  else
+    hipLaunchKernelGGL((bconv_kernel<HCK_MAXSRC>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, force_v0 ? 1 : 0);
+}
+
+// ModDown combine: out = (x - ext) * P^-1 (+ add) [gathered through perm]
+// x rows = Q rows of a QP poly (stride x_bstride), ext rows = Q rows.
+__global__ void moddown_combine_kernel(u64* __restrict__ out, size_t o_bstride, const u64* __restrict__ x, size_t x_bstride,
+                                       const u64* __restrict__ ext, size_t e_bstride, const u64* __restrict__ add, size_t a_bstride,
+                                       int add_batches, const uint32_t* __restrict__ perm, const u64* __restrict__ pinv,
+                                       const u64* __restrict__ pinvp, const ModC* __restrict__ mods, int N) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  int r = blockIdx.y, b = blockIdx.z;
+  int src = perm ? (int)perm[i] : i;
+  u64 q = mods[r].q;
+  u64 v = sub_mod(x[(size_t)b * x_bstride + (size_t)r * N + src], ext[(size_t)b * e_bstride + (size_t)r * N + src], q);
+  v = shoup_mul(v, pinv[r], pinvp[r], q);
+  if (add && b < add_batches) v = add_mod(v, add[(size_t)b * a_bstride + (size_t)r * N + src], q);
+  out[(size_t)b * o_bstride + (size_t)r * N + i] = v;
+}
+void launch_moddown_combine(u64* out, size_t o_bstride, const u64* x, size_t x_bstride, const u64* ext, size_t e_bstride,
+                            const u64* add, size_t a_bstride, int add_batches, const uint32_t* perm, const u64* pinv,
+                            const u64* pinvp, int qrows, int batch, const ModC* mods, int N, hipStream_t st) {
+  if (qrows <= 0 || batch <= 0) return;
+  hipLaunchKernelGGL(moddown_combine_kernel, dim3(N / 256, qrows, batch), dim3(256), 0, st, out, o_bstride, x, x_bstride, ext,
+                     e_bstride, add, a_bstride, add_batches, perm, pinv, pinvp, mods, N);
+}
+
+// ---------------------------------------------------------------------------
+// Key inner product (gadget product) in QP, fused with the automorphism
+// gather.  For output position i the thread reads every operand at
+// src = perm[i]; inside an aligned block of 2^k outputs the sources form an
+// aligned block of 2^k words, so the gathers stay coalesced.
+//   mode 0: out = (sum_d dg_d*k0_d, sum_d dg_d*k1_d)                 (no perm)
+//   mode 1: out = perm(sum dg*k0 + add0[Q rows], sum dg*k1)         (hoisted)
+// Keys are in Montgomery form; the sum is accumulated lazily in 128 bits.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void keymac_kernel(KeyMacArgs a) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  int k = blockIdx.y, b = blockIdx.z;
+  const int N = a.N;
+  const uint32_t* perm = a.perm ? a.perm[b] : nullptr;
+  const u64* key = a.key[b];
+  int src = perm ? (int)perm[i] : i;
+  int kl = k <= a.l ? k : a.L + (k - a.l - 1);
+  ModC mc = a.mods[kl];
+  const u64* dg = a.digits + (size_t)(a.digits_per_batch ? b : 0) * a.dig_bstride;
+  u64 lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+  const size_t kstride = (size_t)(a.L + a.K) * N;
+  for (int d = 0; d < a.dn; d++) {
+    u64 x = dg[((size_t)d * a.nqp + k) * N + src];
+    const u64* kb = key + (size_t)d * 2 * kstride + (size_t)kl * N + src;
+    mac_lazy(lo0, hi0, x, kb[0], mc.q);
+    mac_lazy(lo1, hi1, x, kb[kstride], mc.q);
+  }
+  // add0 enters the high word (v*2^64 == v*R mod q), so the REDC below returns sum + add0
+  if (a.add0 && k <= a.l) hi0 = add_mod(hi0, a.add0[(size_t)k * N + src], mc.q);
+  u64 r0 = redc(lo0, hi0, mc.q, mc.qinv), r1 = redc(lo1, hi1, mc.q, mc.qinv);
+  size_t o = (size_t)b * a.out_bstride + (size_t)k * N + i;
+  a.out0[o] = r0;
+  a.out1[o] = r1;
+}
+void launch_keymac(const KeyMacArgs& a, int batch, hipStream_t st) {
+  if (batch <= 0) return;
+  hipLaunchKernelGGL(keymac_kernel, dim3(a.N / 256, a.nqp, batch), dim3(256), 0, st, a);
+}
+
+// Giant-step accumulation of the BSGS linear transform: for every QP row and
+// output position i, sum over giant groups g of
+//   [ sum_d dg_{g,d} * key_g[d] + T0_g ](perm_g[i])   (part 0)
+//   [ sum_d dg_{g,d} * key_g[d] ](perm_g[i])           (part 1)
+// plus the untransformed group (rotation 0) if present.  Everything folds
+// into one lazy 128-bit accumulator per part: T0 is added to the high word
+// (value*2^64 == value*R), so a single REDC finishes the row.
+__global__ __launch_bounds__(256) void giant_acc_kernel(GiantAccArgs a) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  int k = blockIdx.y;
+  const int N = a.N;
+  int kl = k <= a.l ? k : a.L + (k - a.l - 1);
+  ModC mc = a.mods[kl];
+  u64 lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+  const size_t kstride = (size_t)(a.L + a.K) * N;
+  for (int g = 0; g < a.ng; g++) {
+    const uint32_t* perm = a.perm[g];
+    const u64* key = a.key[g];
+    int src = (int)perm[i];
+    const u64* dg = a.digits + (size_t)g * a.dig_bstride;
+    for (int d = 0; d < a.dn; d++) {
+      u64 x = dg[((size_t)d * a.nqp + k) * N + src];
+      const u64* kb = key + (size_t)d * 2 * kstride + (size_t)kl * N + src;
+      mac_lazy(lo0, hi0, x, kb[0], mc.q);
+      mac_lazy(lo1, hi1, x, kb[kstride], mc.q);
+    }
+    const u64* T0 = a.T + (size_t)a.tg[g] * a.T_gstride;
+    hi0 = add_mod(hi0, T0[(size_t)k * N + src], mc.q);
+  }
+  if (a.t_zero >= 0) {
+    const u64* T0 = a.T + (size_t)a.t_zero * a.T_gstride;
+    hi0 = add_mod(hi0, T0[(size_t)k * N + i], mc.q);
+    hi1 = add_mod(hi1, T0[a.T_pstride + (size_t)k * N + i], mc.q);
+  }
+  size_t o = (size_t)k * N + i;
+  a.out0[o] = redc(lo0, hi0, mc.q, mc.qinv);
+  a.out1[o] = redc(lo1, hi1, mc.q, mc.qinv);
+}
+void launch_giant_acc(const GiantAccArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(giant_acc_kernel, dim3(a.N / 256, a.nqp, 1), dim3(256), 0, st, a);
+}
+
+// ---------------------------------------------------------------------------
+// Fused diagonal MAC of the BSGS linear transform.  One thread per (QP row,
+// coefficient) holds the baby-step operands of its word in registers and
+// streams every plaintext diagonal once, writing one accumulator pair per
+// giant group:
+//   T[g][p][k][x] = sum_{b in baby(g)} diag_{g,b}[k][x] * S_b[p][k][x]
+// S_0 = P*c (Q rows only), S_b = hoisted rotation b (QP).  Diagonals are in
+// Montgomery form; the per-group sum is accumulated lazily in 128 bits.
+// ---------------------------------------------------------------------------
+template <int NB>
+__global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
+  const int k = blockIdx.y;
+  const int N = a.N;
+  const int kl = k <= a.l ? k : a.L + (k - a.l - 1);
+  const ModC mc = a.mods[kl];
+  const int krow = k <= a.l ? k : a.lt_level + 1 + (k - a.l - 1);  // row inside a diagonal
+  const size_t prow = (size_t)krow * N + x;
+  u64 s0[NB], s1[NB];
+#pragma unroll
+  for (int b = 0; b < NB; b++) {
+    int bb = a.b0 + b;
+    s0[b] = 0; s1[b] = 0;
+    if (bb < a.nbaby) {
+      if (a.baby_is_zero[bb]) {
+        if (k <= a.l) { s0[b] = a.pc[(size_t)k * N + x]; s1[b] = a.pc[a.pc_pstride + (size_t)k * N + x]; }
+      } else {
+        const u64* r = a.R + (size_t)a.baby_slot[bb] * a.R_bstride;
+        s0[b] = r[(size_t)k * N + x];
+        s1[b] = r[a.R_pstride + (size_t)k * N + x];
+      }
+    }
+  }
+  for (int g = 0; g < a.ng; g++) {
+    const uint64_t mask = a.gmask[g] >> a.b0;
+    int pidx = a.gpidx[g] + (a.b0 ? __popcll(a.gmask[g] & ((1ULL << a.b0) - 1)) : 0);
+    u64 lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      if ((mask >> b) & 1) {
+        const u64 d = a.diag[(size_t)pidx * a.diag_stride + prow];
+        pidx++;
+        mac_lazy(lo0, hi0, d, s0[b], mc.q);
+        mac_lazy(lo1, hi1, d, s1[b], mc.q);
+      }
+    }
+    u64* T = a.T + (size_t)g * a.T_gstride + (size_t)k * N + x;
+    u64 r0 = redc(lo0, hi0, mc.q, mc.qinv), r1 = redc(lo1, hi1, mc.q, mc.qinv);
+    if (a.b0 > 0) { r0 = add_mod(r0, T[0], mc.q); r1 = add_mod(r1, T[a.T_pstride], mc.q); }
+    T[0] = r0;
+    T[a.T_pstride] = r1;
+  }
+}
+void launch_diag_mac(const DiagMacArgs& a, hipStream_t st) {
+  dim3 grid(a.N / 256, a.nqp, 1);
+  if (a.nb_chunk <= 8) hipLaunchKernelGGL((diag_mac_kernel<8>), grid, dim3(256), 0, st, a);
+  else if (a.nb_chunk <= 16) hipLaunchKernelGGL((diag_mac_kernel<16>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((diag_mac_kernel<32>), grid, dim3(256), 0, st, a);
+}
+
+// ---------------------------------------------------------------------------
+// Rescale helpers (DivRoundByLastModulus): u = iNTT(x_l) per polynomial;
+// t_i = ((u + h) mod q_l - h) mod q_i for i < l; out_i = (x_i - NTT(t_i)) * q_l^-1
+// ---------------------------------------------------------------------------
+__global__ void rescale_spread_kernel(u64* __restrict__ t, const u64* __restrict__ u, int l, u64 half,
+                                      const ModC* __restrict__ mods, int N) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  int i = blockIdx.y, p = blockIdx.z;
+  u64 ql = mods[l].q;
+  u64 w = add_mod(u[(size_t)p * N + x], half, ql);
+  ModC mc = mods[i];
+  u64 wr = mont_mul(w, mc.rmod, mc.q, mc.qinv);  // w mod q_i
+  u64 hr = mont_mul(half, mc.rmod, mc.q, mc.qinv);
+  t[((size_t)p * l + i) * N + x] = sub_mod(wr, hr, mc.q);
+}
+void launch_rescale_spread(u64* t, const u64* u, int l, u64 half, const ModC* mods, int N, hipStream_t st) {
+  hipLaunchKernelGGL(rescale_spread_kernel, dim3(N / 256, l, 2), dim3(256), 0, st, t, u, l, half, mods, N);
+}
+__global__ void rescale_combine_kernel(u64* __restrict__ out, const u64* __restrict__ x, const u64* __restrict__ t, int l,
+                                       const u64* __restrict__ inv, const u64* __restrict__ invp, const ModC* __restrict__ mods, int N) {
+  int j = blockIdx.x * blockDim.x + threadIdx.x;
+  int i = blockIdx.y, p = blockIdx.z;
+  u64 q = mods[i].q;
+  u64 v = sub_mod(x[((size_t)p * (l + 1) + i) * N + j], t[((size_t)p * l + i) * N + j], q);
+  out[((size_t)p * l + i) * N + j] = shoup_mul(v, inv[i], invp[i], q);
+}
+void launch_rescale_combine(u64* out, const u64* x, const u64* t, int l, const u64* inv, const u64* invp, const ModC* mods, int N, hipStream_t st) {
+  hipLaunchKernelGGL(rescale_combine_kernel, dim3(N / 256, l, 2), dim3(256), 0, st, out, x, t, l, inv, invp, mods, N);
+}
+
+// ---------------------------------------------------------------------------
+// Sampling (counter PRNG shared with the key/encryption specification):
+//   rand64(seed, stream, ctr) = mix(mix(seed + G*(stream+1)) ^ (ctr*M1 + M2))
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ u64 mix64(u64 z) {
+  z ^= z >> 30; z *= 0xbf58476d1ce4e5b9ULL;
+  z ^= z >> 27; z *= 0x94d049bb133111ebULL;
+  z ^= z >> 31; return z;
+}
+__device__ __forceinline__ u64 rand64(u64 seed, u64 stream, u64 ctr) {
+  u64 k = mix64(seed + 0x9e3779b97f4a7c15ULL * (stream + 1));
+  return mix64(k ^ (ctr * 0xd1b54a32d192ed03ULL + 0x8cb92ba72f3d8dd7ULL));
+}
+// uniform residues: row r (modulus m) coefficient x gets rand64(seed, stream, m*N + x) * q >> 64
+__global__ void sample_uniform_kernel(u64* __restrict__ out, RowMap rm, u64 seed, u64 stream, const ModC* __restrict__ mods, int N) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  int row = rm.row(blockIdx.y);
+  int m = rm.mod(row);
+  u64 r = rand64(seed, stream, (u64)m * N + x);
+  out[(size_t)row * N + x] = __umul64hi(r, mods[m].q);
+}
+void launch_sample_uniform(u64* out, RowMap rm, u64 seed, u64 stream, const ModC* mods, int N, hipStream_t st) {
+  hipLaunchKernelGGL(sample_uniform_kernel, dim3(N / 256, rm.nact(), 1), dim3(256), 0, st, out, rm, seed, stream, mods, N);
+}
+// centred binomial (eta = 21) error, the same integer reduced into every row; optionally added
+__global__ void sample_cbd_kernel(u64* __restrict__ out, RowMap rm, u64 seed, u64 stream, const ModC* __restrict__ mods, int N, int add) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  int row = rm.row(blockIdx.y);
+  u64 q = mods[rm.mod(row)].q;
+  u64 r = rand64(seed, stream, (u64)x);
+  int e = __popcll(r & 0x1FFFFFULL) - __popcll((r >> 21) & 0x1FFFFFULL);
+  u64 v = e >= 0 ? (u64)e : q - (u64)(-e);
+  size_t o = (size_t)row * N + x;
+  out[o] = add ? add_mod(out[o], v, q) : v;
+}
+void launch_sample_cbd(u64* out, RowMap rm, u64 seed, u64 stream, const ModC* mods, int N, bool add, hipStream_t st) {
+  hipLaunchKernelGGL(sample_cbd_kernel, dim3(N / 256, rm.nact(), 1), dim3(256), 0, st, out, rm, seed, stream, mods, N, add ? 1 : 0);
+}
+// small signed integers (int8, e.g. ternary) reduced into every row
+__global__ void signed_rows_kernel(u64* __restrict__ out, RowMap rm, const int8_t* __restrict__ v, const ModC* __restrict__ mods, int N) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  int row = rm.row(blockIdx.y);
+  u64 q = mods[rm.mod(row)].q;
+  int e = v[x];
+  out[(size_t)row * N + x] = e >= 0 ? (u64)e : q - (u64)(-e);
+}
+void launch_signed_rows(u64* out, RowMap rm, const int8_t* v, const ModC* mods, int N, hipStream_t st) {
+  hipLaunchKernelGGL(signed_rows_kernel, dim3(N / 256, rm.nact(), 1), dim3(256), 0, st, out, rm, v, mods, N);
+}
+// Galois-key body: b = -a*s' + e (+ P*s on own rows), in place on b; a, s', s in
+// (a standard, sR/soR Montgomery), own rows [own0, own1) of the Q chain.
+__global__ void gk_combine_kernel(u64* __restrict__ b, const u64* __restrict__ a, const u64* __restrict__ soR,
+                                  const u64* __restrict__ sR, int own0, int own1, const u64* __restrict__ pmod,
+                                  const ModC* __restrict__ mods, int N) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  int m = blockIdx.y;
+  ModC mc = mods[m];
+  size_t o = (size_t)m * N + x;
+  u64 v = sub_mod(b[o], mont_mul(a[o], soR[o], mc.q, mc.qinv), mc.q);
+  if (m >= own0 && m < own1) v = add_mod(v, mont_mul(pmod[m], sR[o], mc.q, mc.qinv), mc.q);
+  b[o] = v;
+}
+void launch_gk_combine(u64* b, const u64* a, const u64* soR, const u64* sR, int own0, int own1, const u64* pmod, int rows,
+                       const ModC* mods, int N, hipStream_t st) {
+  hipLaunchKernelGGL(gk_combine_kernel, dim3(N / 256, rows, 1), dim3(256), 0, st, b, a, soR, sR, own0, own1, pmod, mods, N);
+}
+
+// Encoder: fixed-point coefficients -> residues.  rec[x] = {mag, exp|flags}
+// where a big value is mag * 2^exp; negative values are negated mod q.
+__global__ void encode_residues_kernel(u64* __restrict__ out, RowMap rm, const u64* __restrict__ rec, const ModC* __restrict__ mods, int N) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  int row = rm.row(blockIdx.y);
+  ModC mc = mods[rm.mod(row)];
+  u64 mag = rec[2 * x], meta = rec[2 * x + 1];
+  int neg = (int)(meta & 1), exp = (int)(meta >> 8);
+  u64 r = mont_mul(mag, mc.rmod, mc.q, mc.qinv);  // mag mod q
+  for (int e = 0; e < exp; e++) r = add_mod(r, r, mc.q);
+  if (neg && r) r = mc.q - r;
+  out[(size_t)row * N + x] = r;
+}
+void launch_encode_residues(u64* out, RowMap rm, const u64* rec, const ModC* mods, int N, hipStream_t st) {
+  hipLaunchKernelGGL(encode_residues_kernel, dim3(N / 256, rm.nact(), 1), dim3(256), 0, st, out, rm, rec, mods, N);
+}

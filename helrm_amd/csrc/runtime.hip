@@ -1,0 +1,1450 @@
+// runtime.hip -- host runtime and C ABI of the MI355X CKKS backend.
+//
+// One global scheme per process (as the Lattigo wrapper's `scheme`,
+// orion/backend/lattigo/scheme.go:32), one HIP stream, ID-handle registries
+// with lowest-free-id reuse (orion/backend/lattigo/minheap.go:27-98).  All
+// polynomial arithmetic runs on the GPU through kernels.hip; the host does
+// only parameter set-up, the encoder's float64 FFT, the decoder's CRT and
+// sampling of the small ternary vectors.  Every entry point returns -1 (or an
+// empty array) and records a message for GetLastError() instead of aborting.
+#include <hip/hip_runtime.h>
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <queue>
+#include <set>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <unordered_map>
+#include <vector>
+
+#include "hipckks.h"
+#include "kernels.h"
+#include "../../include/helrm_hip.h"
+
+namespace {
+
+// ============================================================================
+// errors
+// ============================================================================
+thread_local std::string g_err;
+struct Error : std::runtime_error { using std::runtime_error::runtime_error; };
+#define HCHECK(x)                                                                                   \
+  do {                                                                                              \
+    hipError_t e_ = (x);                                                                            \
+    if (e_ != hipSuccess) throw Error(std::string("HIP error: ") + hipGetErrorString(e_) + " at " + #x); \
+  } while (0)
+#define REQUIRE(c, msg) do { if (!(c)) throw Error(msg); } while (0)
+
+template <class F> int guard(F&& f) {
+  try { return f(); } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+// ============================================================================
+// host number theory
+// ============================================================================
+u64 mulmod(u64 a, u64 b, u64 m) { return (u64)((u128)a * b % m); }
+u64 powmod(u64 a, u64 e, u64 m) { u64 r = 1 % m; a %= m; while (e) { if (e & 1) r = mulmod(r, a, m); a = mulmod(a, a, m); e >>= 1; } return r; }
+u64 invmod(u64 a, u64 p) { return powmod(a % p, p - 2, p); }
+u64 invmod_odd(u64 a, u64 m) {  // gcd(a, m) = 1, m a power of two or odd
+  i64 t = 0, nt = 1; u64 r = m, nr = a % m;
+  while (nr) { u64 q = r / nr; i64 tt = t - (i64)q * nt; t = nt; nt = tt; u64 rr = r - q * nr; r = nr; nr = rr; }
+  if (t < 0) t += (i64)m;
+  return (u64)t;
+}
+u64 shoup(u64 w, u64 q) { return (u64)(((u128)w << 64) / q); }
+bool is_prime(u64 n) {
+  static const u64 B[] = {2, 3, 5, 7, 11, 13, 17, 19, 23, 29, 31, 37};
+  if (n < 2) return false;
+  for (u64 b : B) { if (n == b) return true; if (n % b == 0) return false; }
+  u64 d = n - 1; int s = 0;
+  while (!(d & 1)) { d >>= 1; s++; }
+  for (u64 b : B) {
+    u64 x = powmod(b, d, n);
+    if (x == 1 || x == n - 1) continue;
+    bool comp = true;
+    for (int r = 1; r < s; r++) { x = mulmod(x, x, n); if (x == n - 1) { comp = false; break; } }
+    if (comp) return false;
+  }
+  return true;
+}
+u64 gcd(u64 a, u64 b) { while (b) { u64 t = a % b; a = b; b = t; } return a; }
+u64 pollard(u64 n) {
+  if (n % 2 == 0) return 2;
+  for (u64 c = 1;; c++) {
+    u64 x = 2, y = 2, d = 1;
+    auto f = [&](u64 v) { return (mulmod(v, v, n) + c) % n; };
+    while (d == 1) { x = f(x); y = f(f(y)); d = gcd(x > y ? x - y : y - x, n); }
+    if (d != n) return d;
+  }
+}
+void factor(u64 n, std::vector<u64>& f) {
+  if (n == 1) return;
+  if (is_prime(n)) { if (std::find(f.begin(), f.end(), n) == f.end()) f.push_back(n); return; }
+  for (u64 p = 2; p < 1000; p++)
+    if (n % p == 0) { factor(p, f); while (n % p == 0) n /= p; factor(n, f); return; }
+  u64 d = pollard(n);
+  factor(d, f); factor(n / d, f);
+}
+u64 smallest_generator(u64 q) {
+  std::vector<u64> f; factor(q - 1, f);
+  for (u64 g = 2;; g++) {
+    bool ok = true;
+    for (u64 p : f) if (powmod(g, (q - 1) / p, q) == 1) { ok = false; break; }
+    if (ok) return g;
+  }
+}
+// NTT-friendly chain (rlwe.GenModuli): per bit size, candidates 2^b + 1 +- k*2N,
+// 61-bit downstream only, others alternating starting upstream; Q first, then P.
+void gen_primes(int logN, const std::vector<int>& lq, const std::vector<int>& lp, std::vector<u64>& q, std::vector<u64>& p) {
+  struct G { u64 up, down; bool next_up; };
+  std::map<int, G> gens;
+  u64 nth = (u64)2 << logN;
+  auto next = [&](int b) {
+    REQUIRE(b >= 10 && b <= 61, "prime bit sizes must be in [10, 61]");
+    auto it = gens.find(b);
+    if (it == gens.end()) it = gens.emplace(b, G{((u64)1 << b) + 1, ((u64)1 << b) + 1, true}).first;
+    G& g = it->second;
+    bool up = b == 61 ? false : g.next_up;
+    if (b != 61) g.next_up = !g.next_up;
+    for (;;) {
+      u64 c;
+      if (up) { g.up += nth; c = g.up; } else { g.down -= nth; c = g.down; }
+      if (is_prime(c)) return c;
+    }
+  };
+  q.clear(); p.clear();
+  for (int b : lq) q.push_back(next(b));
+  for (int b : lp) p.push_back(next(b));
+}
+int brv(int x, int logn) { int r = 0; for (int i = 0; i < logn; i++) { r = (r << 1) | (x & 1); x >>= 1; } return r; }
+
+// ============================================================================
+// counter PRNG (same specification as the device one in kernels.hip)
+// ============================================================================
+inline u64 mix64(u64 z) {
+  z ^= z >> 30; z *= 0xbf58476d1ce4e5b9ULL;
+  z ^= z >> 27; z *= 0x94d049bb133111ebULL;
+  z ^= z >> 31; return z;
+}
+inline u64 rand64(u64 seed, u64 stream, u64 ctr) {
+  u64 k = mix64(seed + 0x9e3779b97f4a7c15ULL * (stream + 1));
+  return mix64(k ^ (ctr * 0xd1b54a32d192ed03ULL + 0x8cb92ba72f3d8dd7ULL));
+}
+constexpr u64 ST_SK = 1, ST_PK_A = 2, ST_PK_E = 3;
+inline u64 ST_GK_A(u64 g, u64 d) { return (4ULL << 56) | (g << 8) | d; }
+inline u64 ST_GK_E(u64 g, u64 d) { return (5ULL << 56) | (g << 8) | d; }
+inline u64 ST_ENC_U(u64 e) { return (6ULL << 56) | e; }
+inline u64 ST_ENC_E0(u64 e) { return (7ULL << 56) | e; }
+inline u64 ST_ENC_E1(u64 e) { return (8ULL << 56) | e; }
+// ternary vector with exactly h entries +-1 (partial Fisher-Yates)
+std::vector<int8_t> ternary_hw(u64 seed, u64 stream, int N, int h) {
+  std::vector<int> idx(N);
+  for (int i = 0; i < N; i++) idx[i] = i;
+  std::vector<int8_t> out(N, 0);
+  if (h > N) h = N;
+  for (int k = 0; k < h; k++) {
+    u64 r = rand64(seed, stream, (u64)k);
+    int j = k + (int)(((u128)r * (u64)(N - k)) >> 64);
+    std::swap(idx[k], idx[j]);
+    out[idx[k]] = (rand64(seed, stream, (1ULL << 32) + (u64)k) & 1) ? -1 : 1;
+  }
+  return out;
+}
+
+// ============================================================================
+// device memory: size-bucketed cache (no hipFree on the hot path)
+// ============================================================================
+struct Pool {
+  std::multimap<size_t, void*> free_;
+  std::unordered_map<void*, size_t> size_;
+  size_t live = 0, cached = 0, peak = 0;
+  void* get(size_t bytes) {
+    bytes = (bytes + 255) & ~(size_t)255;
+    if (bytes == 0) bytes = 256;
+    auto it = free_.find(bytes);
+    if (it != free_.end()) { void* p = it->second; free_.erase(it); cached -= bytes; live += bytes; peak = std::max(peak, live); return p; }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) { (void)hipGetLastError(); trim(); HCHECK(hipMalloc(&p, bytes)); }
+    size_[p] = bytes; live += bytes; peak = std::max(peak, live);
+    return p;
+  }
+  void put(void* p) {
+    if (!p) return;
+    size_t b = size_.at(p);
+    free_.emplace(b, p); live -= b; cached += b;
+  }
+  void trim() {
+    (void)hipDeviceSynchronize();
+    for (auto& kv : free_) { (void)hipFree(kv.second); size_.erase(kv.second); }
+    free_.clear(); cached = 0;
+  }
+  void release_all() {
+    (void)hipDeviceSynchronize();
+    for (auto& kv : size_) (void)hipFree(kv.first);
+    free_.clear(); size_.clear(); live = cached = 0;
+  }
+};
+Pool* g_pool = nullptr;
+
+template <class T> struct DevArray {
+  T* p = nullptr; size_t n = 0;
+  DevArray() = default;
+  explicit DevArray(size_t count) : n(count) { if (count) p = (T*)g_pool->get(count * sizeof(T)); }
+  DevArray(const DevArray&) = delete;
+  DevArray& operator=(const DevArray&) = delete;
+  DevArray(DevArray&& o) noexcept : p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
+  DevArray& operator=(DevArray&& o) noexcept { if (this != &o) { reset(); p = o.p; n = o.n; o.p = nullptr; o.n = 0; } return *this; }
+  ~DevArray() { reset(); }
+  void reset() { if (p && g_pool) g_pool->put(p); p = nullptr; n = 0; }
+  size_t bytes() const { return n * sizeof(T); }
+};
+using DU64 = DevArray<u64>;
+
+// ============================================================================
+// scheme objects
+// ============================================================================
+struct IdHeap {  // lowest free id first
+  int next = 0;
+  std::priority_queue<int, std::vector<int>, std::greater<int>> freed;
+  int take() { if (!freed.empty()) { int v = freed.top(); freed.pop(); return v; } return next++; }
+  void give(int v) { freed.push(v); }
+};
+struct Plain { int level; double scale; int logslots; DU64 d; };      // [level+1][N]
+struct Cipher { int level; double scale; int logslots; DU64 d; };     // [2][level+1][N]
+struct LinTrans {
+  int level = 0, N1 = 0, slots = 0;
+  bool naive = false;
+  std::vector<int> keys;                 // diagonal indices as given
+  std::vector<int> rot1, rot2;           // sorted giant / baby rotations
+  std::vector<int> giant;                // giant rotation per group
+  std::vector<std::vector<int>> baby;    // sorted babies per group
+  std::vector<int> plain_idx;            // diagonal index of each stored plaintext
+  DU64 diags;                            // [np][level+1+K][N], Montgomery form
+  DevArray<uint64_t> d_gmask; DevArray<int> d_gpidx, d_bzero, d_bslot;
+  double scale = 0;
+};
+
+struct BConvHost { int ns; BConvTable tab; DU64 hat, vS; };
+
+struct Timing { bool on = false; std::map<std::string, std::vector<std::pair<hipEvent_t, hipEvent_t>>> ev; std::map<std::string, std::pair<long, double>> acc; };
+
+struct Scheme {
+  int logN = 0, N = 0, L = 0, K = 0, dnum = 0, logscale = 0, h = 0;
+  u64 seed = 0;
+  std::vector<u64> mod;
+  hipStream_t st = nullptr;
+  DevArray<ModC> d_mods;
+  DU64 w, wp, iw, iwp, ninv, ninvp;
+  NttTables tw{};
+  std::vector<ModC> hmods;
+  // per-modulus constants (Shoup pairs indexed by modulus)
+  DU64 pmod_w, pmod_wp, pinv_w, pinv_wp, p0inv_w, p0inv_wp, pmod_plain;
+  DU64 rs_inv, rs_invp;  // [l][i] q_l^-1 mod q_i
+  std::map<std::pair<int, int>, std::unique_ptr<BConvHost>> bconv;
+  std::map<u64, DevArray<uint32_t>> perms;
+  // keys
+  bool has_sk = false, has_pk = false;
+  std::vector<int8_t> s;
+  DU64 sR, pkR;
+  std::map<u64, std::unique_ptr<DU64>> gkeys;
+  std::set<u64> rot_keys, lt_keys;
+  u64 enc_counter = 0;
+  // registries
+  IdHeap pt_ids, ct_ids, lt_ids;
+  std::map<int, std::unique_ptr<Plain>> pts;
+  std::map<int, std::unique_ptr<Cipher>> cts;
+  std::map<int, std::unique_ptr<LinTrans>> lts;
+  // encoder
+  std::vector<double> rre, rim;
+  std::vector<int> rotgroup;
+  Timing timing;
+  bool encoder = false, encryptor = false, decryptor = false, evaluator = false, lteval = false;
+};
+Scheme* S = nullptr;
+u64 g_seed_override = 0;
+bool g_seed_set = false;
+
+Scheme& sch() { REQUIRE(S, "no scheme: call NewScheme first"); return *S; }
+void sync() { HCHECK(hipStreamSynchronize(sch().st)); }
+template <class T> void upload(T* d, const T* h, size_t n) { HCHECK(hipMemcpyAsync(d, h, n * sizeof(T), hipMemcpyHostToDevice, sch().st)); HCHECK(hipStreamSynchronize(sch().st)); }
+template <class T> void download(T* h, const T* d, size_t n) { HCHECK(hipMemcpyAsync(h, d, n * sizeof(T), hipMemcpyDeviceToHost, sch().st)); HCHECK(hipStreamSynchronize(sch().st)); }
+void d2d(void* dst, const void* src, size_t bytes) { if (bytes) HCHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, sch().st)); }
+void d2d_2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width, size_t height) {
+  if (height == 1) { d2d(dst, src, width); return; }
+  if (width && height) HCHECK(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height, hipMemcpyDeviceToDevice, sch().st));
+}
+
+RowMap rows_q(int l) { return RowMap{l + 1, l + 1, 0, 0, 0, 0}; }
+RowMap rows_qp(int l) { Scheme& s = sch(); return RowMap{l + 1 + s.K, l + 1, 0, s.L, 0, 0}; }
+RowMap rows_p() { Scheme& s = sch(); return RowMap{s.K, 0, 0, s.L, 0, 0}; }
+RowMap rows_all() { Scheme& s = sch(); return RowMap{s.L + s.K, s.L + s.K, 0, 0, 0, 0}; }
+inline int qp_mod(int l, int k) { Scheme& s = sch(); return k <= l ? k : s.L + (k - l - 1); }
+
+void ntt(u64* d, size_t bstride, int batch, RowMap rm, bool fwd) { Scheme& s = sch(); launch_ntt(d, bstride, batch, rm, s.logN, fwd, s.tw, s.st); }
+
+// timing of named launches (HIP events on the scheme stream)
+template <class F> void timed(const char* name, F&& f) {
+  Scheme& s = sch();
+  if (!s.timing.on) { f(); return; }
+  hipEvent_t a, b;
+  HCHECK(hipEventCreate(&a)); HCHECK(hipEventCreate(&b));
+  HCHECK(hipEventRecord(a, s.st));
+  f();
+  HCHECK(hipEventRecord(b, s.st));
+  s.timing.ev[name].push_back({a, b});
+}
+void timing_collect() {
+  Scheme& s = sch();
+  for (auto& kv : s.timing.ev) {
+    for (auto& pr : kv.second) {
+      HCHECK(hipEventSynchronize(pr.second));
+      float ms = 0; HCHECK(hipEventElapsedTime(&ms, pr.first, pr.second));
+      auto& a = s.timing.acc[kv.first]; a.first++; a.second += ms;
+      (void)hipEventDestroy(pr.first); (void)hipEventDestroy(pr.second);
+    }
+  }
+  s.timing.ev.clear();
+}
+
+// ============================================================================
+// basis-conversion tables: src = moduli [s0, s1) (indices), all moduli as targets
+// ============================================================================
+BConvHost& bconv_table(int s0, int s1) {
+  Scheme& s = sch();
+  auto key = std::make_pair(s0, s1);
+  auto it = s.bconv.find(key);
+  if (it != s.bconv.end()) return *it->second;
+  int ns = s1 - s0, nm = s.L + s.K;
+  REQUIRE(ns >= 1 && ns <= HCK_MAXSRC, "basis conversion source too large");
+  auto b = std::make_unique<BConvHost>();
+  b->ns = ns;
+  std::vector<u64> hat((size_t)nm * ns), vS((size_t)nm * (ns + 1));
+  for (int i = 0; i < ns; i++) {
+    u64 si = s.mod[s0 + i], pr = 1;
+    for (int j = 0; j < ns; j++) if (j != i) pr = mulmod(pr, s.mod[s0 + j] % si, si);
+    u64 hi = invmod(pr, si);
+    b->tab.src[i] = BConvSrc{si, hi, shoup(hi, si), (double)si};
+  }
+  for (int m = 0; m < nm; m++) {
+    u64 t = s.mod[m], R = s.hmods[m].rmod, Sm = 1;
+    for (int j = 0; j < ns; j++) Sm = mulmod(Sm, s.mod[s0 + j] % t, t);
+    for (int v = 0; v <= ns; v++) vS[(size_t)m * (ns + 1) + v] = mulmod((u64)v, Sm, t);
+    for (int i = 0; i < ns; i++) {
+      u64 pr = 1;
+      for (int j = 0; j < ns; j++) if (j != i) pr = mulmod(pr, s.mod[s0 + j] % t, t);
+      hat[(size_t)m * ns + i] = mulmod(pr, R, t);
+    }
+  }
+  b->hat = DU64(hat.size()); upload(b->hat.p, hat.data(), hat.size());
+  b->vS = DU64(vS.size()); upload(b->vS.p, vS.data(), vS.size());
+  b->tab.hat = b->hat.p; b->tab.vS = b->vS.p; b->tab.rows_per_block = 8;
+  auto& ref = *b;
+  s.bconv[key] = std::move(b);
+  return ref;
+}
+
+const uint32_t* perm_for(u64 galel) {
+  Scheme& s = sch();
+  auto it = s.perms.find(galel);
+  if (it != s.perms.end()) return it->second.p;
+  std::vector<uint32_t> idx(s.N);
+  u64 mask = 2 * (u64)s.N - 1;
+  for (int i = 0; i < s.N; i++) {
+    u64 e = 2 * (u64)brv(i, s.logN) + 1;
+    u64 t = ((galel * e) & mask) - 1;
+    idx[i] = (uint32_t)brv((int)(t >> 1), s.logN);
+  }
+  DevArray<uint32_t> d(s.N); upload(d.p, idx.data(), idx.size());
+  const uint32_t* p = d.p;
+  s.perms[galel] = std::move(d);
+  return p;
+}
+u64 galois_element(int k) { Scheme& s = sch(); u64 M = 2 * (u64)s.N; return powmod(5, (u64)(i64)k & (M - 1), M); }
+
+// ============================================================================
+// key switching building blocks
+// ============================================================================
+// digits[b][d][nqp][N] from c1 (NTT, Q rows 0..l) of batch b (stride c1_bstride)
+void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* digits) {
+  Scheme& s = sch();
+  const int N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
+  const size_t dstride = (size_t)dn * nqp * N;
+  DU64 coef((size_t)batch * (l + 1) * N);
+  d2d_2d(coef.p, (size_t)(l + 1) * N * 8, c1, c1_bstride * 8, (size_t)(l + 1) * N * 8, batch);
+  ntt(coef.p, (size_t)(l + 1) * N, batch, rows_q(l), false);
+  for (int d = 0; d < dn; d++) {
+    int st0 = d * K, en = std::min(st0 + K, l + 1), ns = en - st0;
+    BConvHost& bt = bconv_table(st0, en);
+    RowList rl{}; rl.n = 0;
+    for (int k = 0; k < nqp; k++) if (k < st0 || k >= en) { rl.row[rl.n] = (short)k; rl.mod[rl.n] = (short)qp_mod(l, k); rl.n++; }
+    u64* D = digits + (size_t)d * nqp * N;
+    launch_bconv(coef.p + (size_t)st0 * N, (size_t)(l + 1) * N, ns, bt.tab, D, dstride, batch, rl, s.d_mods.p, N, ns == 1, s.st);
+    d2d_2d(D + (size_t)st0 * N, dstride * 8, c1 + (size_t)st0 * N, c1_bstride * 8, (size_t)ns * N * 8, batch);
+    RowMap rm{nqp, l + 1, 0, s.L, st0, en};
+    ntt(D, dstride, batch, rm, true);
+  }
+}
+// out[b] (Q rows, stride o_bstride) = ModDown(x[b]) (QP rows, stride x_bstride) [+ add[b<add_batches]] [gathered by perm]
+void mod_down(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t o_bstride, const u64* add = nullptr,
+              size_t a_bstride = 0, int add_batches = 0, const uint32_t* perm = nullptr) {
+  Scheme& s = sch();
+  const int N = s.N, K = s.K;
+  DU64 pc((size_t)batch * K * N), ext((size_t)batch * (l + 1) * N);
+  d2d_2d(pc.p, (size_t)K * N * 8, x + (size_t)(l + 1) * N, x_bstride * 8, (size_t)K * N * 8, batch);
+  ntt(pc.p, (size_t)K * N, batch, rows_p(), false);
+  BConvHost& bt = bconv_table(s.L, s.L + K);
+  RowList rl{}; rl.n = l + 1;
+  for (int i = 0; i <= l; i++) { rl.row[i] = (short)i; rl.mod[i] = (short)i; }
+  launch_bconv(pc.p, (size_t)K * N, K, bt.tab, ext.p, (size_t)(l + 1) * N, batch, rl, s.d_mods.p, N, false, s.st);
+  ntt(ext.p, (size_t)(l + 1) * N, batch, rows_q(l), true);
+  launch_moddown_combine(out, o_bstride, x, x_bstride, ext.p, (size_t)(l + 1) * N, add, a_bstride, add_batches, perm,
+                         s.pinv_w.p, s.pinv_wp.p, l + 1, batch, s.d_mods.p, N, s.st);
+}
+
+const u64* key_ptr(u64 galel, bool for_lt) {
+  Scheme& s = sch();
+  auto& set = for_lt ? s.lt_keys : s.rot_keys;
+  REQUIRE(set.count(galel), std::string("missing Galois key for element ") + std::to_string(galel));
+  return s.gkeys.at(galel)->p;
+}
+
+// ============================================================================
+// key generation (GPU), identical specification to the checker
+// ============================================================================
+void gen_secret() {
+  Scheme& s = sch();
+  const int N = s.N, nm = s.L + s.K;
+  s.s = ternary_hw(s.seed, ST_SK, N, s.h);
+  DevArray<int8_t> ds(N); upload(ds.p, s.s.data(), N);
+  s.sR = DU64((size_t)nm * N);
+  launch_signed_rows(s.sR.p, rows_all(), ds.p, s.d_mods.p, N, s.st);
+  ntt(s.sR.p, 0, 1, rows_all(), true);
+  launch_mont_convert(s.sR.p, 0, 1, rows_all(), s.d_mods.p, N, true, s.st);
+  sync();
+  s.has_sk = true;
+}
+void gen_public() {
+  Scheme& s = sch();
+  REQUIRE(s.has_sk, "secret key not generated");
+  const int N = s.N, nm = s.L + s.K;
+  DU64 b((size_t)nm * N), a((size_t)nm * N);
+  launch_sample_uniform(a.p, rows_all(), s.seed, ST_PK_A, s.d_mods.p, N, s.st);
+  ntt(a.p, 0, 1, rows_all(), true);
+  launch_sample_cbd(b.p, rows_all(), s.seed, ST_PK_E, s.d_mods.p, N, false, s.st);
+  ntt(b.p, 0, 1, rows_all(), true);
+  launch_gk_combine(b.p, a.p, s.sR.p, s.sR.p, 0, 0, s.pmod_plain.p, nm, s.d_mods.p, N, s.st);
+  s.pkR = DU64((size_t)2 * nm * N);
+  d2d(s.pkR.p, b.p, (size_t)nm * N * 8);
+  d2d(s.pkR.p + (size_t)nm * N, a.p, (size_t)nm * N * 8);
+  launch_mont_convert(s.pkR.p, (size_t)nm * N, 2, rows_all(), s.d_mods.p, N, true, s.st);
+  sync();
+  s.has_pk = true;
+}
+void ensure_galois_key(u64 galel) {
+  Scheme& s = sch();
+  if (s.gkeys.count(galel)) return;
+  REQUIRE(s.has_sk, "secret key not generated");
+  const int N = s.N, nm = s.L + s.K, K = s.K;
+  u64 M = 2 * (u64)N, ginv = invmod_odd(galel, M);
+  std::vector<int8_t> so(N, 0);
+  for (int i = 0; i < N; i++) { u64 t = ((u64)i * ginv) % M; if (t < (u64)N) so[t] = (int8_t)(so[t] + s.s[i]); else so[t - N] = (int8_t)(so[t - N] - s.s[i]); }
+  DevArray<int8_t> dso(N); upload(dso.p, so.data(), N);
+  DU64 soR((size_t)nm * N);
+  launch_signed_rows(soR.p, rows_all(), dso.p, s.d_mods.p, N, s.st);
+  ntt(soR.p, 0, 1, rows_all(), true);
+  launch_mont_convert(soR.p, 0, 1, rows_all(), s.d_mods.p, N, true, s.st);
+  auto key = std::make_unique<DU64>((size_t)s.dnum * 2 * nm * N);
+  for (int d = 0; d < s.dnum; d++) {
+    u64* b = key->p + (size_t)d * 2 * nm * N;
+    u64* a = b + (size_t)nm * N;
+    launch_sample_uniform(a, rows_all(), s.seed, ST_GK_A(galel, d), s.d_mods.p, N, s.st);
+    ntt(a, 0, 1, rows_all(), true);
+    launch_sample_cbd(b, rows_all(), s.seed, ST_GK_E(galel, d), s.d_mods.p, N, false, s.st);
+    ntt(b, 0, 1, rows_all(), true);
+    launch_gk_combine(b, a, soR.p, s.sR.p, d * K, std::min((d + 1) * K, s.L), s.pmod_plain.p, nm, s.d_mods.p, N, s.st);
+  }
+  launch_mont_convert(key->p, (size_t)nm * N, 2 * s.dnum, rows_all(), s.d_mods.p, N, true, s.st);
+  sync();
+  s.gkeys[galel] = std::move(key);
+}
+
+// ============================================================================
+// encoder: float64 special FFT on the host (Lattigo ckks.Encoder algorithm),
+// fixed-point rounding to per-coefficient records, residues + NTT on the GPU
+// ============================================================================
+void init_encoder(Scheme& s) {
+  const int M = 2 * s.N, slots = s.N / 2, quarm = M >> 2;
+  s.rre.assign(M + 1, 0.0); s.rim.assign(M + 1, 0.0);
+  const double angle = 2.0 * 3.141592653589793 / (double)M;
+  for (int i = 0; i < quarm; i++) s.rre[i] = std::cos(angle * (double)i);
+  for (int i = 0; i < quarm; i++) s.rim[quarm - i] += s.rre[i];
+  for (int i = 1; i < quarm + 1; i++) { s.rre[i + quarm] = -s.rre[quarm - i]; s.rim[i + quarm] = s.rim[quarm - i]; }
+  for (int i = 1; i < quarm + 1; i++) { s.rre[i + 2 * quarm] = -s.rre[i]; s.rim[i + 2 * quarm] = -s.rim[i]; }
+  for (int i = 1; i < quarm; i++) { s.rre[i + 3 * quarm] = s.rre[quarm - i]; s.rim[i + 3 * quarm] = -s.rim[quarm - i]; }
+  s.rre[M] = s.rre[0]; s.rim[M] = s.rim[0];
+  s.rotgroup.resize(slots);
+  u64 p = 1;
+  for (int j = 0; j < slots; j++) { s.rotgroup[j] = (int)p; p = (p * 5) & (u64)(M - 1); }
+}
+void bitrev(std::vector<double>& re, std::vector<double>& im, int n) {
+  int logn = 0; while ((1 << logn) < n) logn++;
+  for (int i = 0; i < n; i++) { int j = brv(i, logn); if (j > i) { std::swap(re[i], re[j]); std::swap(im[i], im[j]); } }
+}
+void special_ifft(const Scheme& s, std::vector<double>& re, std::vector<double>& im, int n) {
+  const int M = 2 * s.N;
+  for (int len = n; len >= 2; len >>= 1) {
+    int lenh = len >> 1, lenq = len << 2, gap = M / lenq, mask = lenq - 1;
+    for (int i = 0; i < n; i += len)
+      for (int j = 0; j < lenh; j++) {
+        int k = i + j;
+        double ur = re[k], ui = im[k], vr = re[k + lenh], vi = im[k + lenh];
+        int idx = (lenq - (s.rotgroup[j] & mask)) * gap;
+        double wr = s.rre[idx], wi = s.rim[idx];
+        double dr = ur - vr, di = ui - vi;
+        re[k] = ur + vr; im[k] = ui + vi;
+        re[k + lenh] = dr * wr - di * wi; im[k + lenh] = dr * wi + di * wr;
+      }
+  }
+  bitrev(re, im, n);
+  for (int i = 0; i < n; i++) { re[i] /= (double)n; im[i] /= (double)n; }
+}
+void special_fft(const Scheme& s, std::vector<double>& re, std::vector<double>& im, int n) {
+  const int M = 2 * s.N;
+  bitrev(re, im, n);
+  for (int len = 2; len <= n; len <<= 1) {
+    int lenh = len >> 1, lenq = len << 2, gap = M / lenq, mask = lenq - 1;
+    for (int i = 0; i < n; i += len)
+      for (int j = 0; j < lenh; j++) {
+        int k = i + j;
+        int idx = (s.rotgroup[j] & mask) * gap;
+        double wr = s.rre[idx], wi = s.rim[idx];
+        double ur = re[k], ui = im[k], xr = re[k + lenh], xi = im[k + lenh];
+        double vr = xr * wr - xi * wi, vi = xr * wi + xi * wr;
+        re[k] = ur + vr; im[k] = ui + vi;
+        re[k + lenh] = ur - vr; im[k + lenh] = ui - vi;
+      }
+  }
+}
+// one coefficient -> {magnitude, neg | shift<<8}: |v|*scale, +0.5 and truncate
+// below 2^64; exact mantissa * 2^shift above (Lattigo SingleFloat64ToFixedPointCRT)
+inline void fixed_point(double value, double scale, u64* rec) {
+  if (value == 0) { rec[0] = 0; rec[1] = 0; return; }
+  u64 neg = 0;
+  if (value < 0) { neg = 1; scale *= -1; }
+  value *= scale;
+  if (value >= 1.8446744073709552e+19) {
+    int e; double m = std::frexp(value, &e);
+    rec[0] = (u64)std::ldexp(m, 53);
+    rec[1] = neg | ((u64)(e - 53) << 8);
+  } else {
+    rec[0] = (u64)(value + 0.5);
+    rec[1] = neg;
+  }
+}
+void encode_records(const Scheme& s, const double* v, int n, double scale, std::vector<u64>& rec) {
+  const int slots = s.N / 2;
+  std::vector<double> re(slots, 0.0), im(slots, 0.0);
+  for (int i = 0; i < n && i < slots; i++) re[i] = v[i];
+  special_ifft(s, re, im, slots);
+  rec.resize((size_t)2 * s.N);
+  for (int i = 0; i < slots; i++) { fixed_point(re[i], scale, &rec[2 * i]); fixed_point(im[i], scale, &rec[2 * (i + slots)]); }
+}
+// residues of records into rows rm of out, then forward NTT
+void encode_to_device(const std::vector<u64>& rec, RowMap rm, u64* out) {
+  Scheme& s = sch();
+  DU64 drec(rec.size()); upload(drec.p, rec.data(), rec.size());
+  launch_encode_residues(out, rm, drec.p, s.d_mods.p, s.N, s.st);
+  ntt(out, 0, 1, rm, true);
+  sync();
+}
+
+// ---- big integers for the decoder's centred CRT ----
+struct Big { std::vector<u64> w; };
+void big_norm(Big& a) { while (!a.w.empty() && a.w.back() == 0) a.w.pop_back(); }
+void big_mul_small(Big& a, u64 m) {
+  u128 c = 0;
+  for (auto& x : a.w) { u128 t = (u128)x * m + c; x = (u64)t; c = t >> 64; }
+  if (c) a.w.push_back((u64)c);
+  big_norm(a);
+}
+int big_cmp(const Big& a, const Big& b) {
+  if (a.w.size() != b.w.size()) return a.w.size() < b.w.size() ? -1 : 1;
+  for (size_t i = a.w.size(); i-- > 0;) if (a.w[i] != b.w[i]) return a.w[i] < b.w[i] ? -1 : 1;
+  return 0;
+}
+void big_add(Big& a, const Big& b) {
+  size_t n = std::max(a.w.size(), b.w.size()); a.w.resize(n, 0); u64 c = 0;
+  for (size_t i = 0; i < n; i++) { u128 t = (u128)a.w[i] + (i < b.w.size() ? b.w[i] : 0) + c; a.w[i] = (u64)t; c = (u64)(t >> 64); }
+  if (c) a.w.push_back(c);
+}
+void big_sub(Big& a, const Big& b) {  // a >= b
+  u64 br = 0;
+  for (size_t i = 0; i < a.w.size(); i++) { u128 t = (u128)a.w[i] - (i < b.w.size() ? b.w[i] : 0) - br; a.w[i] = (u64)t; br = (u64)(t >> 64) ? 1 : 0; }
+  big_norm(a);
+}
+double big_to_double(const Big& a) {  // nearest, ties to even
+  if (a.w.empty()) return 0.0;
+  int top = (int)a.w.size() - 1, lz = __builtin_clzll(a.w[top]);
+  int bitlen = top * 64 + (64 - lz);
+  if (bitlen <= 64) return (double)a.w[0];
+  int sh = bitlen - 64, wi = sh / 64, bi = sh % 64;
+  u64 hi = bi ? (a.w[wi] >> bi) | (a.w[wi + 1] << (64 - bi)) : a.w[wi];
+  bool sticky = bi && (a.w[wi] & ((1ULL << bi) - 1));
+  for (int i = 0; i < wi; i++) if (a.w[i]) sticky = true;
+  if (sticky) hi |= 1;
+  return std::ldexp((double)hi, sh);
+}
+// Lattigo Encoder.Decode (float64): centred CRT value / scale, SpecialFFT, real part
+std::vector<double> decode_host(const std::vector<u64>& coef, int level, double scale) {
+  Scheme& s = sch();
+  const int N = s.N, slots = N / 2, nl = level + 1;
+  std::vector<double> vals(N);
+  if (level == 0) {
+    u64 q = s.mod[0];
+    for (int x = 0; x < N; x++) { u64 v = coef[x]; vals[x] = (v >= (q >> 1) ? -(double)(q - v) : (double)v) / scale; }
+  } else {
+    Big Q; Q.w = {1};
+    for (int i = 0; i < nl; i++) big_mul_small(Q, s.mod[i]);
+    Big Qh = Q;
+    for (size_t i = 0; i < Qh.w.size(); i++) Qh.w[i] = (Qh.w[i] >> 1) | (i + 1 < Qh.w.size() ? Qh.w[i + 1] << 63 : 0);
+    big_norm(Qh);
+    std::vector<Big> hat(nl); std::vector<u64> hinv(nl);
+    for (int i = 0; i < nl; i++) {
+      hat[i].w = {1}; u64 pr = 1;
+      for (int j = 0; j < nl; j++) if (j != i) { big_mul_small(hat[i], s.mod[j]); pr = mulmod(pr, s.mod[j] % s.mod[i], s.mod[i]); }
+      hinv[i] = invmod(pr, s.mod[i]);
+    }
+    auto work = [&](int x0, int x1) {
+      for (int x = x0; x < x1; x++) {
+        Big acc;
+        for (int i = 0; i < nl; i++) {
+          u64 y = mulmod(coef[(size_t)i * N + x], hinv[i], s.mod[i]);
+          Big t = hat[i]; big_mul_small(t, y); big_add(acc, t);
+        }
+        while (big_cmp(acc, Q) >= 0) big_sub(acc, Q);
+        double d;
+        if (big_cmp(acc, Qh) >= 0) { Big t = Q; big_sub(t, acc); d = -big_to_double(t); }
+        else d = big_to_double(acc);
+        vals[x] = d / scale;
+      }
+    };
+    int nt = (int)std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency()));
+    if (N < 4096) nt = 1;
+    std::vector<std::thread> th;
+    for (int t = 0; t < nt; t++) th.emplace_back(work, (int)((long)N * t / nt), (int)((long)N * (t + 1) / nt));
+    for (auto& t : th) t.join();
+  }
+  std::vector<double> re(slots), im(slots);
+  for (int i = 0; i < slots; i++) { re[i] = vals[i]; im[i] = vals[i + slots]; }
+  special_fft(s, re, im, slots);
+  return re;
+}
+
+// ============================================================================
+// scheme construction
+// ============================================================================
+void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p, int logscale, int h, u64 seed) {
+  REQUIRE(logN >= 10 && logN <= 16, "LogN must be in [10, 16] on this backend");
+  REQUIRE(!q.empty() && !p.empty(), "need at least one Q and one P prime");
+  REQUIRE(q.size() + p.size() <= HCK_MAXMOD, "too many moduli");
+  if (!g_pool) g_pool = new Pool();
+  auto sp = std::make_unique<Scheme>();
+  Scheme& s = *sp;
+  s.logN = logN; s.N = 1 << logN; s.L = (int)q.size(); s.K = (int)p.size();
+  s.dnum = (s.L + s.K - 1) / s.K; s.logscale = logscale; s.h = h; s.seed = seed;
+  REQUIRE(s.K <= HCK_MAXSRC, "too many special primes");
+  s.mod = q; s.mod.insert(s.mod.end(), p.begin(), p.end());
+  for (u64 m : s.mod) {
+    REQUIRE(m < (1ULL << 62) && m > 2, "moduli must be < 2^62");
+    REQUIRE((m - 1) % (2 * (u64)s.N) == 0, "moduli must be 1 mod 2N");
+    REQUIRE(is_prime(m), "moduli must be prime");
+  }
+  for (size_t i = 0; i < s.mod.size(); i++) for (size_t j = i + 1; j < s.mod.size(); j++) REQUIRE(s.mod[i] != s.mod[j], "moduli must be distinct");
+  HCHECK(hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking));
+  Scheme* old = S; S = sp.get();
+  try {
+    const int N = s.N, nm = s.L + s.K;
+    s.hmods.resize(nm);
+    for (int m = 0; m < nm; m++) {
+      u64 qq = s.mod[m];
+      u64 inv = 1; for (int it = 0; it < 7; it++) inv *= 2 - qq * inv;  // q^-1 mod 2^64
+      u64 rmod = (u64)(((u128)1 << 64) % qq);
+      s.hmods[m] = ModC{qq, (u64)0 - inv, mulmod(rmod, rmod, qq), rmod};
+    }
+    s.d_mods = DevArray<ModC>(nm); upload(s.d_mods.p, s.hmods.data(), nm);
+    std::vector<u64> hw((size_t)nm * N), hwp((size_t)nm * N), hiw((size_t)nm * N), hiwp((size_t)nm * N), hn(nm), hnp(nm);
+    for (int m = 0; m < nm; m++) {
+      u64 qq = s.mod[m];
+      u64 g = smallest_generator(qq);
+      u64 psi = powmod(g, (qq - 1) / (2 * (u64)N), qq), ipsi = invmod(psi, qq);
+      std::vector<u64> pw(N), ipw(N);
+      pw[0] = ipw[0] = 1;
+      for (int i = 1; i < N; i++) { pw[i] = mulmod(pw[i - 1], psi, qq); ipw[i] = mulmod(ipw[i - 1], ipsi, qq); }
+      for (int i = 0; i < N; i++) {
+        int r = brv(i, logN);
+        hw[(size_t)m * N + i] = pw[r]; hwp[(size_t)m * N + i] = shoup(pw[r], qq);
+        hiw[(size_t)m * N + i] = ipw[r]; hiwp[(size_t)m * N + i] = shoup(ipw[r], qq);
+      }
+      hn[m] = invmod((u64)N, qq); hnp[m] = shoup(hn[m], qq);
+    }
+    auto up = [&](DU64& d, const std::vector<u64>& h) { d = DU64(h.size()); upload(d.p, h.data(), h.size()); };
+    up(s.w, hw); up(s.wp, hwp); up(s.iw, hiw); up(s.iwp, hiwp); up(s.ninv, hn); up(s.ninvp, hnp);
+    s.tw = NttTables{s.d_mods.p, s.w.p, s.wp.p, s.iw.p, s.iwp.p, s.ninv.p, s.ninvp.p};
+    std::vector<u64> pm(nm), pmp(nm), pin(nm), pinp(nm), p0i(nm), p0ip(nm), pmr(nm);
+    for (int m = 0; m < nm; m++) {
+      u64 qq = s.mod[m], P = 1;
+      for (int j = 0; j < s.K; j++) P = mulmod(P, s.mod[s.L + j] % qq, qq);
+      pm[m] = P; pmp[m] = shoup(P, qq);
+      pmr[m] = P;  // P mod q, multiplied against s*R by the Galois-key kernel
+      pin[m] = m < s.L ? invmod(P, qq) : 0; pinp[m] = shoup(pin[m], qq);
+      p0i[m] = m < s.L ? invmod(s.mod[s.L] % qq, qq) : 0; p0ip[m] = shoup(p0i[m], qq);
+    }
+    up(s.pmod_w, pm); up(s.pmod_wp, pmp); up(s.pinv_w, pin); up(s.pinv_wp, pinp); up(s.p0inv_w, p0i); up(s.p0inv_wp, p0ip); up(s.pmod_plain, pmr);
+    std::vector<u64> ri((size_t)s.L * s.L, 0), rip((size_t)s.L * s.L, 0);
+    for (int l = 1; l < s.L; l++)
+      for (int i = 0; i < l; i++) { u64 v = invmod(s.mod[l] % s.mod[i], s.mod[i]); ri[(size_t)l * s.L + i] = v; rip[(size_t)l * s.L + i] = shoup(v, s.mod[i]); }
+    up(s.rs_inv, ri); up(s.rs_invp, rip);
+    init_encoder(s);
+  } catch (...) {
+    S = old;
+    throw;
+  }
+  if (old) { HCHECK(hipStreamSynchronize(old->st)); (void)hipStreamDestroy(old->st); delete old; }
+  sp.release();
+}
+
+// ============================================================================
+// object helpers
+// ============================================================================
+Plain& get_pt(int id) { auto it = sch().pts.find(id); REQUIRE(it != sch().pts.end(), "plaintext not found: " + std::to_string(id)); return *it->second; }
+Cipher& get_ct(int id) { auto it = sch().cts.find(id); REQUIRE(it != sch().cts.end(), "ciphertext not found: " + std::to_string(id)); return *it->second; }
+LinTrans& get_lt(int id) { auto it = sch().lts.find(id); REQUIRE(it != sch().lts.end(), "linear transform not found: " + std::to_string(id)); return *it->second; }
+int push_pt(std::unique_ptr<Plain> p) { Scheme& s = sch(); int id = s.pt_ids.take(); s.pts[id] = std::move(p); return id; }
+int push_ct(std::unique_ptr<Cipher> c) { Scheme& s = sch(); int id = s.ct_ids.take(); s.cts[id] = std::move(c); return id; }
+std::unique_ptr<Cipher> new_ct(int level, double scale) {
+  Scheme& s = sch();
+  auto c = std::make_unique<Cipher>();
+  c->level = level; c->scale = scale; c->logslots = s.logN - 1;
+  c->d = DU64((size_t)2 * (level + 1) * s.N);
+  return c;
+}
+std::unique_ptr<Cipher> copy_ct(const Cipher& a) {
+  auto c = new_ct(a.level, a.scale); c->logslots = a.logslots;
+  d2d(c->d.p, a.d.p, a.d.bytes());
+  return c;
+}
+// drop ciphertext limbs above `level`
+void ct_drop_to(Cipher& c, int level) {
+  Scheme& s = sch();
+  if (c.level == level) return;
+  DU64 d((size_t)2 * (level + 1) * s.N);
+  d2d_2d(d.p, (size_t)(level + 1) * s.N * 8, c.d.p, (size_t)(c.level + 1) * s.N * 8, (size_t)(level + 1) * s.N * 8, 2);
+  c.d = std::move(d); c.level = level;
+}
+
+// ============================================================================
+// evaluator operations
+// ============================================================================
+std::unique_ptr<Cipher> automorphism(const Cipher& ct, u64 galel, bool lt_keyset) {
+  Scheme& s = sch();
+  const int l = ct.level, N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
+  const u64* key = key_ptr(galel, lt_keyset);
+  DU64 digits((size_t)dn * nqp * N);
+  decompose_modup(l, ct.d.p + (size_t)(l + 1) * N, 0, 1, digits.p);
+  DU64 dd((size_t)2 * nqp * N);
+  DevArray<const u64*> kp(1); DevArray<const uint32_t*> pp(1);
+  const u64* kh[1] = {key}; const uint32_t* ph[1] = {nullptr};
+  upload(kp.p, kh, 1); upload(pp.p, ph, 1);
+  KeyMacArgs a{};
+  a.digits = digits.p; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = kp.p; a.perm = pp.p; a.add0 = nullptr;
+  a.out0 = dd.p; a.out1 = dd.p + (size_t)nqp * N; a.out_bstride = 0; a.mods = s.d_mods.p;
+  a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
+  launch_keymac(a, 1, s.st);
+  auto out = new_ct(l, ct.scale); out->logslots = ct.logslots;
+  mod_down(l, dd.p, (size_t)nqp * N, 2, out->d.p, (size_t)(l + 1) * N, ct.d.p, 0, 1, perm_for(galel));
+  return out;
+}
+std::unique_ptr<Cipher> rescale_ct(const Cipher& ct) {
+  Scheme& s = sch();
+  const int l = ct.level, N = s.N;
+  REQUIRE(l >= 1, "cannot rescale: ciphertext already at level 0");
+  DU64 u((size_t)2 * N), t((size_t)2 * l * N);
+  d2d_2d(u.p, (size_t)N * 8, ct.d.p + (size_t)l * N, (size_t)(l + 1) * N * 8, (size_t)N * 8, 2);
+  ntt(u.p, N, 2, RowMap{1, 1, l, 0, 0, 0}, false);
+  launch_rescale_spread(t.p, u.p, l, s.mod[l] >> 1, s.d_mods.p, N, s.st);
+  ntt(t.p, (size_t)l * N, 2, rows_q(l - 1), true);
+  auto out = new_ct(l - 1, ct.scale / (double)s.mod[l]); out->logslots = ct.logslots;
+  launch_rescale_combine(out->d.p, ct.d.p, t.p, l, s.rs_inv.p + (size_t)l * s.L, s.rs_invp.p + (size_t)l * s.L, s.d_mods.p, N, s.st);
+  return out;
+}
+// Lattigo ckks Rescale: divide by the last moduli while the scale stays >= default/2
+std::unique_ptr<Cipher> rescale_lattigo(const Cipher& ct) {
+  Scheme& s = sch();
+  REQUIRE(ct.level >= 1, "cannot rescale: ciphertext already at level 0");
+  double minscale = std::ldexp(1.0, s.logscale) / 2.0;
+  double sc = ct.scale; int lvl = ct.level, nb = 0;
+  while (lvl >= 1) { double ns = sc / (double)s.mod[lvl]; if (ns < minscale) break; sc = ns; lvl--; nb++; }
+  if (nb == 0) return copy_ct(ct);
+  std::unique_ptr<Cipher> cur = rescale_ct(ct);
+  for (int i = 1; i < nb; i++) cur = rescale_ct(*cur);
+  return cur;
+}
+void add_inplace(Cipher& a, const Cipher& b, bool sub) {
+  Scheme& s = sch();
+  REQUIRE(a.scale == b.scale, "ciphertext scales differ");
+  int l = std::min(a.level, b.level);
+  ct_drop_to(a, l);
+  const size_t bs_b = (size_t)(b.level + 1) * s.N;
+  for (int p = 0; p < 2; p++)
+    launch_add(a.d.p + (size_t)p * (l + 1) * s.N, a.d.p + (size_t)p * (l + 1) * s.N, b.d.p + (size_t)p * bs_b, 0, 1, rows_q(l), s.d_mods.p, s.N, sub, s.st);
+}
+void add_plain_inplace(Cipher& a, const Plain& p, bool sub) {
+  Scheme& s = sch();
+  REQUIRE(a.scale == p.scale, "ciphertext and plaintext scales differ");
+  int l = std::min(a.level, p.level);
+  ct_drop_to(a, l);
+  launch_add(a.d.p, a.d.p, p.d.p, 0, 1, rows_q(l), s.d_mods.p, s.N, sub, s.st);
+}
+
+// ============================================================================
+// linear transform (lintrans restated for the GPU)
+// ============================================================================
+void bsgs_index(const std::vector<int>& diags, int slots, int N1, std::vector<int>& r1, std::vector<int>& r2) {
+  std::set<int> a, b;
+  for (int d : diags) { int r = d & (slots - 1); a.insert(((r / N1) * N1) & (slots - 1)); b.insert(r & (N1 - 1)); }
+  r1.assign(a.begin(), a.end()); r2.assign(b.begin(), b.end());
+}
+int find_best_bsgs_ratio(const std::vector<int>& diags, int maxN, int logMaxRatio) {
+  double maxRatio = (double)(1 << logMaxRatio);
+  for (int N1 = 1; N1 < maxN; N1 <<= 1) {
+    std::vector<int> r1, r2; bsgs_index(diags, maxN, N1, r1, r2);
+    double nbN1 = (double)r1.size() - 1, nbN2 = (double)r2.size() - 1;
+    double ratio = nbN2 / nbN1;
+    if (ratio == maxRatio) return N1;
+    if (ratio > maxRatio) return N1 / 2;
+  }
+  return 1;
+}
+std::vector<int> lt_rotations(const LinTrans& t) {
+  std::vector<int> out;
+  if (t.naive) { for (int r : t.rot2) out.push_back(r); return out; }
+  for (int r : t.rot1) out.push_back(r);
+  for (int r : t.rot2) if (std::find(out.begin(), out.end(), r) == out.end()) out.push_back(r);
+  return out;
+}
+
+int generate_lt(const int* idx, int nidx, const float* data, int ndata, int level, float ratio) {
+  Scheme& s = sch();
+  const int N = s.N, slots = N / 2, K = s.K;
+  REQUIRE(nidx > 0, "no diagonals");
+  REQUIRE(ndata == nidx * slots, "diagonal data length must be len(diag_idxs) * slots");
+  REQUIRE(level >= 0 && level < s.L, "invalid level");
+  auto t = std::make_unique<LinTrans>();
+  t->level = level; t->slots = slots;
+  t->keys.assign(idx, idx + nidx);
+  int logratio = (int)std::log((double)ratio);
+  t->scale = (double)s.mod[level];
+  std::vector<std::pair<int, int>> order;  // (diag index, source row)
+  auto src_of = [&](int di) { for (int i = 0; i < nidx; i++) if (idx[i] == di || idx[i] == di - slots) return i; throw Error("lintrans: diagonal missing"); };
+  std::vector<int> rotv;  // pre-rotation per plaintext
+  if (logratio < 0) {
+    t->naive = true; t->N1 = 0;
+    bsgs_index(t->keys, slots, slots, t->rot1, t->rot2);
+    for (int i = 0; i < nidx; i++) { int di = idx[i] < 0 ? idx[i] + slots : idx[i]; order.push_back({di, i}); rotv.push_back(0); }
+  } else {
+    t->N1 = find_best_bsgs_ratio(t->keys, slots, logratio);
+    REQUIRE(t->N1 >= 1, "invalid baby-step size");
+    bsgs_index(t->keys, slots, t->N1, t->rot1, t->rot2);
+    REQUIRE(t->rot2.size() <= 64, "more than 64 baby steps are not supported");
+    t->giant = t->rot1;
+    t->baby.assign(t->giant.size(), {});
+    for (int d : t->keys) {
+      int r = d & (slots - 1), j = ((r / t->N1) * t->N1) & (slots - 1), b = r & (t->N1 - 1);
+      size_t g = std::lower_bound(t->giant.begin(), t->giant.end(), j) - t->giant.begin();
+      t->baby[g].push_back(b);
+    }
+    for (auto& bl : t->baby) { std::sort(bl.begin(), bl.end()); bl.erase(std::unique(bl.begin(), bl.end()), bl.end()); }
+    for (size_t g = 0; g < t->giant.size(); g++)
+      for (int b : t->baby[g]) { int di = t->giant[g] + b; order.push_back({di, src_of(di)}); rotv.push_back((-t->giant[g]) & (slots - 1)); }
+  }
+  const int np = (int)order.size(), nqp_lt = level + 1 + K;
+  t->diags = DU64((size_t)np * nqp_lt * N);
+  RowMap rm{nqp_lt, level + 1, 0, s.L, 0, 0};
+  // host FFT in parallel, device residues + NTT + Montgomery conversion per batch
+  const int chunk = 16;
+  std::vector<std::vector<u64>> recs(chunk);
+  for (int c0 = 0; c0 < np; c0 += chunk) {
+    int c1 = std::min(np, c0 + chunk);
+    std::vector<std::thread> th;
+    for (int p = c0; p < c1; p++)
+      th.emplace_back([&, p]() {
+        std::vector<double> buf(slots);
+        int src = order[p].second, rot = rotv[p];
+        for (int k = 0; k < slots; k++) buf[k] = (double)data[(size_t)src * slots + ((k + rot) & (slots - 1))];
+        encode_records(s, buf.data(), slots, t->scale, recs[p - c0]);
+      });
+    for (auto& x : th) x.join();
+    for (int p = c0; p < c1; p++) encode_to_device(recs[p - c0], rm, t->diags.p + (size_t)p * nqp_lt * N);
+  }
+  launch_mont_convert(t->diags.p, (size_t)nqp_lt * N, np, rm, s.d_mods.p, N, true, s.st);
+  for (auto& o : order) t->plain_idx.push_back(o.first);
+  if (!t->naive) {
+    const int ng = (int)t->giant.size(), nb = (int)t->rot2.size();
+    std::vector<uint64_t> gmask(ng, 0); std::vector<int> gpidx(ng, 0), bzero(nb, 0), bslot(nb, 0);
+    int pidx = 0;
+    for (int g = 0; g < ng; g++) {
+      gpidx[g] = pidx;
+      for (int b : t->baby[g]) { int pos = (int)(std::lower_bound(t->rot2.begin(), t->rot2.end(), b) - t->rot2.begin()); gmask[g] |= 1ULL << pos; pidx++; }
+    }
+    int slot = 0;
+    for (int i = 0; i < nb; i++) { bzero[i] = t->rot2[i] == 0; bslot[i] = t->rot2[i] == 0 ? 0 : slot++; }
+    t->d_gmask = DevArray<uint64_t>(ng); upload(t->d_gmask.p, gmask.data(), ng);
+    t->d_gpidx = DevArray<int>(ng); upload(t->d_gpidx.p, gpidx.data(), ng);
+    t->d_bzero = DevArray<int>(nb); upload(t->d_bzero.p, bzero.data(), nb);
+    t->d_bslot = DevArray<int>(nb); upload(t->d_bslot.p, bslot.data(), nb);
+  }
+  sync();
+  int id = s.lt_ids.take();
+  s.lts[id] = std::move(t);
+  return id;
+}
+
+// MultiplyByDiagMatrixBSGS on the GPU: one decomposition, batched hoisted
+// baby rotations, one fused diagonal-MAC pass producing every giant group's
+// QP accumulators, batched ModDown + decomposition of the giant groups' c1
+// parts, one fused key-product/automorphism/accumulate pass, final ModDown.
+std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct) {
+  Scheme& s = sch();
+  const int N = s.N, K = s.K;
+  const int l = std::min(ct.level, t.level), nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
+  const size_t qp = (size_t)nqp * N;
+  const u64* c0 = ct.d.p;
+  const u64* c1 = ct.d.p + (size_t)(ct.level + 1) * N;
+  // 1. decomposition of c1 and P*c
+  DU64 digits((size_t)dn * qp);
+  decompose_modup(l, c1, 0, 1, digits.p);
+  DU64 pc((size_t)2 * (l + 1) * N);
+  launch_mul_const(pc.p, c0, 0, 1, rows_q(l), s.pmod_w.p, s.pmod_wp.p, s.d_mods.p, N, s.st);
+  launch_mul_const(pc.p + (size_t)(l + 1) * N, c1, 0, 1, rows_q(l), s.pmod_w.p, s.pmod_wp.p, s.d_mods.p, N, s.st);
+  // 2. hoisted baby rotations (sigma(d0 + P c0), sigma(d1)) in QP
+  std::vector<int> babies;
+  for (int b : t.rot2) if (b != 0) babies.push_back(b);
+  const int nbr = (int)babies.size();
+  DU64 R((size_t)std::max(nbr, 1) * 2 * qp);
+  if (nbr > 0) {
+    std::vector<const u64*> kh(nbr); std::vector<const uint32_t*> ph(nbr);
+    for (int i = 0; i < nbr; i++) { u64 ge = galois_element(babies[i]); kh[i] = key_ptr(ge, true); ph[i] = perm_for(ge); }
+    DevArray<const u64*> kp(nbr); DevArray<const uint32_t*> pp(nbr);
+    upload(kp.p, kh.data(), nbr); upload(pp.p, ph.data(), nbr);
+    KeyMacArgs a{};
+    a.digits = digits.p; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = kp.p; a.perm = pp.p; a.add0 = pc.p;
+    a.out0 = R.p; a.out1 = R.p + qp; a.out_bstride = 2 * qp; a.mods = s.d_mods.p;
+    a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
+    timed("keymac_baby", [&] { launch_keymac(a, nbr, s.st); });
+  }
+  // 3. fused diagonal MAC -> T[g][2][nqp][N]
+  const int ng = (int)t.giant.size(), nb = (int)t.rot2.size();
+  DU64 T((size_t)ng * 2 * qp);
+  {
+    DiagMacArgs a{};
+    a.diag = t.diags.p; a.diag_stride = (size_t)(t.level + 1 + K) * N;
+    a.R = R.p; a.R_bstride = 2 * qp; a.R_pstride = qp;
+    a.pc = pc.p; a.pc_pstride = (size_t)(l + 1) * N;
+    a.baby_is_zero = t.d_bzero.p; a.baby_slot = t.d_bslot.p; a.gmask = t.d_gmask.p; a.gpidx = t.d_gpidx.p;
+    a.T = T.p; a.T_gstride = 2 * qp; a.T_pstride = qp; a.mods = s.d_mods.p;
+    a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.lt_level = t.level; a.ng = ng; a.nbaby = nb;
+    for (int b0 = 0; b0 < nb; b0 += 32) {
+      a.b0 = b0; a.nb_chunk = std::min(32, nb - b0);
+      timed("diag_mac", [&] { launch_diag_mac(a, s.st); });
+    }
+  }
+  // 4. giant groups with a nonzero rotation: ModDown of part 1, decomposition, key product + automorphism + accumulate
+  const int gs = (ng > 0 && t.giant[0] == 0) ? 1 : 0;
+  const int ngk = ng - gs;
+  DU64 acc((size_t)2 * qp);
+  if (ngk > 0) {
+    DU64 t1q((size_t)ngk * (l + 1) * N);
+    mod_down(l, T.p + (size_t)gs * 2 * qp + qp, 2 * qp, ngk, t1q.p, (size_t)(l + 1) * N);
+    DU64 dg2((size_t)ngk * dn * qp);
+    decompose_modup(l, t1q.p, (size_t)(l + 1) * N, ngk, dg2.p);
+    std::vector<const u64*> kh(ngk); std::vector<const uint32_t*> ph(ngk); std::vector<int> tg(ngk);
+    for (int g = 0; g < ngk; g++) { u64 ge = galois_element(t.giant[gs + g]); kh[g] = key_ptr(ge, true); ph[g] = perm_for(ge); tg[g] = gs + g; }
+    DevArray<const u64*> kp(ngk); DevArray<const uint32_t*> pp(ngk); DevArray<int> dtg(ngk);
+    upload(kp.p, kh.data(), ngk); upload(pp.p, ph.data(), ngk); upload(dtg.p, tg.data(), ngk);
+    GiantAccArgs a{};
+    a.digits = dg2.p; a.dig_bstride = (size_t)dn * qp; a.key = kp.p; a.perm = pp.p; a.tg = dtg.p; a.ng = ngk;
+    a.T = T.p; a.T_gstride = 2 * qp; a.T_pstride = qp; a.t_zero = gs ? 0 : -1;
+    a.out0 = acc.p; a.out1 = acc.p + qp; a.mods = s.d_mods.p;
+    a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
+    timed("giant_acc", [&] { launch_giant_acc(a, s.st); });
+    // dg2 / t1q / kp stay alive until the stream reaches this point (pool reuse is stream-ordered)
+  } else {
+    d2d(acc.p, T.p, 2 * qp * 8);
+  }
+  // 5. final ModDown of both parts
+  auto out = new_ct(l, ct.scale * t.scale); out->logslots = ct.logslots;
+  mod_down(l, acc.p, qp, 2, out->d.p, (size_t)(l + 1) * N);
+  return out;
+}
+// MultiplyByDiagMatrix (naive, N1 = 0)
+std::unique_ptr<Cipher> eval_lt_naive(const LinTrans& t, const Cipher& ct) {
+  Scheme& s = sch();
+  const int N = s.N, K = s.K;
+  const int l = std::min(ct.level, t.level), nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
+  const size_t qp = (size_t)nqp * N;
+  const u64* c0 = ct.d.p;
+  const u64* c1 = ct.d.p + (size_t)(ct.level + 1) * N;
+  DU64 digits((size_t)dn * qp);
+  decompose_modup(l, c1, 0, 1, digits.p);
+  DU64 pc((size_t)(l + 1) * N);
+  launch_mul_const(pc.p, c0, 0, 1, rows_q(l), s.pmod_w.p, s.pmod_wp.p, s.d_mods.p, N, s.st);
+  std::vector<int> nz; int zero_p = -1;
+  for (size_t i = 0; i < t.plain_idx.size(); i++) { if ((t.plain_idx[i] & (t.slots - 1)) == 0) zero_p = (int)i; else nz.push_back((int)i); }
+  DU64 acc((size_t)2 * qp);
+  HCHECK(hipMemsetAsync(acc.p, 0, acc.bytes(), s.st));
+  const size_t dstride = (size_t)(t.level + 1 + K) * N;
+  if (!nz.empty()) {
+    const int n = (int)nz.size();
+    std::vector<const u64*> kh(n); std::vector<const uint32_t*> ph(n);
+    for (int i = 0; i < n; i++) { u64 ge = galois_element(t.plain_idx[nz[i]] & (t.slots - 1)); kh[i] = key_ptr(ge, true); ph[i] = perm_for(ge); }
+    DevArray<const u64*> kp(n); DevArray<const uint32_t*> pp(n);
+    upload(kp.p, kh.data(), n); upload(pp.p, ph.data(), n);
+    DU64 R((size_t)n * 2 * qp);
+    KeyMacArgs a{};
+    a.digits = digits.p; a.key = kp.p; a.perm = pp.p; a.add0 = pc.p;
+    a.out0 = R.p; a.out1 = R.p + qp; a.out_bstride = 2 * qp; a.mods = s.d_mods.p;
+    a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
+    launch_keymac(a, n, s.st);
+    RowMap rm = rows_qp(l);
+    RowMap prm{nqp, l + 1, 0, t.level + 1, 0, 0};  // unused mapping helper
+    (void)prm;
+    for (int i = 0; i < n; i++) {
+      const u64* dp = t.diags.p + (size_t)nz[i] * dstride;
+      // the diagonal's P rows sit after its own Q rows (level t.level); multiply Q and P parts separately
+      launch_mont_mul(acc.p, qp, R.p + (size_t)i * 2 * qp, qp, dp, 0, 2, rows_q(l), s.d_mods.p, N, true, s.st);
+      launch_mont_mul(acc.p + (size_t)(l + 1) * N, qp, R.p + (size_t)i * 2 * qp + (size_t)(l + 1) * N, qp, dp + (size_t)(t.level + 1) * N, 0, 2,
+                      RowMap{K, 0, 0, s.L, 0, 0}, s.d_mods.p, N, true, s.st);
+      (void)rm;
+    }
+  }
+  auto out = new_ct(l, ct.scale * t.scale); out->logslots = ct.logslots;
+  mod_down(l, acc.p, qp, 2, out->d.p, (size_t)(l + 1) * N);
+  if (zero_p >= 0) {
+    const u64* dp = t.diags.p + (size_t)zero_p * dstride;
+    launch_mont_mul(out->d.p, (size_t)(l + 1) * N, c0, 0, dp, 0, 1, rows_q(l), s.d_mods.p, N, true, s.st);
+    launch_mont_mul(out->d.p + (size_t)(l + 1) * N, 0, c1, 0, dp, 0, 1, rows_q(l), s.d_mods.p, N, true, s.st);
+  }
+  return out;
+}
+
+// ============================================================================
+// encrypt / decrypt
+// ============================================================================
+std::unique_ptr<Cipher> encrypt_pt(const Plain& pt) {
+  Scheme& s = sch();
+  REQUIRE(s.has_pk, "public key not generated");
+  const int l = pt.level, N = s.N, nm = s.L + s.K, nr = l + 2;
+  const u64 enc = s.enc_counter++;
+  std::vector<int8_t> u = ternary_hw(s.seed, ST_ENC_U(enc), N, s.h);
+  DevArray<int8_t> du(N); upload(du.p, u.data(), N);
+  RowMap rm{nr, l + 1, 0, s.L, 0, 0};
+  DU64 uq((size_t)nr * N), pk((size_t)2 * nr * N), tt((size_t)2 * nr * N);
+  launch_signed_rows(uq.p, rm, du.p, s.d_mods.p, N, s.st);
+  ntt(uq.p, 0, 1, rm, true);
+  for (int p = 0; p < 2; p++) {
+    d2d(pk.p + (size_t)p * nr * N, s.pkR.p + (size_t)p * nm * N, (size_t)(l + 1) * N * 8);
+    d2d(pk.p + (size_t)p * nr * N + (size_t)(l + 1) * N, s.pkR.p + (size_t)p * nm * N + (size_t)s.L * N, (size_t)N * 8);
+  }
+  launch_mont_mul(tt.p, (size_t)nr * N, uq.p, 0, pk.p, (size_t)nr * N, 2, rm, s.d_mods.p, N, false, s.st);
+  ntt(tt.p, (size_t)nr * N, 2, rm, false);
+  launch_sample_cbd(tt.p, rm, s.seed, ST_ENC_E0(enc), s.d_mods.p, N, true, s.st);
+  launch_sample_cbd(tt.p + (size_t)nr * N, rm, s.seed, ST_ENC_E1(enc), s.d_mods.p, N, true, s.st);
+  // ModDown from Q + {p_0} in the coefficient domain
+  DU64 ext((size_t)2 * (l + 1) * N);
+  BConvHost& bt = bconv_table(s.L, s.L + 1);
+  RowList rl{}; rl.n = l + 1;
+  for (int i = 0; i <= l; i++) { rl.row[i] = (short)i; rl.mod[i] = (short)i; }
+  launch_bconv(tt.p + (size_t)(l + 1) * N, (size_t)nr * N, 1, bt.tab, ext.p, (size_t)(l + 1) * N, 2, rl, s.d_mods.p, N, false, s.st);
+  auto out = new_ct(l, pt.scale); out->logslots = pt.logslots;
+  launch_moddown_combine(out->d.p, (size_t)(l + 1) * N, tt.p, (size_t)nr * N, ext.p, (size_t)(l + 1) * N, nullptr, 0, 0, nullptr,
+                         s.p0inv_w.p, s.p0inv_wp.p, l + 1, 2, s.d_mods.p, N, s.st);
+  ntt(out->d.p, (size_t)(l + 1) * N, 2, rows_q(l), true);
+  launch_add(out->d.p, out->d.p, pt.d.p, 0, 1, rows_q(l), s.d_mods.p, N, false, s.st);
+  sync();
+  return out;
+}
+std::unique_ptr<Plain> decrypt_ct(const Cipher& ct) {
+  Scheme& s = sch();
+  REQUIRE(s.has_sk, "secret key not generated");
+  const int l = ct.level, N = s.N;
+  auto p = std::make_unique<Plain>();
+  p->level = l; p->scale = ct.scale; p->logslots = ct.logslots;
+  p->d = DU64((size_t)(l + 1) * N);
+  d2d(p->d.p, ct.d.p, (size_t)(l + 1) * N * 8);
+  launch_mont_mul(p->d.p, 0, ct.d.p + (size_t)(l + 1) * N, 0, s.sR.p, 0, 1, rows_q(l), s.d_mods.p, N, true, s.st);
+  sync();
+  return p;
+}
+
+std::unique_ptr<Plain> encode_values(const double* v, int n, int level, double scale) {
+  Scheme& s = sch();
+  REQUIRE(level >= 0 && level < s.L, "invalid level");
+  REQUIRE(n <= s.N / 2, "too many values for the slot count");
+  auto p = std::make_unique<Plain>();
+  p->level = level; p->scale = scale; p->logslots = s.logN - 1;
+  p->d = DU64((size_t)(level + 1) * s.N);
+  std::vector<u64> rec;
+  encode_records(s, v, n, scale, rec);
+  encode_to_device(rec, rows_q(level), p->d.p);
+  return p;
+}
+std::vector<double> decode_pt(const Plain& p) {
+  Scheme& s = sch();
+  const int N = s.N, l = p.level;
+  DU64 tmp((size_t)(l + 1) * N);
+  d2d(tmp.p, p.d.p, tmp.bytes());
+  ntt(tmp.p, 0, 1, rows_q(l), false);
+  std::vector<u64> coef((size_t)(l + 1) * N);
+  download(coef.data(), tmp.p, coef.size());
+  return decode_host(coef, l, p.scale);
+}
+
+template <class T> T* c_array(const std::vector<T>& v) {
+  T* p = (T*)std::malloc(std::max<size_t>(1, v.size()) * sizeof(T));
+  if (!p) throw Error("out of host memory");
+  if (!v.empty()) std::memcpy(p, v.data(), v.size() * sizeof(T));
+  return p;
+}
+unsigned long scale_to_ulong(double sc) { if (!(sc < 18446744073709551616.0)) return ~0UL; return sc < 0 ? 0UL : (unsigned long)sc; }
+
+}  // namespace
+
+// ============================================================================
+// C ABI
+// ============================================================================
+extern "C" {
+
+const char* GetLastError(void) { return g_err.c_str(); }
+void SetSchemeSeed(uint64_t seed) { g_seed_override = seed; g_seed_set = true; }
+
+int NewScheme(int logN, int* logQ, int lenQ, int* logP, int lenP, int logScale, int h, const char* ringType,
+              const char* keysPath, const char* ioMode) {
+  return guard([&] {
+    (void)keysPath; (void)ioMode;
+    REQUIRE(ringType && std::string(ringType) == "standard", "only the standard ring is supported by the hip backend");
+    std::vector<int> lq(logQ, logQ + lenQ), lp(logP, logP + lenP);
+    std::vector<u64> q, p;
+    gen_primes(logN, lq, lp, q, p);
+    u64 seed = g_seed_override;
+    if (!g_seed_set) { FILE* f = std::fopen("/dev/urandom", "rb"); if (f) { if (std::fread(&seed, 8, 1, f) != 1) seed = 0; std::fclose(f); } }
+    build_scheme(logN, q, p, logScale, h, seed);
+    return 0;
+  });
+}
+int NewSchemeWithModuli(int logN, const uint64_t* q, int lenQ, const uint64_t* p, int lenP, int logScale, int h, uint64_t seed) {
+  return guard([&] {
+    build_scheme(logN, std::vector<u64>(q, q + lenQ), std::vector<u64>(p, p + lenP), logScale, h, seed);
+    return 0;
+  });
+}
+int DeleteScheme(void) {
+  return guard([&] {
+    if (S) { (void)hipStreamSynchronize(S->st); (void)hipStreamDestroy(S->st); delete S; S = nullptr; }
+    if (g_pool) g_pool->release_all();
+    return 0;
+  });
+}
+int GeneratePrimes(int logN, const int* logQ, int lenQ, const int* logP, int lenP, uint64_t* q, uint64_t* p) {
+  return guard([&] {
+    std::vector<u64> qq, pp;
+    gen_primes(logN, std::vector<int>(logQ, logQ + lenQ), std::vector<int>(logP, logP + lenP), qq, pp);
+    std::copy(qq.begin(), qq.end(), q); std::copy(pp.begin(), pp.end(), p);
+    return 0;
+  });
+}
+
+// ---- keys ----
+int NewKeyGenerator(void) { return guard([&] { sch(); return 0; }); }
+int GenerateSecretKey(void) { return guard([&] { gen_secret(); return 0; }); }
+int GeneratePublicKey(void) { return guard([&] { gen_public(); return 0; }); }
+int GenerateRelinearizationKey(void) { return guard([&] { sch(); return 0; }); }
+int GenerateEvaluationKeys(void) { return guard([&] { sch(); return 0; }); }
+
+// ---- encoder ----
+int NewEncoder(void) { return guard([&] { sch().encoder = true; return 0; }); }
+int Encode(const float* values, int lenValues, int level, unsigned long scale) {
+  return guard([&] {
+    std::vector<double> v(values, values + lenValues);
+    return push_pt(encode_values(v.data(), lenValues, level, (double)scale));
+  });
+}
+ArrayResultFloat Decode(int plaintextID) {
+  ArrayResultFloat r{nullptr, 0};
+  guard([&] {
+    std::vector<double> v = decode_pt(get_pt(plaintextID));
+    std::vector<float> f(v.begin(), v.end());
+    r.Data = c_array(f); r.Length = f.size();
+    return 0;
+  });
+  return r;
+}
+int DecodeDouble(int plaintextID, double* out, int len) {
+  return guard([&] {
+    std::vector<double> v = decode_pt(get_pt(plaintextID));
+    REQUIRE(len >= (int)v.size(), "output buffer too small");
+    std::copy(v.begin(), v.end(), out);
+    return (int)v.size();
+  });
+}
+
+// ---- encryptor ----
+int NewEncryptor(void) { return guard([&] { sch().encryptor = true; return 0; }); }
+int NewDecryptor(void) { return guard([&] { sch().decryptor = true; return 0; }); }
+int Encrypt(int plaintextID) { return guard([&] { return push_ct(encrypt_pt(get_pt(plaintextID))); }); }
+int Decrypt(int ciphertextID) { return guard([&] { return push_pt(decrypt_ct(get_ct(ciphertextID))); }); }
+int SetEncryptionCounter(uint64_t v) { return guard([&] { sch().enc_counter = v; return 0; }); }
+
+// ---- evaluator ----
+int AddRotationKey(int rotation) {
+  return guard([&] { u64 ge = galois_element(rotation); ensure_galois_key(ge); sch().rot_keys.insert(ge); return 0; });
+}
+int NewEvaluator(void) {
+  return guard([&] {
+    Scheme& s = sch();
+    s.evaluator = true;
+    for (int i = 1; i < s.N / 2; i *= 2) { u64 ge = galois_element(i); ensure_galois_key(ge); s.rot_keys.insert(ge); }
+    u64 conj = 2 * (u64)s.N - 1;
+    ensure_galois_key(conj); s.rot_keys.insert(conj);
+    return 0;
+  });
+}
+int Rotate(int ctID, int amount) {
+  return guard([&] {
+    AddRotationKey(amount);
+    Cipher& c = get_ct(ctID);
+    auto r = automorphism(c, galois_element(amount), false);
+    c.d = std::move(r->d);
+    return ctID;
+  });
+}
+int RotateNew(int ctID, int amount) {
+  return guard([&] {
+    u64 ge = galois_element(amount); ensure_galois_key(ge); sch().rot_keys.insert(ge);
+    return push_ct(automorphism(get_ct(ctID), ge, false));
+  });
+}
+int Conjugate(int ctID) {
+  return guard([&] { Scheme& s = sch(); u64 ge = 2 * (u64)s.N - 1; ensure_galois_key(ge); s.rot_keys.insert(ge);
+    Cipher& c = get_ct(ctID); auto r = automorphism(c, ge, false); c.d = std::move(r->d); return ctID; });
+}
+int ConjugateNew(int ctID) {
+  return guard([&] { Scheme& s = sch(); u64 ge = 2 * (u64)s.N - 1; ensure_galois_key(ge); s.rot_keys.insert(ge);
+    return push_ct(automorphism(get_ct(ctID), ge, false)); });
+}
+int Rescale(int ctID) {
+  return guard([&] { Cipher& c = get_ct(ctID); auto r = rescale_lattigo(c); c = std::move(*r); return ctID; });
+}
+// As the reference wrapper (evaluator.go RescaleNew): rescales the input in place, returns a copy.
+int RescaleNew(int ctID) {
+  return guard([&] { Cipher& c = get_ct(ctID); auto r = rescale_lattigo(c); c = std::move(*r); return push_ct(copy_ct(c)); });
+}
+int AddCiphertext(int a, int b) { return guard([&] { add_inplace(get_ct(a), get_ct(b), false); return a; }); }
+int AddCiphertextNew(int a, int b) { return guard([&] { auto c = copy_ct(get_ct(a)); add_inplace(*c, get_ct(b), false); return push_ct(std::move(c)); }); }
+int SubCiphertext(int a, int b) { return guard([&] { add_inplace(get_ct(a), get_ct(b), true); return a; }); }
+int SubCiphertextNew(int a, int b) { return guard([&] { auto c = copy_ct(get_ct(a)); add_inplace(*c, get_ct(b), true); return push_ct(std::move(c)); }); }
+int AddPlaintext(int ct, int pt) { return guard([&] { add_plain_inplace(get_ct(ct), get_pt(pt), false); return ct; }); }
+int AddPlaintextNew(int ct, int pt) { return guard([&] { auto c = copy_ct(get_ct(ct)); add_plain_inplace(*c, get_pt(pt), false); return push_ct(std::move(c)); }); }
+int SubPlaintext(int ct, int pt) { return guard([&] { add_plain_inplace(get_ct(ct), get_pt(pt), true); return ct; }); }
+int SubPlaintextNew(int ct, int pt) { return guard([&] { auto c = copy_ct(get_ct(ct)); add_plain_inplace(*c, get_pt(pt), true); return push_ct(std::move(c)); }); }
+
+// ---- linear transforms ----
+int NewLinearTransformEvaluator(void) { return guard([&] { sch().lteval = true; return 0; }); }
+int GenerateLinearTransform(const int* diagIdxs, int diagIdxsLen, const float* diagData, int diagDataLen, int level,
+                            float bsgsRatio, const char* ioMode) {
+  return guard([&] {
+    REQUIRE(!ioMode || std::string(ioMode) == "none", "only io_mode 'none' is supported by the hip backend");
+    return generate_lt(diagIdxs, diagIdxsLen, diagData, diagDataLen, level, bsgsRatio);
+  });
+}
+int EvaluateLinearTransform(int transformID, int ctxtID) {
+  return guard([&] {
+    LinTrans& t = get_lt(transformID);
+    Cipher& c = get_ct(ctxtID);
+    auto out = t.naive ? eval_lt_naive(t, c) : eval_lt_bsgs(t, c);
+    return push_ct(std::move(out));
+  });
+}
+ArrayResultInt GetLinearTransformRotationKeys(int transformID) {
+  ArrayResultInt r{nullptr, 0};
+  guard([&] {
+    std::vector<int> ge;
+    for (int k : lt_rotations(get_lt(transformID))) ge.push_back((int)galois_element(k));
+    r.Data = c_array(ge); r.Length = ge.size();
+    return 0;
+  });
+  return r;
+}
+int GenerateLinearTransformRotationKey(int galEl) {
+  return guard([&] { ensure_galois_key((u64)(unsigned)galEl); sch().lt_keys.insert((u64)(unsigned)galEl); return 0; });
+}
+int DeleteLinearTransform(int id) {
+  return guard([&] { Scheme& s = sch(); sync(); if (s.lts.erase(id)) s.lt_ids.give(id); return 0; });
+}
+int RemoveRotationKeys(void) { return guard([&] { sch().lt_keys.clear(); return 0; }); }
+
+// ---- tensors ----
+int DeletePlaintext(int id) { return guard([&] { Scheme& s = sch(); sync(); if (s.pts.erase(id)) s.pt_ids.give(id); return 0; }); }
+int DeleteCiphertext(int id) { return guard([&] { Scheme& s = sch(); sync(); if (s.cts.erase(id)) s.ct_ids.give(id); return 0; }); }
+unsigned long GetPlaintextScale(int id) { unsigned long v = 0; guard([&] { v = scale_to_ulong(get_pt(id).scale); return 0; }); return v; }
+unsigned long GetCiphertextScale(int id) { unsigned long v = 0; guard([&] { v = scale_to_ulong(get_ct(id).scale); return 0; }); return v; }
+double GetCiphertextScaleDouble(int id) { double v = -1; guard([&] { v = get_ct(id).scale; return 0; }); return v; }
+double GetPlaintextScaleDouble(int id) { double v = -1; guard([&] { v = get_pt(id).scale; return 0; }); return v; }
+int SetPlaintextScale(int id, unsigned long scale) { return guard([&] { get_pt(id).scale = (double)scale; return 0; }); }
+int SetCiphertextScale(int id, unsigned long scale) { return guard([&] { get_ct(id).scale = (double)scale; return 0; }); }
+int GetPlaintextLevel(int id) { return guard([&] { return get_pt(id).level; }); }
+int GetCiphertextLevel(int id) { return guard([&] { return get_ct(id).level; }); }
+int GetPlaintextSlots(int id) { return guard([&] { return 1 << get_pt(id).logslots; }); }
+int GetCiphertextSlots(int id) { return guard([&] { return 1 << get_ct(id).logslots; }); }
+int GetCiphertextDegree(int id) { return guard([&] { get_ct(id); return 1; }); }
+ArrayResultUInt64 GetModuliChain(void) {
+  ArrayResultUInt64 r{nullptr, 0};
+  guard([&] { Scheme& s = sch(); std::vector<u64> v(s.mod.begin(), s.mod.begin() + s.L); r.Data = (unsigned long long*)c_array(v); r.Length = v.size(); return 0; });
+  return r;
+}
+ArrayResultUInt64 GetAuxModuliChain(void) {
+  ArrayResultUInt64 r{nullptr, 0};
+  guard([&] { Scheme& s = sch(); std::vector<u64> v(s.mod.begin() + s.L, s.mod.end()); r.Data = (unsigned long long*)c_array(v); r.Length = v.size(); return 0; });
+  return r;
+}
+ArrayResultInt GetLivePlaintexts(void) {
+  ArrayResultInt r{nullptr, 0};
+  guard([&] { std::vector<int> v; for (auto& kv : sch().pts) v.push_back(kv.first); r.Data = c_array(v); r.Length = v.size(); return 0; });
+  return r;
+}
+ArrayResultInt GetLiveCiphertexts(void) {
+  ArrayResultInt r{nullptr, 0};
+  guard([&] { std::vector<int> v; for (auto& kv : sch().cts) v.push_back(kv.first); r.Data = c_array(v); r.Length = v.size(); return 0; });
+  return r;
+}
+void FreeCArray(void* ptr) { std::free(ptr); }
+
+// ---- raw residue import/export (parity and measurement) ----
+int ExportCiphertext(int id, uint64_t* buf, size_t len, int coeff) {
+  return guard([&] {
+    Scheme& s = sch(); Cipher& c = get_ct(id);
+    size_t n = (size_t)2 * (c.level + 1) * s.N;
+    REQUIRE(len >= n, "buffer too small");
+    DU64 t(n); d2d(t.p, c.d.p, n * 8);
+    if (coeff) ntt(t.p, (size_t)(c.level + 1) * s.N, 2, rows_q(c.level), false);
+    download(buf, t.p, n);
+    return (int)(n / s.N);
+  });
+}
+int ImportCiphertext(const uint64_t* buf, int level, double scale, int coeff) {
+  return guard([&] {
+    Scheme& s = sch();
+    REQUIRE(level >= 0 && level < s.L, "invalid level");
+    auto c = new_ct(level, scale);
+    upload(c->d.p, buf, c->d.n);
+    if (coeff) ntt(c->d.p, (size_t)(level + 1) * s.N, 2, rows_q(level), true);
+    sync();
+    return push_ct(std::move(c));
+  });
+}
+int ExportPlaintext(int id, uint64_t* buf, size_t len, int coeff) {
+  return guard([&] {
+    Scheme& s = sch(); Plain& p = get_pt(id);
+    size_t n = (size_t)(p.level + 1) * s.N;
+    REQUIRE(len >= n, "buffer too small");
+    DU64 t(n); d2d(t.p, p.d.p, n * 8);
+    if (coeff) ntt(t.p, 0, 1, rows_q(p.level), false);
+    download(buf, t.p, n);
+    return (int)(n / s.N);
+  });
+}
+int ImportPlaintext(const uint64_t* buf, int level, double scale, int coeff) {
+  return guard([&] {
+    Scheme& s = sch();
+    REQUIRE(level >= 0 && level < s.L, "invalid level");
+    auto p = std::make_unique<Plain>();
+    p->level = level; p->scale = scale; p->logslots = s.logN - 1; p->d = DU64((size_t)(level + 1) * s.N);
+    upload(p->d.p, buf, p->d.n);
+    if (coeff) ntt(p->d.p, 0, 1, rows_q(level), true);
+    sync();
+    return push_pt(std::move(p));
+  });
+}
+int ExportGaloisKey(uint64_t galel, uint64_t* buf, size_t len) {
+  return guard([&] {
+    Scheme& s = sch();
+    ensure_galois_key(galel);
+    const DU64& k = *s.gkeys.at(galel);
+    REQUIRE(len >= k.n, "buffer too small");
+    DU64 t(k.n); d2d(t.p, k.p, k.bytes());
+    launch_mont_convert(t.p, (size_t)(s.L + s.K) * s.N, 2 * s.dnum, rows_all(), s.d_mods.p, s.N, false, s.st);
+    download(buf, t.p, k.n);
+    return 0;
+  });
+}
+int ExportSecretKey(int64_t* buf, size_t len) {
+  return guard([&] { Scheme& s = sch(); REQUIRE(s.has_sk && len >= (size_t)s.N, "no secret key / buffer too small");
+    for (int i = 0; i < s.N; i++) buf[i] = s.s[i]; return 0; });
+}
+int ExportLinearTransformDiagonal(int ltID, int diag, uint64_t* buf, size_t len) {
+  return guard([&] {
+    Scheme& s = sch(); LinTrans& t = get_lt(ltID);
+    auto it = std::find(t.plain_idx.begin(), t.plain_idx.end(), diag);
+    REQUIRE(it != t.plain_idx.end(), "diagonal not stored");
+    size_t p = it - t.plain_idx.begin(), n = (size_t)(t.level + 1 + s.K) * s.N;
+    REQUIRE(len >= n, "buffer too small");
+    DU64 tmp(n); d2d(tmp.p, t.diags.p + p * n, n * 8);
+    launch_mont_convert(tmp.p, 0, 1, RowMap{t.level + 1 + s.K, t.level + 1, 0, s.L, 0, 0}, s.d_mods.p, s.N, false, s.st);
+    download(buf, tmp.p, n);
+    return (int)(n / s.N);
+  });
+}
+int GetLinearTransformInfo(int ltID, int* out, int len) {
+  return guard([&] {
+    LinTrans& t = get_lt(ltID);
+    REQUIRE(len >= 4, "buffer too small");
+    out[0] = t.N1; out[1] = (int)t.giant.size(); out[2] = (int)t.rot2.size(); out[3] = (int)t.plain_idx.size();
+    return 0;
+  });
+}
+
+int GetSchemeInfo(int* out, int len) {
+  return guard([&] {
+    Scheme& s = sch();
+    REQUIRE(len >= 6, "buffer too small");
+    out[0] = s.logN; out[1] = s.L; out[2] = s.K; out[3] = s.dnum; out[4] = s.logscale; out[5] = s.h;
+    return 0;
+  });
+}
+
+// ---- stream / timing ----
+int Synchronize(void) { return guard([&] { sync(); return 0; }); }
+void* GetStream(void) { return S ? (void*)S->st : nullptr; }
+int KernelTimingEnable(int on) { return guard([&] { Scheme& s = sch(); sync(); timing_collect(); s.timing.acc.clear(); s.timing.on = on != 0; return 0; }); }
+int KernelTimingGet(const char* name, long* count, double* total_ms) {
+  return guard([&] {
+    Scheme& s = sch(); sync(); timing_collect();
+    auto it = s.timing.acc.find(name);
+    *count = it == s.timing.acc.end() ? 0 : it->second.first;
+    *total_ms = it == s.timing.acc.end() ? 0.0 : it->second.second;
+    return 0;
+  });
+}
+int GetMemoryStats(uint64_t* live, uint64_t* cached, uint64_t* peak) {
+  return guard([&] { REQUIRE(g_pool, "no device pool"); *live = g_pool->live; *cached = g_pool->cached; *peak = g_pool->peak; return 0; });
+}
+
+}  // extern "C"

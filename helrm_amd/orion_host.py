@@ -1,0 +1,355 @@
+"""Host-side callers of the embedding PCMM, restated from the reference so the
+path runs end to end without the reference tree:
+
+  * HE-LRM selector / plaintext lookup   examples/criteo/dlrm.py:66-124,202-247
+  * hybrid diagonal extraction           orion/core/packing.py:510-529,626-865
+  * encode padding                        orion/backend/python/encoder.py:14-107
+  * transform generation + rotation keys  orion/backend/python/lt_evaluator.py:29-57,132-160
+  * block loop + rescale                  orion/backend/python/lt_evaluator.py:224-275
+  * output fold + bias                    orion/nn/linear.py:99-140,191-209
+  * CipherTensor roll / add               orion/backend/python/tensors.py:154-186,256-262
+
+Everything here is host bookkeeping; all ciphertext arithmetic goes through
+the backend object (a HipLibrary, or any object with the Lattigo method set).
+"""
+import math
+
+import numpy as np
+
+# --------------------------------------------------------------------------
+# parameters (orion/backend/python/parameters.py:168-358, the getters used)
+# --------------------------------------------------------------------------
+
+
+class Params:
+    def __init__(self, logn, logq, logp, logscale=None, h=192, ringtype="standard",
+                 embedding_method="hybrid", io_mode="none", seed=None):
+        self.logn, self.logq, self.logp = int(logn), list(logq), list(logp)
+        self.logscale = int(logscale or self.logq[-1])
+        self.h, self.ringtype = int(h), ringtype.lower()
+        self.embedding_method, self.io_mode, self.seed = embedding_method, io_mode, seed
+
+    @classmethod
+    def from_config(cls, cfg, seed=None):
+        ck = {k.lower(): v for k, v in cfg.get("ckks_params", {}).items()}
+        on = {k.lower(): v for k, v in cfg.get("orion", {}).items()}
+        return cls(ck["logn"], ck["logq"], ck["logp"], ck.get("logscale"), ck.get("h", 192),
+                   ck.get("ringtype", "standard"), on.get("embedding_method", "hybrid"),
+                   on.get("io_mode", "none"), seed)
+
+    def get_logn(self): return self.logn
+    def get_logq(self): return self.logq
+    def get_logp(self): return self.logp
+    def get_logscale(self): return self.logscale
+    def get_default_scale(self): return 1 << self.logscale
+    def get_hamming_weight(self): return self.h
+    def get_ringtype(self): return self.ringtype
+    def get_max_level(self): return len(self.logq) - 1
+    def get_slots(self): return 1 << (self.logn - 1)
+    def get_embedding_method(self): return self.embedding_method
+    def get_io_mode(self): return self.io_mode
+    def get_keys_path(self): return ""
+    def get_diags_path(self): return ""
+    def get_seed(self): return self.seed
+
+
+# --------------------------------------------------------------------------
+# HE-LRM selector and plaintext reference (examples/criteo/dlrm.py)
+# --------------------------------------------------------------------------
+
+def digits(index, base, width):
+    """dlrm.py:66-72: little-endian base-`base` digits of `index`."""
+    index = np.asarray(index, dtype=np.int64)
+    out = []
+    for _ in range(width):
+        out.append(np.remainder(index, base))
+        index = np.floor_divide(index, base)
+    return np.stack(out)
+
+
+def radix_width(categories, base):
+    """dlrm.py:75-76"""
+    return math.ceil(math.log(categories, base))
+
+
+def expanded_width(categories, compress_threshold, base):
+    """dlrm.py:79-82"""
+    if categories > compress_threshold:
+        return base * radix_width(categories, base)
+    return categories
+
+
+def expanded_id(index, size, compress_threshold, base):
+    """dlrm.py:202-213: one-hot of each digit (digit 0 first), or a plain one-hot."""
+    if size <= compress_threshold:
+        out = np.zeros(size, dtype=np.float32)
+        out[index] = 1.0
+        return out
+    pieces = []
+    for d in digits(index, base, radix_width(size, base)):
+        piece = np.zeros(base, dtype=np.float32)
+        piece[int(d)] = 1.0
+        pieces.append(piece)
+    return np.concatenate(pieces)
+
+
+def expanded_sparse(indices, sizes, compress_threshold, base):
+    """dlrm.py:215-221: concatenation of the fields' selectors."""
+    return np.concatenate([expanded_id(int(i), s, compress_threshold, base) for i, s in zip(indices, sizes)])
+
+
+def radix_lookup(tables, index, base):
+    """RadixTable.forward (dlrm.py:111-119): sum of the digit rows (fp32)."""
+    width = len(tables)
+    out = np.zeros(tables[0].shape[1], dtype=np.float32)
+    for t, d in zip(tables, digits(index, base, width)):
+        out = out + t[int(d)]
+    return out
+
+
+def block_diag_matrix(field_tables):
+    """export (dlrm.py:241-247): block_diag(W_0..W_F).T with W_f = cat of the
+    field's digit tables; rows = outputs, columns = selector positions."""
+    blocks = [np.concatenate(t, axis=0) for t in field_tables]  # (width*base) x dim
+    rows = sum(b.shape[1] for b in blocks)
+    cols = sum(b.shape[0] for b in blocks)
+    M = np.zeros((rows, cols), dtype=np.float32)
+    r = c = 0
+    for b in blocks:
+        M[r:r + b.shape[1], c:c + b.shape[0]] = b.T
+        r += b.shape[1]
+        c += b.shape[0]
+    return M
+
+
+# --------------------------------------------------------------------------
+# hybrid diagonal extraction (orion/core/packing.py:626-865, uniform path)
+# --------------------------------------------------------------------------
+
+def diagonalize(matrix, num_slots, embed_method="hybrid", is_last_layer=False):
+    """Generalised diagonals per (num_slots x num_slots) block.
+
+    Returns ({(row, col): {diag_index: float32 values}}, output_rotations).
+    Hybrid (one block row, not the last layer): block_height = 2^ceil(log2 H),
+    diagonal i holds M[row0 + (j mod bh), col0 + (i + j) mod slots], zero
+    diagonals dropped (a block with none keeps diagonal 0 of zeros) and the
+    output needs log2(slots / bh) fold rotations.
+    """
+    M = np.asarray(matrix, dtype=np.float32)
+    H, W = M.shape
+    nbr = math.ceil(H / num_slots)
+    nbc = math.ceil(W / num_slots)
+    if nbr == 1 and embed_method == "hybrid" and not is_last_layer:
+        block_height = 2 ** math.ceil(math.log2(H))
+        output_rotations = int(math.log2(num_slots // block_height))
+    else:
+        block_height = num_slots
+        output_rotations = 0
+    padded = np.zeros((nbr * block_height, nbc * num_slots), dtype=np.float32)
+    padded[:H, :W] = M
+    j = np.arange(num_slots)
+    row_idx = np.tile(np.arange(block_height), num_slots // block_height)
+    out = {}
+    for br in range(nbr):
+        for bc in range(nbc):
+            block = padded[br * num_slots: br * num_slots + block_height, bc * num_slots:(bc + 1) * num_slots]
+            diags = {}
+            for i in range(block_height):
+                col_idx = (i + j) % num_slots
+                d = block[row_idx, col_idx]
+                if np.any(d):
+                    diags[i] = d.astype(np.float32)
+            out[(br, bc)] = diags or {0: np.zeros(num_slots, dtype=np.float32)}
+    return out, output_rotations
+
+
+# --------------------------------------------------------------------------
+# scheme, tensors and the linear layer
+# --------------------------------------------------------------------------
+
+class Scheme:
+    """Minimal counterpart of orion.core.orion.Scheme for this path: creates
+    the backend, keys, encoder/encryptor/evaluator (init_scheme order,
+    orion/core/orion.py:66-126 and orion/backend/python/*)."""
+
+    def __init__(self, params, backend):
+        self.params = params
+        self.backend = backend
+        backend.setup_bindings(params)
+        backend.NewKeyGenerator()
+        backend.GenerateSecretKey()
+        backend.GeneratePublicKey()
+        backend.GenerateRelinearizationKey()
+        backend.GenerateEvaluationKeys()
+        backend.NewEncoder()
+        backend.NewEncryptor()
+        backend.NewDecryptor()
+        backend.NewEvaluator()
+        backend.NewLinearTransformEvaluator()
+        self.saved_rotation_keys = set()
+
+    # orion/backend/python/encoder.py:14-88 (real values, default path)
+    def encode(self, values, level=None, scale=None):
+        values = np.asarray(values, dtype=np.float64).reshape(-1)
+        if level is None:
+            level = self.params.get_max_level()
+        if not scale:
+            scale = self.params.get_default_scale()
+        slots = self.params.get_slots()
+        pad = (-len(values)) % slots
+        vec = np.concatenate([values, np.zeros(pad)]) if pad or len(values) == 0 else values
+        if len(vec) == 0:
+            vec = np.zeros(slots)
+        ids = [self.backend.Encode(vec[i * slots:(i + 1) * slots].tolist(), level, int(scale))
+               for i in range(len(vec) // slots)]
+        return PlainTensor(self, ids, len(values))
+
+    def decode(self, pt):
+        vals = []
+        for i in pt.ids:
+            vals.extend(self.backend.Decode(i))
+        return np.asarray(vals[: pt.n], dtype=np.float64)
+
+    def encrypt(self, pt):
+        return CipherTensor(self, [self.backend.Encrypt(i) for i in pt.ids], pt.n)
+
+    def decrypt(self, ct):
+        return PlainTensor(self, [self.backend.Decrypt(i) for i in ct.ids], ct.n)
+
+    def moduli(self):
+        return self.backend.GetModuliChain()
+
+
+class PlainTensor:
+    def __init__(self, scheme, ids, n):
+        self.scheme, self.ids, self.n = scheme, list(ids), n
+
+
+class CipherTensor:
+    """tensors.py:154-186 (add), 256-262 (roll)."""
+
+    def __init__(self, scheme, ids, n):
+        self.scheme, self.ids, self.n = scheme, list(ids), n
+
+    def add(self, other, in_place=False):
+        b = self.scheme.backend
+        out = []
+        for i, cid in enumerate(self.ids):
+            if isinstance(other, PlainTensor):
+                f = b.AddPlaintext if in_place else b.AddPlaintextNew
+            else:
+                f = b.AddCiphertext if in_place else b.AddCiphertextNew
+            out.append(f(cid, other.ids[i]))
+        if in_place:
+            return self
+        return CipherTensor(self.scheme, out, self.n)
+
+    def __add__(self, other):
+        return self.add(other, False)
+
+    def __iadd__(self, other):
+        return self.add(other, True)
+
+    def roll(self, amount, in_place=False):
+        b = self.scheme.backend
+        f = b.Rotate if in_place else b.RotateNew
+        return CipherTensor(self.scheme, [f(c, int(amount)) for c in self.ids], self.n)
+
+    def free(self):
+        for c in self.ids:
+            self.scheme.backend.DeleteCiphertext(c)
+        self.ids = []
+
+
+class LinearLayer:
+    """Linear / Embedding (orion/nn/linear.py:143-225, orion/nn/embedding.py:12-21)
+    compiled at `level` with the hybrid packing; bias zeros for Embedding."""
+
+    def __init__(self, scheme, weight, bias=None, level=None, bsgs_ratio=2.0, last=False):
+        self.scheme = scheme
+        self.weight = np.asarray(weight, dtype=np.float32)
+        self.out_features = self.weight.shape[0]
+        self.bias = np.zeros(self.out_features, dtype=np.float32) if bias is None else np.asarray(bias, np.float32)
+        self.level = scheme.params.get_max_level() if level is None else level
+        self.depth = 1
+        self.bsgs_ratio = float(bsgs_ratio)
+        self.last = last
+        self.transform_ids = {}
+
+    def compile(self):
+        p = self.scheme.params
+        slots = p.get_slots()
+        self.diagonals, self.output_rotations = diagonalize(self.weight, slots, p.get_embedding_method(), self.last)
+        # linear.py:191-209: bias encoded at level - depth, then the transforms
+        self.on_bias_ptxt = self.scheme.encode(self.bias, self.level - self.depth)
+        self.transform_ids = self.generate_transforms()
+        return self
+
+    # lt_evaluator.py:29-57
+    def generate_transforms(self):
+        b = self.scheme.backend
+        ids = {}
+        for (row, col), diags in self.diagonals.items():
+            idxs = list(diags.keys())
+            data = np.concatenate([diags[i] for i in idxs]).astype(np.float32)
+            tid = b.GenerateLinearTransform(idxs, data, self.level, self.bsgs_ratio, "none")
+            ids[(row, col)] = tid
+            self.generate_rotation_keys(tid)
+        return ids
+
+    # lt_evaluator.py:132-146
+    def generate_rotation_keys(self, tid):
+        b = self.scheme.backend
+        keys = b.GetLinearTransformRotationKeys(tid)
+        new = set(keys).difference(self.scheme.saved_rotation_keys)
+        self.scheme.saved_rotation_keys.update(new)
+        for k in new:
+            b.GenerateLinearTransformRotationKey(k)
+
+    # lt_evaluator.py:224-275 (uniform path)
+    def evaluate_lt(self, x):
+        b = self.scheme.backend
+        tids = np.array(list(self.transform_ids.values()))
+        cols = len(x.ids)
+        rows = len(tids) // cols
+        tids = tids.reshape(rows, cols)
+        cts_out = []
+        for i in range(rows):
+            ct_out = None
+            for j in range(cols):
+                res = CipherTensor(self.scheme, [b.EvaluateLinearTransform(int(tids[i][j]), x.ids[j])], x.n)
+                if ct_out is None:
+                    ct_out = res
+                else:
+                    ct_out = ct_out + res
+                    res.free()
+            if getattr(b, "lt_output_prerescaled", False):
+                cts_out.append(ct_out.ids[0])
+            else:
+                cts_out.append(b.RescaleNew(ct_out.ids[0]))
+                ct_out.free()
+        return CipherTensor(self.scheme, cts_out, self.out_features)
+
+    # linear.py:99-140 (no slicing, no fold-retag on the Lattigo path)
+    def forward(self, x):
+        out = self.evaluate_lt(x)
+        slots = self.scheme.params.get_slots()
+        for i in range(1, self.output_rotations + 1):
+            rolled = out.roll(slots // (2 ** i))
+            out += rolled
+            rolled.free()
+        out += self.on_bias_ptxt
+        return out
+
+    def free(self):
+        for t in self.transform_ids.values():
+            self.scheme.backend.DeleteLinearTransform(int(t))
+        self.transform_ids = {}
+
+
+def embedding_pcmm(scheme, layer, selector):
+    """One query: encode + encrypt the selector at the layer's level and run
+    the embedding PCMM (HELRM.sparse, dlrm.py:226-230).  Returns (ct, pt_in)."""
+    pt = scheme.encode(selector, layer.level)
+    ct = scheme.encrypt(pt)
+    return layer.forward(ct), ct

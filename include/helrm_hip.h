@@ -1,0 +1,144 @@
+/*
+ * helrm_hip.h -- C ABI of the MI355X (gfx950) CKKS backend for the HE-LRM
+ * embedding PCMM (libhelrm_hip.so, built from helrm_amd/csrc/).
+ *
+ * The entry points keep the names, argument meaning, handle semantics and
+ * return conventions of the cgo exports of Orion's Lattigo backend
+ * (reference: the Go files of orion/backend/lattigo, bound by ctypes in
+ * orion/backend/lattigo/bindings.py), so a ctypes binding written for that
+ * library binds this one.  Differences, all deliberate:
+ *   - functions that return void in the Lattigo library return int here:
+ *     0 on success, -1 on failure; handle-returning functions return -1 on
+ *     failure.  The message is available from GetLastError().  (Lattigo
+ *     panics and aborts the process instead.)
+ *   - array results use the same {Data, Length} structs, malloc'ed by the
+ *     library and released with FreeCArray.
+ * Entry points marked [ext] have no counterpart in the reference; they exist
+ * for parity checks (explicit moduli, seeds and raw residues) and for
+ * measurement.
+ */
+#ifndef HELRM_HIP_H
+#define HELRM_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* orion/backend/lattigo/bindings.py:801-815 (ArrayResult* ctypes structs) */
+typedef struct { int* Data; unsigned long Length; } ArrayResultInt;
+typedef struct { float* Data; unsigned long Length; } ArrayResultFloat;
+typedef struct { unsigned long long* Data; unsigned long long Length; } ArrayResultUInt64;
+
+/* ---- scheme --------------------------------------------------------------- */
+/* orion/backend/lattigo/scheme.go:34-87 NewScheme (primes generated from the
+ * bit sizes as rlwe.GenModuli; keysPath/ioMode accepted, unused). */
+int NewScheme(int logN, int* logQ, int lenQ, int* logP, int lenP, int logScale,
+              int h, const char* ringType, const char* keysPath, const char* ioMode);
+/* orion/backend/lattigo/scheme.go:88-100 DeleteScheme */
+int DeleteScheme(void);
+/* [ext] scheme from explicit moduli and a key/randomness seed */
+int NewSchemeWithModuli(int logN, const uint64_t* q, int lenQ, const uint64_t* p,
+                        int lenP, int logScale, int h, uint64_t seed);
+/* [ext] seed used by the next NewScheme (default: /dev/urandom) */
+void SetSchemeSeed(uint64_t seed);
+/* [ext] the prime chain NewScheme would use */
+int GeneratePrimes(int logN, const int* logQ, int lenQ, const int* logP, int lenP,
+                   uint64_t* q, uint64_t* p);
+/* [ext] last error message of the calling thread */
+const char* GetLastError(void);
+
+/* ---- key generator ---------------------------------------------------------- */
+int NewKeyGenerator(void);            /* keygenerator.go:12 */
+int GenerateSecretKey(void);          /* keygenerator.go:17 */
+int GeneratePublicKey(void);          /* keygenerator.go:22 */
+int GenerateRelinearizationKey(void); /* keygenerator.go:27 (no relinearization on this path: no-op) */
+int GenerateEvaluationKeys(void);     /* keygenerator.go:32 */
+
+/* ---- encoder ------------------------------------------------------------------ */
+int NewEncoder(void);                                                      /* encoder.go:10 */
+int Encode(const float* values, int lenValues, int level, unsigned long scale); /* encoder.go:15-30 */
+ArrayResultFloat Decode(int plaintextID);                                  /* encoder.go:32-47 */
+int DecodeDouble(int plaintextID, double* out, int len);                   /* [ext] Decode before the float cast */
+
+/* ---- encryptor -------------------------------------------------------------- */
+int NewEncryptor(void);              /* encryptor.go:9 */
+int NewDecryptor(void);              /* encryptor.go:14 */
+int Encrypt(int plaintextID);        /* encryptor.go:19-27 */
+int Decrypt(int ciphertextID);       /* encryptor.go:29-38 */
+int SetEncryptionCounter(uint64_t v); /* [ext] index of the next encryption's randomness */
+
+/* ---- evaluator ---------------------------------------------------------------- */
+int NewEvaluator(void);                   /* evaluator.go:13-35 (+ power-of-two and conjugation keys) */
+int AddRotationKey(int rotation);         /* evaluator.go:37-52 */
+int Rotate(int ciphertextID, int amount); /* evaluator.go:80-87 */
+int RotateNew(int ciphertextID, int amount); /* evaluator.go:89-101 */
+int Conjugate(int ciphertextID);          /* evaluator.go:103-114 */
+int ConjugateNew(int ciphertextID);       /* evaluator.go:116-128 */
+int Rescale(int ciphertextID);            /* evaluator.go:130-136 */
+int RescaleNew(int ciphertextID);         /* evaluator.go:138-146 (rescales the input in place too) */
+int AddPlaintext(int ciphertextID, int plaintextID);     /* evaluator.go:228-235 */
+int AddPlaintextNew(int ciphertextID, int plaintextID);  /* evaluator.go:237-249 */
+int SubPlaintext(int ciphertextID, int plaintextID);     /* evaluator.go:251-258 */
+int SubPlaintextNew(int ciphertextID, int plaintextID);  /* evaluator.go:260-272 */
+int AddCiphertext(int ctID0, int ctID1);                 /* evaluator.go:297-304 */
+int AddCiphertextNew(int ctID0, int ctID1);              /* evaluator.go:306-318 */
+int SubCiphertext(int ctID0, int ctID1);                 /* evaluator.go:320-327 */
+int SubCiphertextNew(int ctID0, int ctID1);              /* evaluator.go:329-341 */
+
+/* ---- linear transforms -------------------------------------------------------- */
+int NewLinearTransformEvaluator(void);   /* lineartransform.go:30-34 */
+/* lineartransform.go:36-93 (diagonals as C floats, LevelQ = level,
+ * Scale = Q[level], LogBabyStepGiantStepRatio = int(ln(bsgsRatio))). */
+int GenerateLinearTransform(const int* diagIdxs, int diagIdxsLen, const float* diagData,
+                            int diagDataLen, int level, float bsgsRatio, const char* ioMode);
+int EvaluateLinearTransform(int transformID, int ctxtID);         /* lineartransform.go:95-113 */
+ArrayResultInt GetLinearTransformRotationKeys(int transformID);   /* lineartransform.go:115-122 */
+int GenerateLinearTransformRotationKey(int galEl);                /* lineartransform.go:124-128 */
+int DeleteLinearTransform(int id);                                /* lineartransform.go:25-28 */
+int RemoveRotationKeys(void);                                     /* lineartransform.go:203-211 */
+
+/* ---- tensors -------------------------------------------------------------------- */
+int DeletePlaintext(int plaintextID);                       /* tensors.go:34-37 */
+int DeleteCiphertext(int ciphertextID);                     /* tensors.go:39-42 */
+unsigned long GetPlaintextScale(int plaintextID);           /* tensors.go:44-50 (UINT64_MAX above 2^64) */
+unsigned long GetCiphertextScale(int ciphertextID);         /* tensors.go:52-58 */
+int SetPlaintextScale(int plaintextID, unsigned long scale); /* tensors.go:60-64 */
+int SetCiphertextScale(int ciphertextID, unsigned long scale); /* tensors.go:66-70 */
+int GetPlaintextLevel(int plaintextID);                     /* tensors.go:72-76 */
+int GetCiphertextLevel(int ciphertextID);                   /* tensors.go:78-82 */
+int GetPlaintextSlots(int plaintextID);                     /* tensors.go:84-89 */
+int GetCiphertextSlots(int ciphertextID);                   /* tensors.go:91-96 */
+int GetCiphertextDegree(int ciphertextID);                  /* tensors.go:98-102 */
+ArrayResultUInt64 GetModuliChain(void);                     /* tensors.go:104-109 */
+ArrayResultUInt64 GetAuxModuliChain(void);                  /* tensors.go:111-116 */
+ArrayResultInt GetLivePlaintexts(void);                     /* tensors.go:118-123 */
+ArrayResultInt GetLiveCiphertexts(void);                    /* tensors.go:125-130 */
+void FreeCArray(void* ptr);                                 /* utils.go:96-99 */
+double GetCiphertextScaleDouble(int ciphertextID);          /* [ext] scale as a double (no 2^64 clamp) */
+double GetPlaintextScaleDouble(int plaintextID);            /* [ext] */
+
+/* ---- [ext] raw residues (limb-major u64[rows][N]; coeff != 0: coefficient
+ *      domain, else the NTT domain; standard representatives in [0, q)) ---- */
+int ExportCiphertext(int ciphertextID, uint64_t* buf, size_t len, int coeff);
+int ImportCiphertext(const uint64_t* buf, int level, double scale, int coeff);
+int ExportPlaintext(int plaintextID, uint64_t* buf, size_t len, int coeff);
+int ImportPlaintext(const uint64_t* buf, int level, double scale, int coeff);
+int ExportGaloisKey(uint64_t galEl, uint64_t* buf, size_t len); /* [dnum][2][L+K][N], NTT */
+int ExportSecretKey(int64_t* buf, size_t len);                   /* ternary coefficients */
+int ExportLinearTransformDiagonal(int transformID, int diag, uint64_t* buf, size_t len);
+int GetLinearTransformInfo(int transformID, int* out, int len);  /* N1, giant, baby, plaintexts */
+int GetSchemeInfo(int* out, int len);  /* logN, L, K, dnum, logScale, h */
+
+/* ---- [ext] stream and measurement ------------------------------------------------ */
+int Synchronize(void);
+void* GetStream(void);                                            /* hipStream_t of the scheme */
+int KernelTimingEnable(int on);                                   /* HIP events around named launches */
+int KernelTimingGet(const char* name, long* count, double* total_ms);
+int GetMemoryStats(uint64_t* live, uint64_t* cached, uint64_t* peak);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

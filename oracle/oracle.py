@@ -1,0 +1,321 @@
+"""ctypes wrapper of the CPU restatement (oracle/ckks_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker.  The product package
+(helrm_amd) never imports this module.
+
+Buffers are numpy uint64 arrays in the layouts documented in ckks_oracle.h:
+a polynomial at level l is u64[l+1][N] (NTT domain), a ciphertext u64[2][l+1][N].
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libckks_oracle.so")
+
+u64p = ctypes.POINTER(ctypes.c_uint64)
+i64p = ctypes.POINTER(ctypes.c_int64)
+u32p = ctypes.POINTER(ctypes.c_uint32)
+intp = ctypes.POINTER(ctypes.c_int)
+fp = ctypes.POINTER(ctypes.c_float)
+dp = ctypes.POINTER(ctypes.c_double)
+vp = ctypes.c_void_p
+
+
+def build():
+    """Compile the checker library (make in oracle/)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        sig = {
+            "orc_is_prime": ([ctypes.c_uint64], ctypes.c_int),
+            "orc_gen_primes": ([ctypes.c_int, intp, ctypes.c_int, intp, ctypes.c_int, u64p, u64p], ctypes.c_int),
+            "orc_mulmod": ([ctypes.c_uint64] * 3, ctypes.c_uint64),
+            "orc_rand64": ([ctypes.c_uint64] * 3, ctypes.c_uint64),
+            "orc_new": ([ctypes.c_int, u64p, ctypes.c_int, u64p, ctypes.c_int, ctypes.c_int, ctypes.c_uint64], vp),
+            "orc_free": ([vp], None),
+            "orc_N": ([vp], ctypes.c_int),
+            "orc_modulus": ([vp, ctypes.c_int], ctypes.c_uint64),
+            "orc_galois_element": ([vp, ctypes.c_int], ctypes.c_uint64),
+            "orc_ntt": ([vp, ctypes.c_int, u64p], None),
+            "orc_intt": ([vp, ctypes.c_int, u64p], None),
+            "orc_automorphism_index": ([vp, ctypes.c_uint64, u32p], None),
+            "orc_secret_key": ([vp, i64p], None),
+            "orc_galois_key": ([vp, ctypes.c_uint64], u64p),
+            "orc_public_key": ([vp, u64p], None),
+            "orc_encode": ([vp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_int, u64p], None),
+            "orc_encode_f64": ([vp, dp, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_int, u64p], None),
+            "orc_decode": ([vp, u64p, ctypes.c_int, ctypes.c_double, fp], None),
+            "orc_decode_f64": ([vp, u64p, ctypes.c_int, ctypes.c_double, dp], None),
+            "orc_encrypt": ([vp, u64p, ctypes.c_int, ctypes.c_uint64, u64p], None),
+            "orc_decrypt": ([vp, u64p, ctypes.c_int, u64p], None),
+            "orc_add": ([vp, u64p, u64p, ctypes.c_int, ctypes.c_int, u64p], None),
+            "orc_rescale": ([vp, u64p, ctypes.c_int, u64p], None),
+            "orc_rotate": ([vp, u64p, ctypes.c_int, ctypes.c_int, u64p], None),
+            "orc_automorphism_ct": ([vp, u64p, ctypes.c_int, ctypes.c_uint64, u64p], None),
+            "orc_mod_down": ([vp, ctypes.c_int, u64p, u64p], None),
+            "orc_decompose_modup": ([vp, ctypes.c_int, u64p, u64p], None),
+            "orc_basis_extend": ([vp, intp, ctypes.c_int, intp, ctypes.c_int, u64p, u64p], None),
+            "orc_lt_new": ([vp, intp, ctypes.c_int, fp, ctypes.c_int, ctypes.c_float], vp),
+            "orc_lt_free": ([vp], None),
+            "orc_lt_n1": ([vp], ctypes.c_int),
+            "orc_lt_level": ([vp], ctypes.c_int),
+            "orc_lt_num_plaintexts": ([vp], ctypes.c_int),
+            "orc_lt_plaintext_index": ([vp, ctypes.c_int], ctypes.c_int),
+            "orc_lt_plaintext": ([vp, ctypes.c_int], u64p),
+            "orc_lt_rotations": ([vp, intp], ctypes.c_int),
+            "orc_lt_eval": ([vp, vp, u64p, ctypes.c_int, u64p], None),
+            "orc_lt_eval_partial": ([vp, vp, u64p, ctypes.c_int, ctypes.c_int, ctypes.c_int, u64p], None),
+            "orc_lt_num_giant": ([vp], ctypes.c_int),
+            "orc_set_threads": ([ctypes.c_int], None),
+        }
+        for name, (args, res) in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = L
+    return _lib
+
+
+def _p(a, t=u64p):
+    return a.ctypes.data_as(t)
+
+
+def gen_primes(logN, logq, logp):
+    q = np.zeros(len(logq), dtype=np.uint64)
+    p = np.zeros(len(logp), dtype=np.uint64)
+    lq = (ctypes.c_int * len(logq))(*logq)
+    lp = (ctypes.c_int * len(logp))(*logp)
+    rc = lib().orc_gen_primes(logN, lq, len(logq), lp, len(logp), _p(q), _p(p))
+    if rc != 0:
+        raise ValueError("prime generation failed")
+    return [int(x) for x in q], [int(x) for x in p]
+
+
+def set_threads(n):
+    lib().orc_set_threads(int(n))
+
+
+class Oracle:
+    """CKKS context of the CPU restatement (keys derived from `seed`)."""
+
+    def __init__(self, logN, q, p, h=192, seed=0):
+        self.logN, self.N = logN, 1 << logN
+        self.q, self.p = [int(x) for x in q], [int(x) for x in p]
+        self.L, self.K = len(self.q), len(self.p)
+        self.slots = self.N // 2
+        qa = np.array(self.q, dtype=np.uint64)
+        pa = np.array(self.p, dtype=np.uint64)
+        self.h, self.seed = h, seed
+        self.ctx = lib().orc_new(logN, _p(qa), self.L, _p(pa), self.K, h, seed)
+        if not self.ctx:
+            raise ValueError("invalid oracle parameters")
+        self.dnum = (self.L + self.K - 1) // self.K
+        self.lts = []
+
+    def close(self):
+        if self.ctx:
+            for t in self.lts:
+                lib().orc_lt_free(t)
+            self.lts = []
+            lib().orc_free(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- moduli helpers ----------------------------------------------------
+    def moduli(self, level, with_p=False):
+        m = self.q[: level + 1]
+        return m + self.p if with_p else m
+
+    def galois_element(self, k):
+        return int(lib().orc_galois_element(self.ctx, int(k)))
+
+    # -- primitives ----------------------------------------------------------
+    def ntt(self, a, mod_idx):
+        a = np.ascontiguousarray(a, dtype=np.uint64).copy()
+        lib().orc_ntt(self.ctx, mod_idx, _p(a))
+        return a
+
+    def intt(self, a, mod_idx):
+        a = np.ascontiguousarray(a, dtype=np.uint64).copy()
+        lib().orc_intt(self.ctx, mod_idx, _p(a))
+        return a
+
+    def to_coeff(self, poly, level, with_p=False):
+        """NTT-domain limbs -> coefficient domain (same limb layout)."""
+        poly = np.array(poly, dtype=np.uint64, copy=True)
+        idx = list(range(level + 1)) + ([self.L + j for j in range(self.K)] if with_p else [])
+        for r, m in enumerate(idx):
+            lib().orc_intt(self.ctx, m, _p(poly[r]))
+        return poly
+
+    def ct_to_coeff(self, ct, level):
+        return np.stack([self.to_coeff(ct[0], level), self.to_coeff(ct[1], level)])
+
+    def automorphism_index(self, galel):
+        idx = np.zeros(self.N, dtype=np.uint32)
+        lib().orc_automorphism_index(self.ctx, int(galel), _p(idx, u32p))
+        return idx
+
+    def basis_extend(self, src, dst, x):
+        x = np.ascontiguousarray(x, dtype=np.uint64)
+        out = np.zeros((len(dst), self.N), dtype=np.uint64)
+        s = (ctypes.c_int * len(src))(*src)
+        d = (ctypes.c_int * len(dst))(*dst)
+        lib().orc_basis_extend(self.ctx, s, len(src), d, len(dst), _p(x), _p(out))
+        return out
+
+    # -- keys ------------------------------------------------------------------
+    def secret_key(self):
+        s = np.zeros(self.N, dtype=np.int64)
+        lib().orc_secret_key(self.ctx, _p(s, i64p))
+        return s
+
+    def public_key(self):
+        out = np.zeros((2, self.L + self.K, self.N), dtype=np.uint64)
+        lib().orc_public_key(self.ctx, _p(out))
+        return out
+
+    def galois_key(self, galel):
+        ptr = lib().orc_galois_key(self.ctx, int(galel))
+        n = self.dnum * 2 * (self.L + self.K) * self.N
+        return np.ctypeslib.as_array(ptr, shape=(n,)).reshape(self.dnum, 2, self.L + self.K, self.N).copy()
+
+    # -- encoder -----------------------------------------------------------------
+    def encode(self, values, level, scale, with_p=False):
+        v = np.ascontiguousarray(np.asarray(values, dtype=np.float32))
+        nl = level + 1 + (self.K if with_p else 0)
+        out = np.zeros((nl, self.N), dtype=np.uint64)
+        lib().orc_encode(self.ctx, _p(v, fp), len(v), level, float(scale), int(with_p), _p(out))
+        return out
+
+    def encode_f64(self, values, level, scale, with_p=False):
+        v = np.ascontiguousarray(np.asarray(values, dtype=np.float64))
+        nl = level + 1 + (self.K if with_p else 0)
+        out = np.zeros((nl, self.N), dtype=np.uint64)
+        lib().orc_encode_f64(self.ctx, _p(v, dp), len(v), level, float(scale), int(with_p), _p(out))
+        return out
+
+    def decode(self, pt, level, scale):
+        pt = np.ascontiguousarray(pt, dtype=np.uint64)
+        out = np.zeros(self.slots, dtype=np.float32)
+        lib().orc_decode(self.ctx, _p(pt), level, float(scale), _p(out, fp))
+        return out
+
+    def decode_f64(self, pt, level, scale):
+        pt = np.ascontiguousarray(pt, dtype=np.uint64)
+        out = np.zeros(self.slots, dtype=np.float64)
+        lib().orc_decode_f64(self.ctx, _p(pt), level, float(scale), _p(out, dp))
+        return out
+
+    # -- encryptor -----------------------------------------------------------------
+    def encrypt(self, pt, level, enc_index):
+        pt = np.ascontiguousarray(pt, dtype=np.uint64)
+        ct = np.zeros((2, level + 1, self.N), dtype=np.uint64)
+        lib().orc_encrypt(self.ctx, _p(pt), level, int(enc_index), _p(ct))
+        return ct
+
+    def decrypt(self, ct, level):
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        pt = np.zeros((level + 1, self.N), dtype=np.uint64)
+        lib().orc_decrypt(self.ctx, _p(ct), level, _p(pt))
+        return pt
+
+    # -- evaluator -------------------------------------------------------------------
+    def add(self, a, b, level):
+        a = np.ascontiguousarray(a, dtype=np.uint64)
+        b = np.ascontiguousarray(b, dtype=np.uint64)
+        npoly = a.size // ((level + 1) * self.N)
+        out = np.zeros_like(a)
+        lib().orc_add(self.ctx, _p(a), _p(b), level, npoly, _p(out))
+        return out
+
+    def rescale(self, ct, level):
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        out = np.zeros((2, level, self.N), dtype=np.uint64)
+        lib().orc_rescale(self.ctx, _p(ct), level, _p(out))
+        return out
+
+    def rotate(self, ct, level, k):
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        out = np.zeros((2, level + 1, self.N), dtype=np.uint64)
+        lib().orc_rotate(self.ctx, _p(ct), level, int(k), _p(out))
+        return out
+
+    def mod_down(self, qp, level):
+        qp = np.ascontiguousarray(qp, dtype=np.uint64)
+        out = np.zeros((level + 1, self.N), dtype=np.uint64)
+        lib().orc_mod_down(self.ctx, level, _p(qp), _p(out))
+        return out
+
+    def decompose_modup(self, c1, level):
+        c1 = np.ascontiguousarray(c1, dtype=np.uint64)
+        dn = (level + 1 + self.K - 1) // self.K
+        out = np.zeros((dn, level + 1 + self.K, self.N), dtype=np.uint64)
+        lib().orc_decompose_modup(self.ctx, level, _p(c1), _p(out))
+        return out
+
+    # -- linear transform ------------------------------------------------------------
+    def lt_new(self, idx, data, level, bsgs_ratio):
+        idx = list(idx)
+        d = np.ascontiguousarray(np.asarray(data, dtype=np.float32).reshape(-1))
+        ia = (ctypes.c_int * len(idx))(*idx)
+        t = lib().orc_lt_new(self.ctx, ia, len(idx), _p(d, fp), level, ctypes.c_float(bsgs_ratio))
+        self.lts.append(t)
+        return t
+
+    def lt_n1(self, t):
+        return lib().orc_lt_n1(t)
+
+    def lt_rotations(self, t):
+        buf = (ctypes.c_int * (self.slots + 1))()
+        n = lib().orc_lt_rotations(t, buf)
+        return [buf[i] for i in range(n)]
+
+    def lt_galois_elements(self, t):
+        return [self.galois_element(k) for k in self.lt_rotations(t)]
+
+    def lt_plaintext(self, t, diag):
+        lvl = lib().orc_lt_level(t)
+        ptr = lib().orc_lt_plaintext(t, int(diag))
+        if not ptr:
+            return None
+        n = (lvl + 1 + self.K) * self.N
+        return np.ctypeslib.as_array(ptr, shape=(n,)).reshape(lvl + 1 + self.K, self.N).copy()
+
+    def lt_plaintext_indices(self, t):
+        return [lib().orc_lt_plaintext_index(t, i) for i in range(lib().orc_lt_num_plaintexts(t))]
+
+    def lt_eval(self, t, ct, ct_level):
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        l = min(ct_level, lib().orc_lt_level(t))
+        out = np.zeros((2, l + 1, self.N), dtype=np.uint64)
+        lib().orc_lt_eval(self.ctx, t, _p(ct), ct_level, _p(out))
+        return out, l
+
+    def lt_eval_partial(self, t, ct, ct_level, g0, g1):
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        l = min(ct_level, lib().orc_lt_level(t))
+        acc = np.zeros((2, l + 1 + self.K, self.N), dtype=np.uint64)
+        lib().orc_lt_eval_partial(self.ctx, t, _p(ct), ct_level, g0, g1, _p(acc))
+        return acc
+
+    def lt_num_giant(self, t):
+        return lib().orc_lt_num_giant(t)

@@ -1,0 +1,40 @@
+"""Shared set-up for parity tests: one parameter set, the oracle and the HIP
+library on the same moduli, secret key seed and encryption indices."""
+import numpy as np
+
+from oracle import oracle as O
+
+
+def make_params(logN, logq, logp):
+    q, p = O.gen_primes(logN, logq, logp)
+    return q, p
+
+
+def new_hip_scheme(lib, logN, q, p, logscale, h, seed, evaluator=True):
+    lib.NewSchemeWithModuli(logN, list(q), list(p), logscale, h, seed)
+    lib.NewKeyGenerator()
+    lib.GenerateSecretKey()
+    lib.GeneratePublicKey()
+    lib.NewEncoder()
+    lib.NewEncryptor()
+    lib.NewDecryptor()
+    if evaluator:
+        lib.NewEvaluator()
+    lib.NewLinearTransformEvaluator()
+
+
+def cfg1_tables(seed):
+    """Single-table cfg: 2 digit sub-tables of 16x16, U[-0.1, 0.1], index in [0, 256)."""
+    rng = np.random.default_rng(seed)
+    T = [rng.uniform(-0.1, 0.1, (16, 16)).astype(np.float32) for _ in range(2)]
+    idx = int(rng.integers(0, 256))
+    return T, idx
+
+
+def assert_equal_u64(a, b, what):
+    a = np.asarray(a, dtype=np.uint64)
+    b = np.asarray(b, dtype=np.uint64)
+    assert a.shape == b.shape, f"{what}: shape {a.shape} vs {b.shape}"
+    if not np.array_equal(a, b):
+        bad = np.argwhere(a != b)
+        raise AssertionError(f"{what}: {len(bad)} of {a.size} words differ, first at {tuple(bad[0])}: {a[tuple(bad[0])]} vs {b[tuple(bad[0])]}")

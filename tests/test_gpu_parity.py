@@ -1,0 +1,162 @@
+"""GPU parity: every operation on the path, HIP library vs the CPU
+restatement (oracle/), bit-exact on the same moduli, keys and randomness.
+
+Parameter sets:
+  small   N=2^11, Q=[40,30x3], P=[41,41]   (dnum 2)
+  digit1  N=2^12, Q=[50x7],   P=[55x3]     (dnum 3, last digit has one limb)
+  cfg1    N=2^13, Q=[60,40x4], P=[61]      (dnum 5; the single-table PCMM config)
+"""
+import numpy as np
+import pytest
+
+from helpers import assert_equal_u64, make_params, new_hip_scheme
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+PARAMS = {
+    "small": dict(logN=11, logq=[40, 30, 30, 30], logp=[41, 41], logscale=30, h=64, seed=11),
+    "digit1": dict(logN=12, logq=[50] * 7, logp=[55] * 3, logscale=40, h=128, seed=5),
+    "cfg1": dict(logN=13, logq=[60, 40, 40, 40, 40], logp=[61], logscale=40, h=192, seed=7),
+}
+
+
+class Ctx:
+    def __init__(self, lib, name):
+        P = PARAMS[name]
+        self.name = name
+        self.lib = lib
+        self.logN, self.N, self.slots = P["logN"], 1 << P["logN"], 1 << (P["logN"] - 1)
+        self.q, self.p = make_params(P["logN"], P["logq"], P["logp"])
+        self.L, self.K = len(self.q), len(self.p)
+        self.logscale, self.h, self.seed = P["logscale"], P["h"], P["seed"]
+        print(f"[parity] set {name}: N={self.N} L={self.L} K={self.K}", flush=True)
+        new_hip_scheme(lib, self.logN, self.q, self.p, self.logscale, self.h, self.seed)
+        self.orc = O.Oracle(self.logN, self.q, self.p, h=self.h, seed=self.seed)
+        self.rng = np.random.default_rng(1234)
+
+    def fresh_ct(self, level, enc_index, values=None):
+        vals = self.rng.uniform(-1, 1, self.slots).astype(np.float32) if values is None else np.asarray(values, np.float32)
+        scale = float(1 << self.logscale)
+        pt_id = self.lib.Encode(vals.tolist(), level, 1 << self.logscale)
+        self.lib.SetEncryptionCounter(enc_index)
+        ct_id = self.lib.Encrypt(pt_id)
+        ref = self.orc.encrypt(self.orc.encode(vals, level, scale), level, enc_index)
+        return ct_id, ref, vals
+
+
+@pytest.fixture(scope="module", params=list(PARAMS))
+def ctx(request, hip_lib):
+    c = Ctx(hip_lib, request.param)
+    yield c
+    c.orc.close()
+    hip_lib.DeleteScheme()
+
+
+def test_moduli_and_secret_key(ctx):
+    assert ctx.lib.GetModuliChain() == ctx.q
+    assert ctx.lib.GetAuxModuliChain() == ctx.p
+    np.testing.assert_array_equal(ctx.lib.export_secret_key(), ctx.orc.secret_key())
+
+
+def test_prime_generation_matches_oracle(ctx):
+    P = PARAMS[ctx.name]
+    import ctypes
+    q = (ctypes.c_uint64 * len(P["logq"]))()
+    p = (ctypes.c_uint64 * len(P["logp"]))()
+    ctx.lib.GeneratePrimes(P["logN"], P["logq"], P["logp"], q, p)
+    assert list(q) == ctx.q and list(p) == ctx.p
+
+
+@pytest.mark.parametrize("rot", [1, 3, -1])
+def test_galois_keys(ctx, rot):
+    ge = ctx.orc.galois_element(rot)
+    assert_equal_u64(ctx.lib.export_galois_key(ge), ctx.orc.galois_key(ge), f"galois key rot {rot}")
+
+
+def test_encode(ctx):
+    for level in (ctx.L - 1, 0):
+        vals = ctx.rng.uniform(-2, 2, ctx.slots).astype(np.float32)
+        scale = 1 << ctx.logscale
+        pt = ctx.lib.Encode(vals.tolist(), level, scale)
+        assert_equal_u64(ctx.lib.export_plaintext(pt), ctx.orc.encode(vals, level, float(scale)), f"encode level {level}")
+        dec = np.asarray(ctx.lib.Decode(pt), dtype=np.float32)
+        ref = ctx.orc.decode(ctx.orc.encode(vals, level, float(scale)), level, float(scale))
+        np.testing.assert_array_equal(dec, ref)
+        ctx.lib.DeletePlaintext(pt)
+
+
+def test_encrypt_decrypt(ctx):
+    level = ctx.L - 1
+    ct, ref, vals = ctx.fresh_ct(level, 3)
+    assert_equal_u64(ctx.lib.export_ciphertext(ct), ref, "encrypt")
+    pt = ctx.lib.Decrypt(ct)
+    assert_equal_u64(ctx.lib.export_plaintext(pt), ctx.orc.decrypt(ref, level), "decrypt")
+    dec = np.asarray(ctx.lib.Decode(pt))
+    assert np.abs(dec - vals).max() < 1e-3
+    ctx.lib.DeletePlaintext(pt)
+    ctx.lib.DeleteCiphertext(ct)
+
+
+@pytest.mark.parametrize("rot", [1, 5, "half"])
+def test_rotate(ctx, rot):
+    k = ctx.slots // 2 if rot == "half" else rot
+    level = ctx.L - 1
+    ct, ref, vals = ctx.fresh_ct(level, 10 + (k % 7))
+    out = ctx.lib.RotateNew(ct, k)
+    assert_equal_u64(ctx.lib.export_ciphertext(out), ctx.orc.rotate(ref, level, k), f"rotate {k}")
+    dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(out)))
+    assert np.abs(dec - np.roll(vals, -k)).max() < 1e-2
+
+
+def test_rescale(ctx):
+    level = ctx.L - 1
+    ct, ref, _ = ctx.fresh_ct(level, 21)
+    # give the ciphertext the scale of an LT output (delta * q_l): the Lattigo rule divides once
+    ct2 = ctx.lib.import_ciphertext(ctx.lib.export_ciphertext(ct), level, float(1 << ctx.logscale) * ctx.q[level])
+    out = ctx.lib.RescaleNew(ct2)
+    assert ctx.lib.GetCiphertextLevel(out) == level - 1
+    assert_equal_u64(ctx.lib.export_ciphertext(out), ctx.orc.rescale(ref, level), "rescale")
+
+
+def test_add(ctx):
+    level = ctx.L - 1
+    a, ra, _ = ctx.fresh_ct(level, 30)
+    b, rb, _ = ctx.fresh_ct(level, 31)
+    c = ctx.lib.AddCiphertextNew(a, b)
+    assert_equal_u64(ctx.lib.export_ciphertext(c), ctx.orc.add(ra, rb, level), "add")
+
+
+@pytest.mark.parametrize("case", ["dense16", "sparse", "ratio1", "above_level"])
+def test_linear_transform(ctx, case):
+    S = ctx.slots
+    rng = np.random.default_rng({"dense16": 1, "sparse": 2, "ratio1": 3, "above_level": 4}[case])
+    if case == "dense16":
+        idx, ratio, lt_level, ct_level = list(range(16)), 2.0, ctx.L - 1, ctx.L - 1
+    elif case == "sparse":
+        idx, ratio, lt_level, ct_level = [0, 1, 2, 5, 8, 37, S // 2 + 3], 2.0, ctx.L - 1, ctx.L - 1
+    elif case == "ratio1":
+        idx, ratio, lt_level, ct_level = list(range(0, 40, 3)), 1.0, ctx.L - 1, ctx.L - 1
+    else:
+        idx, ratio, lt_level, ct_level = [0, 1, 2, 5, 8], 2.0, 1, ctx.L - 1
+    data = rng.uniform(-1, 1, (len(idx), S)).astype(np.float32)
+    tid = ctx.lib.GenerateLinearTransform(idx, data.reshape(-1), lt_level, ratio, "none")
+    t = ctx.orc.lt_new(idx, data, lt_level, ratio)
+    assert ctx.lib.lt_info(tid)["N1"] == ctx.orc.lt_n1(t)
+    gal = ctx.lib.GetLinearTransformRotationKeys(tid)
+    assert gal == ctx.orc.lt_galois_elements(t)
+    for g in gal:
+        ctx.lib.GenerateLinearTransformRotationKey(g)
+    for di in ctx.orc.lt_plaintext_indices(t)[:3]:
+        assert_equal_u64(ctx.lib.export_lt_diagonal(tid, di, lt_level), ctx.orc.lt_plaintext(t, di), f"diagonal {di}")
+    ct, ref, vals = ctx.fresh_ct(ct_level, 40)
+    out = ctx.lib.EvaluateLinearTransform(tid, ct)
+    want, l = ctx.orc.lt_eval(t, ref, ct_level)
+    assert ctx.lib.GetCiphertextLevel(out) == l
+    assert_equal_u64(ctx.lib.export_ciphertext(out), want, f"linear transform {case}")
+    # numerics: out[i] = sum_k diag_k[i] * in[(i + k) mod S]
+    r = ctx.lib.RescaleNew(out)
+    dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(r)))
+    exp = sum(data[n].astype(np.float64) * np.roll(vals.astype(np.float64), -k) for n, k in enumerate(idx))
+    assert np.abs(dec - exp).max() < 0.05
+    ctx.lib.DeleteLinearTransform(tid)
