@@ -23,8 +23,10 @@ struct KeyMacArgs {
   const u64* digits;       // [dn][nqp][N] (per batch if digits_per_batch)
   size_t dig_bstride;
   int digits_per_batch;
-  const u64* const* key;   // per batch: [dnum][2][L+K][N] Montgomery form
-  const uint32_t* const* perm;  // per batch (nullptr: identity)
+  const u64* const* key;   // per batch: [dnum][2][L+K][N] Montgomery form (nullptr: use key1)
+  const uint32_t* const* perm;  // per batch (nullptr: use perm1)
+  const u64* key1;         // single-batch key
+  const uint32_t* perm1;   // single-batch permutation (nullptr: identity)
   const u64* add0;         // Q rows added to part 0 before the gather (mode 1)
   u64 *out0, *out1;
   size_t out_bstride;

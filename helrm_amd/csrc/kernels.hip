@@ -273,8 +273,8 @@ __global__ __launch_bounds__(256) void keymac_kernel(KeyMacArgs a) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
   int k = blockIdx.y, b = blockIdx.z;
   const int N = a.N;
-  const uint32_t* perm = a.perm ? a.perm[b] : nullptr;
-  const u64* key = a.key[b];
+  const uint32_t* perm = a.perm ? a.perm[b] : a.perm1;
+  const u64* key = a.key ? a.key[b] : a.key1;
   int src = perm ? (int)perm[i] : i;
   int kl = k <= a.l ? k : a.L + (k - a.l - 1);
   ModC mc = a.mods[kl];

@@ -231,6 +231,9 @@ struct LinTrans {
   DU64 diags;                            // [np][level+1+K][N], Montgomery form
   DevArray<uint64_t> d_gmask; DevArray<int> d_gpidx, d_bzero, d_bslot;
   double scale = 0;
+  // device arrays of key / permutation pointers (baby and giant rotations), built on first use
+  DevArray<const u64*> d_bkey, d_gkey; DevArray<const uint32_t*> d_bperm, d_gperm; DevArray<int> d_tg;
+  bool ptrs_ready = false;
 };
 
 struct BConvHost { int ns; BConvTable tab; DU64 hat, vS; };
@@ -761,11 +764,9 @@ std::unique_ptr<Cipher> automorphism(const Cipher& ct, u64 galel, bool lt_keyset
   DU64 digits((size_t)dn * nqp * N);
   decompose_modup(l, ct.d.p + (size_t)(l + 1) * N, 0, 1, digits.p);
   DU64 dd((size_t)2 * nqp * N);
-  DevArray<const u64*> kp(1); DevArray<const uint32_t*> pp(1);
-  const u64* kh[1] = {key}; const uint32_t* ph[1] = {nullptr};
-  upload(kp.p, kh, 1); upload(pp.p, ph, 1);
   KeyMacArgs a{};
-  a.digits = digits.p; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = kp.p; a.perm = pp.p; a.add0 = nullptr;
+  a.digits = digits.p; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = nullptr; a.perm = nullptr;
+  a.key1 = key; a.perm1 = nullptr; a.add0 = nullptr;
   a.out0 = dd.p; a.out1 = dd.p + (size_t)nqp * N; a.out_bstride = 0; a.mods = s.d_mods.p;
   a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
   launch_keymac(a, 1, s.st);
@@ -939,20 +940,33 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct) {
   std::vector<int> babies;
   for (int b : t.rot2) if (b != 0) babies.push_back(b);
   const int nbr = (int)babies.size();
+  const int ng = (int)t.giant.size(), nb = (int)t.rot2.size();
+  const int gs = (ng > 0 && t.giant[0] == 0) ? 1 : 0;
+  const int ngk = ng - gs;
+  {
+    // every key must be in the transform key set (checked on each call); pointer tables are uploaded once
+    std::vector<const u64*> bk(nbr), gk(ngk); std::vector<const uint32_t*> bp(nbr), gp(ngk); std::vector<int> tg(ngk);
+    for (int i = 0; i < nbr; i++) { u64 ge = galois_element(babies[i]); bk[i] = key_ptr(ge, true); bp[i] = perm_for(ge); }
+    for (int g = 0; g < ngk; g++) { u64 ge = galois_element(t.giant[gs + g]); gk[g] = key_ptr(ge, true); gp[g] = perm_for(ge); tg[g] = gs + g; }
+    LinTrans& tm = const_cast<LinTrans&>(t);
+    if (!tm.ptrs_ready) {
+      tm.d_bkey = DevArray<const u64*>(std::max(nbr, 1)); tm.d_bperm = DevArray<const uint32_t*>(std::max(nbr, 1));
+      tm.d_gkey = DevArray<const u64*>(std::max(ngk, 1)); tm.d_gperm = DevArray<const uint32_t*>(std::max(ngk, 1));
+      tm.d_tg = DevArray<int>(std::max(ngk, 1));
+      if (nbr) { upload(tm.d_bkey.p, bk.data(), nbr); upload(tm.d_bperm.p, bp.data(), nbr); }
+      if (ngk) { upload(tm.d_gkey.p, gk.data(), ngk); upload(tm.d_gperm.p, gp.data(), ngk); upload(tm.d_tg.p, tg.data(), ngk); }
+      tm.ptrs_ready = true;
+    }
+  }
   DU64 R((size_t)std::max(nbr, 1) * 2 * qp);
   if (nbr > 0) {
-    std::vector<const u64*> kh(nbr); std::vector<const uint32_t*> ph(nbr);
-    for (int i = 0; i < nbr; i++) { u64 ge = galois_element(babies[i]); kh[i] = key_ptr(ge, true); ph[i] = perm_for(ge); }
-    DevArray<const u64*> kp(nbr); DevArray<const uint32_t*> pp(nbr);
-    upload(kp.p, kh.data(), nbr); upload(pp.p, ph.data(), nbr);
     KeyMacArgs a{};
-    a.digits = digits.p; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = kp.p; a.perm = pp.p; a.add0 = pc.p;
+    a.digits = digits.p; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = t.d_bkey.p; a.perm = t.d_bperm.p; a.add0 = pc.p;
     a.out0 = R.p; a.out1 = R.p + qp; a.out_bstride = 2 * qp; a.mods = s.d_mods.p;
     a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
     timed("keymac_baby", [&] { launch_keymac(a, nbr, s.st); });
   }
   // 3. fused diagonal MAC -> T[g][2][nqp][N]
-  const int ng = (int)t.giant.size(), nb = (int)t.rot2.size();
   DU64 T((size_t)ng * 2 * qp);
   {
     DiagMacArgs a{};
@@ -968,25 +982,18 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct) {
     }
   }
   // 4. giant groups with a nonzero rotation: ModDown of part 1, decomposition, key product + automorphism + accumulate
-  const int gs = (ng > 0 && t.giant[0] == 0) ? 1 : 0;
-  const int ngk = ng - gs;
   DU64 acc((size_t)2 * qp);
   if (ngk > 0) {
     DU64 t1q((size_t)ngk * (l + 1) * N);
     mod_down(l, T.p + (size_t)gs * 2 * qp + qp, 2 * qp, ngk, t1q.p, (size_t)(l + 1) * N);
     DU64 dg2((size_t)ngk * dn * qp);
     decompose_modup(l, t1q.p, (size_t)(l + 1) * N, ngk, dg2.p);
-    std::vector<const u64*> kh(ngk); std::vector<const uint32_t*> ph(ngk); std::vector<int> tg(ngk);
-    for (int g = 0; g < ngk; g++) { u64 ge = galois_element(t.giant[gs + g]); kh[g] = key_ptr(ge, true); ph[g] = perm_for(ge); tg[g] = gs + g; }
-    DevArray<const u64*> kp(ngk); DevArray<const uint32_t*> pp(ngk); DevArray<int> dtg(ngk);
-    upload(kp.p, kh.data(), ngk); upload(pp.p, ph.data(), ngk); upload(dtg.p, tg.data(), ngk);
     GiantAccArgs a{};
-    a.digits = dg2.p; a.dig_bstride = (size_t)dn * qp; a.key = kp.p; a.perm = pp.p; a.tg = dtg.p; a.ng = ngk;
+    a.digits = dg2.p; a.dig_bstride = (size_t)dn * qp; a.key = t.d_gkey.p; a.perm = t.d_gperm.p; a.tg = t.d_tg.p; a.ng = ngk;
     a.T = T.p; a.T_gstride = 2 * qp; a.T_pstride = qp; a.t_zero = gs ? 0 : -1;
     a.out0 = acc.p; a.out1 = acc.p + qp; a.mods = s.d_mods.p;
     a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
     timed("giant_acc", [&] { launch_giant_acc(a, s.st); });
-    // dg2 / t1q / kp stay alive until the stream reaches this point (pool reuse is stream-ordered)
   } else {
     d2d(acc.p, T.p, 2 * qp * 8);
   }
@@ -1302,8 +1309,8 @@ int DeleteLinearTransform(int id) {
 int RemoveRotationKeys(void) { return guard([&] { sch().lt_keys.clear(); return 0; }); }
 
 // ---- tensors ----
-int DeletePlaintext(int id) { return guard([&] { Scheme& s = sch(); sync(); if (s.pts.erase(id)) s.pt_ids.give(id); return 0; }); }
-int DeleteCiphertext(int id) { return guard([&] { Scheme& s = sch(); sync(); if (s.cts.erase(id)) s.ct_ids.give(id); return 0; }); }
+int DeletePlaintext(int id) { return guard([&] { Scheme& s = sch(); if (s.pts.erase(id)) s.pt_ids.give(id); return 0; }); }
+int DeleteCiphertext(int id) { return guard([&] { Scheme& s = sch(); if (s.cts.erase(id)) s.ct_ids.give(id); return 0; }); }
 unsigned long GetPlaintextScale(int id) { unsigned long v = 0; guard([&] { v = scale_to_ulong(get_pt(id).scale); return 0; }); return v; }
 unsigned long GetCiphertextScale(int id) { unsigned long v = 0; guard([&] { v = scale_to_ulong(get_ct(id).scale); return 0; }); return v; }
 double GetCiphertextScaleDouble(int id) { double v = -1; guard([&] { v = get_ct(id).scale; return 0; }); return v; }

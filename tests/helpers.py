@@ -38,3 +38,25 @@ def assert_equal_u64(a, b, what):
     if not np.array_equal(a, b):
         bad = np.argwhere(a != b)
         raise AssertionError(f"{what}: {len(bad)} of {a.size} words differ, first at {tuple(bad[0])}: {a[tuple(bad[0])]} vs {b[tuple(bad[0])]}")
+
+
+def oracle_pcmm(orc, diagonals, output_rotations, level, selector, logscale, enc_index, bias=None, bsgs_ratio=2.0):
+    """The Orion embedding-PCMM flow (encode + encrypt the selector, LT,
+    rescale, hybrid fold, bias) run on the CPU restatement.  Returns the
+    output ciphertext, its level and scale."""
+    scale = float(1 << logscale)
+    idx = list(diagonals.keys())
+    data = np.stack([diagonals[i] for i in idx])
+    t = orc.lt_new(idx, data, level, bsgs_ratio)
+    ct = orc.encrypt(orc.encode(selector, level, scale), level, enc_index)
+    out, l = orc.lt_eval(t, ct, level)
+    sc = scale * orc.q[level]
+    out = orc.rescale(out, l)
+    sc /= orc.q[l]
+    l -= 1
+    slots = orc.slots
+    for i in range(1, output_rotations + 1):
+        out = orc.add(out, orc.rotate(out, l, slots // (2 ** i)), l)
+    b = np.zeros(1, np.float32) if bias is None else bias
+    out[0] = orc.add(out[0][None], orc.encode(b, l, scale)[None], l)[0]
+    return out, l, sc
