@@ -60,3 +60,42 @@ def test_pcmm26_full_size_decrypts(hip_lib):
     full = np.asarray(w.scheme.decode(w.scheme.decrypt(out.__class__(w.scheme, out.ids, 2 * 512))))
     assert np.abs(full[512:512 + 416] - w.expected).max() < TOL
     hip_lib.DeleteScheme()
+
+
+def test_golden_vectors_on_gpu(hip_lib):
+    """HIP library vs the committed golden vectors (tests/golden/pcmm_n10.npz)."""
+    import os
+    from helpers import new_hip_scheme
+    from helrm_amd import orion_host as oh
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "pcmm_n10.npz"))
+    q, p = g["q"].tolist(), g["p"].tolist()
+    logscale = int(g["logscale"])
+    new_hip_scheme(hip_lib, int(g["logn"]), q, p, logscale, int(g["h"]), int(g["seed"]))
+    np.testing.assert_array_equal(hip_lib.export_secret_key(), g["secret_key"].astype(np.int64))
+    level = len(q) - 1
+    S = 1 << (int(g["logn"]) - 1)
+    pt = hip_lib.Encode(g["selector"].tolist(), level, 1 << logscale)
+    hip_lib.SetEncryptionCounter(0)
+    ct = hip_lib.Encrypt(pt)
+    assert_equal_u64(hip_lib.export_ciphertext(ct), g["ct_in"], "golden ct_in")
+    M = oh.block_diag_matrix([[g["table0"], g["table1"]]])
+    d, rots = oh.diagonalize(M, S)
+    d = d[(0, 0)]
+    idx = list(d.keys())
+    assert idx == g["diag_indices"].tolist() and rots == int(g["fold_rotations"])
+    tid = hip_lib.GenerateLinearTransform(idx, np.concatenate([d[i] for i in idx]), level, 2.0, "none")
+    for ge in hip_lib.GetLinearTransformRotationKeys(tid):
+        hip_lib.GenerateLinearTransformRotationKey(ge)
+    assert_equal_u64(hip_lib.export_lt_diagonal(tid, idx[0], level), g["diag0_plain"], "golden diagonal")
+    out = hip_lib.EvaluateLinearTransform(tid, ct)
+    assert_equal_u64(hip_lib.export_ciphertext(out), g["lt_out"], "golden lt_out")
+    r = hip_lib.RescaleNew(out)
+    assert_equal_u64(hip_lib.export_ciphertext(r), g["rescaled"], "golden rescaled")
+    assert_equal_u64(hip_lib.export_ciphertext(hip_lib.RotateNew(ct, 1)), g["rot1"], "golden rot1")
+    for i in range(1, rots + 1):
+        t = hip_lib.RotateNew(r, S // 2 ** i)
+        hip_lib.AddCiphertext(r, t)
+    b = hip_lib.Encode([0.0], level - 1, 1 << logscale)
+    hip_lib.AddPlaintext(r, b)
+    assert_equal_u64(hip_lib.export_ciphertext(r), g["pcmm_out"], "golden pcmm_out")
+    hip_lib.DeleteScheme()

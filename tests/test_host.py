@@ -1,0 +1,91 @@
+"""Host-side callers (helrm_amd.orion_host) against the reference's
+documented examples and against plain numpy algebra."""
+import math
+
+import numpy as np
+import pytest
+
+from helrm_amd import orion_host as oh
+
+
+def test_diagonalize_docstring_example():
+    """orion/core/packing.py:653-686 docstring: 4x4 matrix, slots=4 and 2."""
+    M = np.arange(16, dtype=np.float32).reshape(4, 4)
+    d, r = oh.diagonalize(M, 4, "square")
+    assert r == 0
+    assert {k: v.tolist() for k, v in d[(0, 0)].items()} == {
+        0: [0., 5., 10., 15.], 1: [1., 6., 11., 12.], 2: [2., 7., 8., 13.], 3: [3., 4., 9., 14.]}
+    d2, _ = oh.diagonalize(M, 2, "square")
+    assert {k: v.tolist() for k, v in d2[(0, 0)].items()} == {0: [0., 5.], 1: [1., 4.]}
+    assert {k: v.tolist() for k, v in d2[(0, 1)].items()} == {0: [2., 7.], 1: [3., 6.]}
+    assert {k: v.tolist() for k, v in d2[(1, 0)].items()} == {0: [8., 13.], 1: [9., 12.]}
+    assert {k: v.tolist() for k, v in d2[(1, 1)].items()} == {0: [10., 15.], 1: [11., 14.]}
+
+
+@pytest.mark.parametrize("H,W,S", [(16, 32, 4096), (416, 1248, 32768), (10, 7, 64)])
+def test_hybrid_diagonals_and_fold_compute_matvec(H, W, S):
+    """sum_i diag_i[j] * x[(i+j) mod S], then the fold sum_k y[j + k*bh] == (M x)[j]."""
+    rng = np.random.default_rng(H)
+    M = rng.standard_normal((H, W)).astype(np.float32)
+    x = np.zeros(S)
+    x[:W] = rng.standard_normal(W)
+    d, rots = oh.diagonalize(M, S, "hybrid", False)
+    bh = 2 ** math.ceil(math.log2(H))
+    assert rots == int(math.log2(S // bh))
+    y = np.zeros(S)
+    for i, v in d[(0, 0)].items():
+        y += v.astype(np.float64) * np.roll(x, -i)
+    for i in range(1, rots + 1):
+        y = y + np.roll(y, -(S // 2 ** i))
+    np.testing.assert_allclose(y[:H], M.astype(np.float64) @ x[:W], rtol=1e-5, atol=1e-4)
+    np.testing.assert_allclose(y[bh:bh + H], y[:H])
+
+
+def test_pcmm26_shapes():
+    """512 nonzero diagonals, 6 fold rotations for 26 x (48 -> 16) blocks at 2^15 slots."""
+    from helrm_amd.workloads import PCMMWorkload
+    w = PCMMWorkload(None, "pcmm26", seed=0)
+    d, r = oh.diagonalize(w.matrix, 32768)
+    assert len(d[(0, 0)]) == 512 and r == 6
+    assert w.matrix.shape == (416, 1248)
+    assert w.selector.sum() == 26 * 3
+    np.testing.assert_allclose(w.matrix @ w.selector, w.expected, atol=1e-6)
+
+
+def test_digits_and_selector():
+    """examples/criteo/dlrm.py:66-82, 202-221."""
+    assert oh.digits(201, 16, 2).tolist() == [9, 12]
+    assert oh.digits(4095, 16, 3).tolist() == [15, 15, 15]
+    assert oh.radix_width(4096, 16) == 3 and oh.radix_width(256, 16) == 2
+    assert oh.expanded_width(4096, 20000, 16) == 4096 and oh.expanded_width(4096, 100, 16) == 48
+    sel = oh.expanded_id(201, 256, 0, 16)
+    assert sel.shape == (32,) and sel[9] == 1 and sel[16 + 12] == 1 and sel.sum() == 2
+    plain = oh.expanded_id(3, 10, 20000, 16)
+    assert plain.tolist() == [0, 0, 0, 1, 0, 0, 0, 0, 0, 0]
+
+
+def test_radix_lookup_is_block_matrix_product():
+    rng = np.random.default_rng(2)
+    tabs = [[rng.standard_normal((16, 16)).astype(np.float32) for _ in range(3)] for _ in range(4)]
+    idx = [5, 4095, 0, 1234]
+    M = oh.block_diag_matrix(tabs)
+    sel = oh.expanded_sparse(idx, [4096] * 4, 0, 16)
+    want = np.concatenate([oh.radix_lookup(t, i, 16) for t, i in zip(tabs, idx)])
+    np.testing.assert_allclose(M @ sel, want, atol=1e-5)
+
+
+def test_encode_padding_matches_orion():
+    """orion/backend/python/encoder.py:70-85: zero-pad to a multiple of slots."""
+    class B:
+        def __init__(self):
+            self.calls = []
+
+        def Encode(self, vals, level, scale):
+            self.calls.append((len(vals), level, scale))
+            return len(self.calls) - 1
+    s = oh.Scheme.__new__(oh.Scheme)
+    s.params = oh.Params(13, [60, 40], [61], 40)
+    s.backend = B()
+    pt = s.encode(np.ones(5000), 1)
+    assert [c[0] for c in s.backend.calls] == [4096, 4096] and pt.n == 5000
+    assert s.backend.calls[0][2] == 1 << 40
