@@ -26,10 +26,16 @@ HBM_PEAK_GBS = 8000.0
 
 
 def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=8):
-    """Per-PCMM and per-diag-MAC-launch algorithmic HBM bytes (words once)."""
+    """Per-PCMM and per-diag-MAC-launch algorithmic HBM bytes (every word once).
+
+    PCMM: the diagonals, each of the R rotation keys, the input and the output
+    ciphertext.  Diagonal MAC: the diagonals, the n1-1 hoisted baby rotations
+    (2 QP polys each), P*c (2 Q polys, baby step 0) read, one QP accumulator
+    pair per giant group written."""
     R = (n1 - 1) + (n2 - 1) + f
     pcmm = D * (L + K) * N * w + R * dnum * 2 * (L + K) * N * w + 2 * L * N * w + 2 * (L - 1) * N * w
-    diag_mac = D * (L + K) * N * w + 2 * n1 * (L + K) * N * w + 2 * n2 * (L + K) * N * w
+    diag_mac = (D * (L + K) * N * w + (n1 - 1) * 2 * (L + K) * N * w + 2 * L * N * w
+                + n2 * 2 * (L + K) * N * w)
     return pcmm, diag_mac
 
 
@@ -93,6 +99,20 @@ def cpu_baseline(q, p, h, key_seed, diagonals, selector, level, logscale, thread
         orc.close()
 
 
+def copy_calibration(mib):
+    """A plain device-to-device copy kernel of known size (torch elementwise
+    copy), run 3 times, so that the FETCH_SIZE / WRITE_SIZE counters can be
+    scaled against bytes that are known exactly."""
+    import torch
+    n = mib * (1 << 20) // 8
+    a = torch.arange(n, dtype=torch.int64, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n * 8, "bytes_written": n * 8, "launches": 3}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,7 +122,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (PMC counter calibration) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: the PCMM runs on a single MI355X (asked for --gpus {args.gpus}, "
@@ -158,8 +183,9 @@ def main():
 
     L, K = len(cfg["logq"]), len(cfg["logp"])
     N = 1 << cfg["logn"]
-    pcmm_bytes, mac_bytes = algorithmic_bytes(N=N, L=L, K=K, D=info["diagonals"], f=info["output_rotations"],
-                                              dnum=(L + K - 1) // K)
+    lti = lib.lt_info(list(w.layer.transform_ids.values())[0])
+    pcmm_bytes, mac_bytes = algorithmic_bytes(N=N, L=L, K=K, D=info["diagonals"], n1=lti["baby"], n2=lti["giant"],
+                                              f=info["output_rotations"], dnum=(L + K - 1) // K)
     mac_ms = kt["diag_mac"]["avg_ms"]
     achieved = mac_bytes / (mac_ms / 1000.0) / 1e9 if mac_ms else None
     roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -191,7 +217,7 @@ def main():
         "config": {"workload": f"{args.workload}: 26-table embedding PCMM, N=2^{cfg['logn']}, "
                                f"L={L} (60+50x{L - 1} bit), K={K} (61 bit), dnum={(L + K - 1) // K}, scale 2^{cfg['logscale']}, "
                                f"tables 4096x16 as 3 base-16 digit sub-tables",
-                   "diagonals": info["diagonals"], "baby_steps": 16, "giant_steps": 32,
+                   "diagonals": info["diagonals"], "baby_steps": lti["baby"], "giant_steps": lti["giant"],
                    "fold_rotations": info["output_rotations"], "matrix": info["matrix"]},
         "pcmm_ms": ms,
         "end_to_end_hbm": {"algorithmic_bytes": pcmm_bytes,
