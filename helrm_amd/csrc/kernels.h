@@ -4,8 +4,8 @@
 
 struct NttTables {
   const ModC* mods;
-  const u64 *w, *wp, *iw, *iwp;  // [mod][N] bit-reversed psi powers and Shoup companions
-  const u64 *ninv, *ninvp;       // [mod]
+  const u64 *tw, *itw;     // [mod][N][2]: (psi^brv(k), Shoup companion) and the same for psi^-1
+  const u64 *ninv, *ninvp; // [mod]
 };
 
 struct BConvSrc {
@@ -58,15 +58,20 @@ struct DiagMacArgs {
   size_t pc_pstride;
   const int* baby_is_zero;  // [nbaby]
   const int* baby_slot;     // [nbaby]
-  const uint64_t* gmask;    // [ng] bit b: baby b present in group g
-  const int* gpidx;         // [ng] first plaintext index of group g
+  const int* gpi;           // [ng][nbaby] plaintext index of baby b in group g, -1 if absent
   u64* T;                   // [ng][2][nqp][N]
   size_t T_gstride, T_pstride;
   const ModC* mods;
   int N, l, L, K, nqp, lt_level, ng, nbaby, b0, nb_chunk;
 };
 
+// In-place NTT (forward) / inverse NTT of rows rm of `batch` polynomials.
 void launch_ntt(u64* data, size_t bstride, int batch, RowMap rm, int logN, bool forward, const NttTables& tw, hipStream_t st);
+// Out-of-place: the transform of src's rows is written to the same rows of dst.
+void launch_ntt(const u64* src, size_t sstride, u64* dst, size_t dstride, int batch, RowMap rm, int logN, bool forward,
+                const NttTables& tw, hipStream_t st);
+// dst[b][0..words) = src[b][0..words) for b < batch.
+void launch_copy(u64* dst, size_t dstride, const u64* src, size_t sstride, size_t words, int batch, hipStream_t st);
 void launch_add(u64* out, const u64* a, const u64* b, size_t bstride, int batch, RowMap rm, const ModC* mods, int N, bool sub, hipStream_t st);
 void launch_mul_const(u64* out, const u64* in, size_t bstride, int batch, RowMap rm, const u64* cw, const u64* cwp, const ModC* mods, int N, hipStream_t st);
 void launch_mont_mul(u64* out, size_t obstride, const u64* a, size_t abstride, const u64* bR, size_t bbstride, int batch, RowMap rm, const ModC* mods, int N, bool acc, hipStream_t st);

@@ -6,107 +6,10 @@
 #include "hipckks.h"
 #include "kernels.h"
 
-// ---------------------------------------------------------------------------
-// Negacyclic NTT.  One LDS tile of E = 2^logE words per workgroup.  A
-// "contiguous" pass covers butterfly distances t < E on E consecutive words;
-// a "strided" pass covers the large distances on R rows x TC columns
-// (column stride C = N/R).  Forward: Cooley-Tukey, distances N/2 .. 1,
-// twiddle psi_rev[N/(2t) + j/(2t)].  Inverse: Gentleman-Sande, distances
-// 1 .. N/2, twiddle psi_inv_rev[N/(2t) + j/(2t)], then N^-1.
-// ---------------------------------------------------------------------------
-constexpr int NTT_THREADS = 512;
-
-template <bool FWD, bool STRIDED>
-__global__ __launch_bounds__(NTT_THREADS) void ntt_pass_kernel(
-    u64* __restrict__ data, size_t bstride, RowMap rm, int logN, int logE, int logR,
-    int lt_first, int lt_last, int scale_last, NttTables tw) {
-  extern __shared__ u64 sm[];
-  const int N = 1 << logN, E = 1 << logE;
-  const int row = rm.row(blockIdx.y);
-  const int m = rm.mod(row);
-  const u64 q = tw.mods[m].q;
-  u64* poly = data + (size_t)blockIdx.z * bstride + (size_t)row * N;
-  const u64* W = (FWD ? tw.w : tw.iw) + (size_t)m * N;
-  const u64* Wp = (FWD ? tw.wp : tw.iwp) + (size_t)m * N;
-  const int logTC = logE - logR;
-  const int logC = logN - logR;
-  const int TC = 1 << logTC;
-  size_t base = 0;
-  if (STRIDED) base = (size_t)blockIdx.x * TC; else base = (size_t)blockIdx.x * E;
-  for (int e = threadIdx.x; e < E; e += NTT_THREADS) {
-    size_t g = STRIDED ? base + (e & (TC - 1)) + ((size_t)(e >> logTC) << logC) : base + e;
-    sm[e] = poly[g];
-  }
-  __syncthreads();
-  const int step = FWD ? -1 : 1;
-  for (int lt = lt_first;; lt += step) {
-    const int t = 1 << lt;
-    for (int p = threadIdx.x; p < (E >> 1); p += NTT_THREADS) {
-      int e1; size_t glob;
-      if (STRIDED) {
-        int ltk = lt - logC;
-        int c = p & (TC - 1), kk = p >> logTC;
-        int k = ((kk >> ltk) << (ltk + 1)) | (kk & ((1 << ltk) - 1));
-        e1 = (k << logTC) | c;
-        glob = base + c + ((size_t)k << logC);
-      } else {
-        int j = ((p >> lt) << (lt + 1)) | (p & (t - 1));
-        e1 = j;
-        glob = base + j;
-      }
-      const int e2 = e1 + (STRIDED ? (t >> logC) << logTC : t);
-      const size_t wi = (size_t)(N >> (lt + 1)) + (glob >> (lt + 1));
-      const u64 w = W[wi], wp = Wp[wi];
-      u64 U = sm[e1], V = sm[e2];
-      if (FWD) {
-        V = shoup_mul(V, w, wp, q);
-        sm[e1] = add_mod(U, V, q);
-        sm[e2] = sub_mod(U, V, q);
-      } else {
-        sm[e1] = add_mod(U, V, q);
-        sm[e2] = shoup_mul(sub_mod(U, V, q), w, wp, q);
-      }
-    }
-    __syncthreads();
-    if (lt == lt_last) break;
-  }
-  const u64 ni = tw.ninv[m], nip = tw.ninvp[m];
-  for (int e = threadIdx.x; e < E; e += NTT_THREADS) {
-    size_t g = STRIDED ? base + (e & (TC - 1)) + ((size_t)(e >> logTC) << logC) : base + e;
-    u64 v = sm[e];
-    if (scale_last) v = shoup_mul(v, ni, nip, q);
-    poly[g] = v;
-  }
-}
-
-void launch_ntt(u64* data, size_t bstride, int batch, RowMap rm, int logN, bool forward,
-                const NttTables& tw, hipStream_t st) {
-  const int N = 1 << logN;
-  const int logE = logN < 12 ? logN : 12;
-  const int E = 1 << logE;
-  const int rows = rm.nact();
-  if (rows <= 0 || batch <= 0) return;
-  const size_t shm = (size_t)E * sizeof(u64);
-  if (logN <= logE) {
-    dim3 grid(1, rows, batch);
-    if (forward)
-      hipLaunchKernelGGL((ntt_pass_kernel<true, false>), grid, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, 0, logN - 1, 0, 0, tw);
-    else
-      hipLaunchKernelGGL((ntt_pass_kernel<false, false>), grid, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, 0, 0, logN - 1, 1, tw);
-    return;
-  }
-  // two passes: strided pass owns the logR largest distances
-  const int logR = logN / 2;
-  const int logC = logN - logR;
-  dim3 gridS(N >> logE, rows, batch), gridC(N >> logE, rows, batch);
-  if (forward) {
-    hipLaunchKernelGGL((ntt_pass_kernel<true, true>), gridS, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, logR, logN - 1, logC, 0, tw);
-    hipLaunchKernelGGL((ntt_pass_kernel<true, false>), gridC, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, 0, logC - 1, 0, 0, tw);
-  } else {
-    hipLaunchKernelGGL((ntt_pass_kernel<false, false>), gridC, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, 0, 0, logC - 1, 0, tw);
-    hipLaunchKernelGGL((ntt_pass_kernel<false, true>), gridS, dim3(NTT_THREADS), shm, st, data, bstride, rm, logN, logE, logR, logC, logN - 1, 1, tw);
-  }
-}
+// High word of a 128-bit sum of products of words < q < 2^62: after at most
+// 16 products (plus one earlier fold) it is below 5q; bring it below q.
+__device__ __forceinline__ u64 csub64(u64 x, u64 m) { return x >= m ? x - m : x; }
+__device__ __forceinline__ u64 fold_hi4(u64 hi, u64 q) { return csub64(csub64(csub64(hi, q << 2), q << 1), q); }
 
 // ---------------------------------------------------------------------------
 // Element-wise kernels over (coefficient, row, batch)
@@ -181,24 +84,52 @@ void launch_permute(u64* out, const u64* in, size_t bstride, int batch, int rows
   hipLaunchKernelGGL(permute_kernel, dim3(N / 256, rows, batch), dim3(256), 0, st, out, in, bstride, rows, perm, N);
 }
 
+// Strided batched copy: dst[b][0..words) = src[b][0..words), 16 bytes per lane.
+template <bool VEC>
+__global__ __launch_bounds__(256) void copy_kernel(u64* __restrict__ dst, size_t dstride, const u64* __restrict__ src,
+                                                   size_t sstride, size_t words) {
+  const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 2;
+  const u64* s = src + (size_t)blockIdx.y * sstride;
+  u64* d = dst + (size_t)blockIdx.y * dstride;
+  if (!VEC) {
+    if (i < words) d[i] = s[i];
+    if (i + 1 < words) d[i + 1] = s[i + 1];
+  } else if (i + 1 < words) {
+    const ulong2 v = *reinterpret_cast<const ulong2*>(s + i);
+    *reinterpret_cast<ulong2*>(d + i) = v;
+  } else if (i < words) {
+    d[i] = s[i];
+  }
+}
+void launch_copy(u64* dst, size_t dstride, const u64* src, size_t sstride, size_t words, int batch, hipStream_t st) {
+  if (words == 0 || batch <= 0) return;
+  const size_t blocks = (words + 511) / 512;
+  const bool vec = (((uintptr_t)dst | (uintptr_t)src | (dstride * 8) | (sstride * 8)) & 15) == 0;
+  if (vec) hipLaunchKernelGGL(copy_kernel<true>, dim3((unsigned)blocks, batch), dim3(256), 0, st, dst, dstride, src, sstride, words);
+  else hipLaunchKernelGGL(copy_kernel<false>, dim3((unsigned)blocks, batch), dim3(256), 0, st, dst, dstride, src, sstride, words);
+}
+
 // ---------------------------------------------------------------------------
 // RNS basis extension (exact, float64 overflow count as Lattigo ModUpExact):
 //   y_i = x_i * (S/s_i)^-1 mod s_i;  v = (u64) sum_i (double)y_i/(double)s_i
 //   out_t = sum_i y_i * (S/s_i mod t) - v*S mod t
-// One thread per coefficient; the source residues stay in registers and
-// every destination row is produced from them (read ns, write nd words).
+// One thread per coefficient computes y and v once and produces a block of
+// destination rows from them (read ns, write nd words); the row sum is
+// exact in 128 bits (folded below 4t after every 16 products), then one
+// Montgomery REDC removes the 2^64 the (S/s_i mod t) table carries.
 // ---------------------------------------------------------------------------
 template <int MAXS>
 __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, size_t in_bstride, int ns,
                                                     BConvTable tab, u64* __restrict__ out, size_t out_bstride,
                                                     RowList rl, const ModC* __restrict__ mods, int N, int force_v0) {
-  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
   const u64* inb = in + (size_t)blockIdx.z * in_bstride;
   u64* outb = out + (size_t)blockIdx.z * out_bstride;
   u64 y[MAXS];
   double vf = 0.0;
 #pragma unroll
   for (int i = 0; i < MAXS; i++) {
+    y[i] = 0;
     if (i < ns) {
       const BConvSrc s = tab.src[i];
       y[i] = shoup_mul(inb[(size_t)i * N + x], s.hinv, s.hinvp, s.q);
@@ -207,17 +138,20 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
   }
   const int v = force_v0 ? 0 : (int)(u64)vf;
   const int r0 = blockIdx.y * tab.rows_per_block;
-  int r1 = r0 + tab.rows_per_block;
-  if (r1 > rl.n) r1 = rl.n;
+  const int r1 = min(r0 + tab.rows_per_block, rl.n);
   for (int r = r0; r < r1; r++) {
     const int m = rl.mod[r];
     const ModC mc = mods[m];
     const u64* h = tab.hat + (size_t)m * ns;
-    u64 lo = 0, hi = 0;
+    u128 acc = 0;
 #pragma unroll
-    for (int i = 0; i < MAXS; i++)
-      if (i < ns) mac_lazy(lo, hi, y[i], h[i], mc.q);
-    u64 res = redc(lo, hi, mc.q, mc.qinv);
+    for (int i = 0; i < MAXS; i++) {
+      if (i < ns) {
+        if (i > 0 && (i & 15) == 0) acc = ((u128)fold_hi4((u64)(acc >> 64), mc.q) << 64) | (u64)acc;
+        acc += (u128)y[i] * h[i];
+      }
+    }
+    u64 res = redc((u64)acc, fold_hi4((u64)(acc >> 64), mc.q), mc.q, mc.qinv);
     res = sub_mod(res, tab.vS[(size_t)m * (ns + 1) + v], mc.q);
     outb[(size_t)rl.row[r] * N + x] = res;
   }
@@ -226,9 +160,13 @@ void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable& ta
                   const RowList& rl, const ModC* mods, int N, bool force_v0, hipStream_t st) {
   if (rl.n <= 0 || batch <= 0) return;
   BConvTable t = tab;
-  t.rows_per_block = 8;
-  int ny = (rl.n + t.rows_per_block - 1) / t.rows_per_block;
-  dim3 grid(N / 256, ny, batch);
+  // all destination rows in one thread unless that leaves too few workgroups
+  const int cols = N / 256;
+  int ny = 1;
+  while (ny < rl.n && (long)cols * batch * ny < 2048) ny *= 2;
+  t.rows_per_block = (rl.n + ny - 1) / ny;
+  ny = (rl.n + t.rows_per_block - 1) / t.rows_per_block;
+  dim3 grid(cols, ny, batch);
   if (ns <= 8)
     hipLaunchKernelGGL((bconv_kernel<8>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, force_v0 ? 1 : 0);
   else if (ns <= 16)
@@ -347,9 +285,14 @@ void launch_giant_acc(const GiantAccArgs& a, hipStream_t st) {
 // streams every plaintext diagonal once, writing one accumulator pair per
 // giant group:
 //   T[g][p][k][x] = sum_{b in baby(g)} diag_{g,b}[k][x] * S_b[p][k][x]
-// S_0 = P*c (Q rows only), S_b = hoisted rotation b (QP).  Diagonals are in
-// Montgomery form; the per-group sum is accumulated lazily in 128 bits.
+// S_0 = P*c (Q rows only), S_b = hoisted rotation b (QP).  The next group's
+// diagonals are loaded while the current group is multiplied (NB loads in
+// flight per thread).  Products are summed exactly in 128 bits (16 products
+// of words < 2^62 cannot overflow; the high word is folded below 4q after
+// every 16), then one Montgomery REDC per word removes the 2^64 the
+// diagonals carry.
 // ---------------------------------------------------------------------------
+
 template <int NB>
 __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
   const int x = blockIdx.x * blockDim.x + threadIdx.x;
@@ -358,40 +301,56 @@ __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
   const int kl = k <= a.l ? k : a.L + (k - a.l - 1);
   const ModC mc = a.mods[kl];
   const int krow = k <= a.l ? k : a.lt_level + 1 + (k - a.l - 1);  // row inside a diagonal
-  const size_t prow = (size_t)krow * N + x;
+  const u64* dbase = a.diag + (size_t)krow * N + x;
   u64 s0[NB], s1[NB];
 #pragma unroll
   for (int b = 0; b < NB; b++) {
-    int bb = a.b0 + b;
+    const int bb = a.b0 + b;
     s0[b] = 0; s1[b] = 0;
     if (bb < a.nbaby) {
       if (a.baby_is_zero[bb]) {
         if (k <= a.l) { s0[b] = a.pc[(size_t)k * N + x]; s1[b] = a.pc[a.pc_pstride + (size_t)k * N + x]; }
       } else {
-        const u64* r = a.R + (size_t)a.baby_slot[bb] * a.R_bstride;
-        s0[b] = r[(size_t)k * N + x];
-        s1[b] = r[a.R_pstride + (size_t)k * N + x];
+        const u64* r = a.R + (size_t)a.baby_slot[bb] * a.R_bstride + (size_t)k * N + x;
+        s0[b] = r[0];
+        s1[b] = r[a.R_pstride];
       }
     }
   }
-  for (int g = 0; g < a.ng; g++) {
-    const uint64_t mask = a.gmask[g] >> a.b0;
-    int pidx = a.gpidx[g] + (a.b0 ? __popcll(a.gmask[g] & ((1ULL << a.b0) - 1)) : 0);
-    u64 lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+  u64 dc[NB], dn[NB];
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-      if ((mask >> b) & 1) {
-        const u64 d = a.diag[(size_t)pidx * a.diag_stride + prow];
-        pidx++;
-        mac_lazy(lo0, hi0, d, s0[b], mc.q);
-        mac_lazy(lo1, hi1, d, s1[b], mc.q);
+  for (int b = 0; b < NB; b++) {
+    const int bb = a.b0 + b;
+    const int pi = bb < a.nbaby ? a.gpi[bb] : -1;
+    dc[b] = pi >= 0 ? dbase[(size_t)pi * a.diag_stride] : 0;
+  }
+  for (int g = 0; g < a.ng; g++) {
+    if (g + 1 < a.ng) {
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        const int bb = a.b0 + b;
+        const int pi = bb < a.nbaby ? a.gpi[(size_t)(g + 1) * a.nbaby + bb] : -1;
+        dn[b] = pi >= 0 ? dbase[(size_t)pi * a.diag_stride] : 0;
       }
     }
+    u128 acc0 = 0, acc1 = 0;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      if (b > 0 && (b & 15) == 0) {
+        acc0 = ((u128)fold_hi4((u64)(acc0 >> 64), mc.q) << 64) | (u64)acc0;
+        acc1 = ((u128)fold_hi4((u64)(acc1 >> 64), mc.q) << 64) | (u64)acc1;
+      }
+      acc0 += (u128)dc[b] * s0[b];
+      acc1 += (u128)dc[b] * s1[b];
+    }
+    u64 r0 = redc((u64)acc0, fold_hi4((u64)(acc0 >> 64), mc.q), mc.q, mc.qinv);
+    u64 r1 = redc((u64)acc1, fold_hi4((u64)(acc1 >> 64), mc.q), mc.q, mc.qinv);
     u64* T = a.T + (size_t)g * a.T_gstride + (size_t)k * N + x;
-    u64 r0 = redc(lo0, hi0, mc.q, mc.qinv), r1 = redc(lo1, hi1, mc.q, mc.qinv);
     if (a.b0 > 0) { r0 = add_mod(r0, T[0], mc.q); r1 = add_mod(r1, T[a.T_pstride], mc.q); }
     T[0] = r0;
     T[a.T_pstride] = r1;
+#pragma unroll
+    for (int b = 0; b < NB; b++) dc[b] = dn[b];
   }
 }
 void launch_diag_mac(const DiagMacArgs& a, hipStream_t st) {

@@ -1,0 +1,249 @@
+// ntt.hip -- negacyclic NTT / inverse NTT for gfx950.
+//
+// Transform of one limb of N = 2^logN words, N = R x C with R = 2^SA rows of
+// C = 2^SB columns (5 <= SA, SB <= 8).  Forward (Cooley-Tukey, distances
+// N/2 .. 1, twiddle W[(N + g) >> (lt + 1)] for the pair (g, g + 2^lt)):
+//   pass A  distances N/2 .. C      (column sub-transforms of size R)
+//   pass B  distances C/2 .. 1      (row sub-transforms of size C)
+// Inverse (Gentleman-Sande, distances 1 .. N/2, then N^-1): pass B, pass A.
+//
+// A sub-transform of size 2^S is computed by 2^(S-4) threads holding 16
+// words each in registers: one radix-16 round (4 butterfly stages without
+// any exchange), one LDS exchange, one round of the remaining S-4 stages.
+// Butterflies are lazy (Harvey): forward values stay in [0, 4q), inverse
+// values in [0, 2q); each pass's output is reduced to [0, q) only where the
+// transform ends, so the result equals the textbook NTT word for word.
+// Twiddles are (w, floor(w 2^64 / q)) pairs read as one 16-byte load.
+#include <algorithm>
+
+#include "hipckks.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int NTT_TPB = 256;
+
+__device__ __forceinline__ u64 shoup_lazy(u64 x, u64 w, u64 wp, u64 q) {  // x*w mod q in [0, 2q)
+  return x * w - __umul64hi(x, wp) * q;
+}
+__device__ __forceinline__ u64 csub(u64 x, u64 m) { return x >= m ? x - m : x; }
+
+// One register round of NST butterfly stages on v[16].  Element i stands for
+// global index g_i = A + B + (i << ls) with B < 2^ls and A a multiple of
+// 2^(ls+4); the pair at register distance rd has index distance rd << ls and
+// uses twiddle ((N + A) >> (ls + log2(rd) + 1)) + (i >> (log2(rd) + 1)).
+template <bool FWD, int NST>
+__device__ __forceinline__ void ntt_round(u64 (&v)[16], u64 A, int ls, u64 Nn, const uint4* __restrict__ tw,
+                                          u64 q) {
+  const u64 q2 = q + q;
+#pragma unroll
+  for (int s = 0; s < NST; s++) {
+    const int lrd = FWD ? NST - 1 - s : s;  // log2 of the register distance
+    const int rd = 1 << lrd;
+    const int sh = lrd + 1;
+    const u64 tb = (Nn + A) >> (ls + sh);
+#pragma unroll
+    for (int k = 0; k < (16 >> sh); k++) {
+      const uint4 t4 = tw[tb + k];
+      const u64 w = ((u64)t4.y << 32) | t4.x, wp = ((u64)t4.w << 32) | t4.z;
+#pragma unroll
+      for (int r = 0; r < rd; r++) {
+        const int i = (k << sh) + r;
+        u64 X = v[i], Y = v[i + rd];
+        if (FWD) {
+          const u64 x = csub(X, q2);
+          const u64 t = shoup_lazy(Y, w, wp, q);
+          v[i] = x + t;
+          v[i + rd] = x - t + q2;
+        } else {
+          v[i] = csub(X + Y, q2);
+          v[i + rd] = shoup_lazy(X - Y + q2, w, wp, q);
+        }
+      }
+    }
+  }
+}
+
+// LDS column swizzle for the row pass: conflict-free both for the strided
+// (j + P*i) and the consecutive (16*j + i) access patterns.
+__device__ __forceinline__ int swz(int col) { return col ^ ((col >> 4) & 15); }
+
+struct NttArgs {
+  const u64* src;  // input of the first pass (src == data: in place)
+  size_t sstride;
+  u64* data;       // output; the second pass works in place on it
+  size_t bstride;
+  RowMap rm;
+  const uint4* tw;   // [mod][N] (w, w') pairs, forward or inverse table
+  const ModC* mods;
+  const u64 *ninv, *ninvp;  // [mod]
+  int logN, SA, SB, nsub;   // nsub: sub-transforms per workgroup
+};
+
+// Column pass (pass A): workgroup = nsub columns x R rows.
+template <bool FWD, int S>
+__global__ __launch_bounds__(NTT_TPB) void ntt_col_kernel(NttArgs a) {
+  // forward: first pass (reads a.src); inverse: second pass (in place)
+  __shared__ u64 sm[4096];
+  constexpr int P = 1 << (S - 4);
+  const int nsub = a.nsub;
+  const int tid = threadIdx.x;
+  const int c = tid & (nsub - 1);
+  const int j = tid / nsub;  // in [0, P)
+  const int row = a.rm.row(blockIdx.y);
+  const int m = a.rm.mod(row);
+  const u64 q = a.mods[m].q;
+  const u64 Nn = 1ull << a.logN;
+  const int SB = a.SB;
+  const size_t C = (size_t)1 << SB;
+  const int col = blockIdx.x * nsub + c;
+  u64* poly = a.data + (size_t)blockIdx.z * a.bstride + (size_t)row * Nn + col;
+  const uint4* tw = a.tw + (size_t)m * Nn;
+  u64 v[16];
+  if (FWD) {
+    const u64* in = a.src + (size_t)blockIdx.z * a.sstride + (size_t)row * Nn + col;
+    // round 1: rows j + P*i, distances R/2 .. R/16 rows
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = in[(size_t)(j + P * i) * C];
+    ntt_round<true, 4>(v, 0, S - 4 + SB, Nn, tw, q);
+#pragma unroll
+    for (int i = 0; i < 16; i++) sm[(j + P * i) * nsub + c] = v[i];
+    __syncthreads();
+    // round 2: rows 16*j + i, the remaining S-4 stages
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = sm[(16 * j + i) * nsub + c];
+    ntt_round<true, S - 4>(v, (u64)(16 * j) << SB, SB, Nn, tw, q);
+#pragma unroll
+    for (int i = 0; i < 16; i++) poly[(size_t)(16 * j + i) * C] = v[i];
+  } else {
+    // round 1: rows 16*j + i, distances C .. 2^(S-5) C
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = poly[(size_t)(16 * j + i) * C];
+    ntt_round<false, S - 4>(v, (u64)(16 * j) << SB, SB, Nn, tw, q);
+#pragma unroll
+    for (int i = 0; i < 16; i++) sm[(16 * j + i) * nsub + c] = v[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = sm[(j + P * i) * nsub + c];
+    ntt_round<false, 4>(v, 0, S - 4 + SB, Nn, tw, q);
+    const u64 ni = a.ninv[m], nip = a.ninvp[m];
+#pragma unroll
+    for (int i = 0; i < 16; i++) poly[(size_t)(j + P * i) * C] = csub(shoup_lazy(v[i], ni, nip, q), q);
+  }
+}
+
+// Row pass (pass B): workgroup = nsub rows x C columns.
+template <bool FWD, int S>
+__global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
+  __shared__ u64 sm[4096];
+  constexpr int P = 1 << (S - 4);
+  constexpr int C = 1 << S;
+  const int tid = threadIdx.x;
+  const int j = tid & (P - 1);
+  const int rho = tid >> (S - 4);
+  const int row = a.rm.row(blockIdx.y);
+  const int m = a.rm.mod(row);
+  const u64 q = a.mods[m].q;
+  const u64 Nn = 1ull << a.logN;
+  const int r = blockIdx.x * a.nsub + rho;  // row of the R x C view
+  u64* poly = a.data + (size_t)blockIdx.z * a.bstride + (size_t)row * Nn + (size_t)r * C;
+  u64* srow = sm + rho * C;
+  const uint4* tw = a.tw + (size_t)m * Nn;
+  const u64 A = (u64)r * C;
+  u64 v[16];
+  if (FWD) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = poly[j + P * i];
+    ntt_round<true, 4>(v, A, S - 4, Nn, tw, q);
+#pragma unroll
+    for (int i = 0; i < 16; i++) srow[swz(j + P * i)] = v[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = srow[swz(16 * j + i)];
+    ntt_round<true, S - 4>(v, A + 16 * j, 0, Nn, tw, q);
+    const u64 q2 = q + q;
+#pragma unroll
+    for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = csub(csub(v[i], q2), q);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) poly[j + P * i] = srow[swz(j + P * i)];
+  } else {
+    const u64* in = a.src + (size_t)blockIdx.z * a.sstride + (size_t)row * Nn + (size_t)r * C;
+#pragma unroll
+    for (int i = 0; i < 16; i++) srow[swz(j + P * i)] = in[j + P * i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = srow[swz(16 * j + i)];
+    ntt_round<false, S - 4>(v, A + 16 * j, 0, Nn, tw, q);
+#pragma unroll
+    for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = v[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = srow[swz(j + P * i)];
+    ntt_round<false, 4>(v, A, S - 4, Nn, tw, q);
+#pragma unroll
+    for (int i = 0; i < 16; i++) poly[j + P * i] = v[i];
+  }
+}
+
+template <bool FWD>
+void launch_col(int S, dim3 grid, dim3 block, const NttArgs& a, hipStream_t st) {
+  switch (S) {
+    case 5: hipLaunchKernelGGL((ntt_col_kernel<FWD, 5>), grid, block, 0, st, a); break;
+    case 6: hipLaunchKernelGGL((ntt_col_kernel<FWD, 6>), grid, block, 0, st, a); break;
+    case 7: hipLaunchKernelGGL((ntt_col_kernel<FWD, 7>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((ntt_col_kernel<FWD, 8>), grid, block, 0, st, a); break;
+  }
+}
+template <bool FWD>
+void launch_row(int S, dim3 grid, dim3 block, const NttArgs& a, hipStream_t st) {
+  switch (S) {
+    case 5: hipLaunchKernelGGL((ntt_row_kernel<FWD, 5>), grid, block, 0, st, a); break;
+    case 6: hipLaunchKernelGGL((ntt_row_kernel<FWD, 6>), grid, block, 0, st, a); break;
+    case 7: hipLaunchKernelGGL((ntt_row_kernel<FWD, 7>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((ntt_row_kernel<FWD, 8>), grid, block, 0, st, a); break;
+  }
+}
+
+}  // namespace
+
+// Split of logN into column (SA) and row (SB) sub-transform sizes.
+void ntt_split(int logN, int* SA, int* SB) {
+  *SA = logN / 2;
+  *SB = logN - *SA;
+}
+
+void launch_ntt(u64* data, size_t bstride, int batch, RowMap rm, int logN, bool forward, const NttTables& tw,
+                hipStream_t st) {
+  launch_ntt(data, bstride, data, bstride, batch, rm, logN, forward, tw, st);
+}
+
+void launch_ntt(const u64* src, size_t sstride, u64* data, size_t bstride, int batch, RowMap rm, int logN, bool forward,
+                const NttTables& tw, hipStream_t st) {
+  const int rows = rm.nact();
+  if (rows <= 0 || batch <= 0) return;
+  int SA, SB;
+  ntt_split(logN, &SA, &SB);
+  NttArgs a{};
+  a.src = src; a.sstride = sstride; a.data = data; a.bstride = bstride; a.rm = rm; a.mods = tw.mods;
+  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN; a.SA = SA; a.SB = SB;
+  a.tw = reinterpret_cast<const uint4*>(forward ? tw.tw : tw.itw);
+  // column pass: P = 2^(SA-4) threads per column, nsub columns per workgroup
+  const int PA = 1 << (SA - 4), C = 1 << SB, R = 1 << SA;
+  const int nsubA = std::min(NTT_TPB / PA, C);
+  const int PB = 1 << (SB - 4);
+  const int nsubB = std::min(NTT_TPB / PB, R);
+  NttArgs aA = a; aA.nsub = nsubA;
+  NttArgs aB = a; aB.nsub = nsubB;
+  // only the first pass reads src
+  if (forward) { aB.src = data; aB.sstride = bstride; } else { aA.src = data; aA.sstride = bstride; }
+  dim3 gridA(C / nsubA, rows, batch), blockA(PA * nsubA);
+  dim3 gridB(R / nsubB, rows, batch), blockB(PB * nsubB);
+  if (forward) {
+    launch_col<true>(SA, gridA, blockA, aA, st);
+    launch_row<true>(SB, gridB, blockB, aB, st);
+  } else {
+    launch_row<false>(SB, gridB, blockB, aB, st);
+    launch_col<false>(SA, gridA, blockA, aA, st);
+  }
+}

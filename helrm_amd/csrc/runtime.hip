@@ -229,7 +229,7 @@ struct LinTrans {
   std::vector<std::vector<int>> baby;    // sorted babies per group
   std::vector<int> plain_idx;            // diagonal index of each stored plaintext
   DU64 diags;                            // [np][level+1+K][N], Montgomery form
-  DevArray<uint64_t> d_gmask; DevArray<int> d_gpidx, d_bzero, d_bslot;
+  DevArray<int> d_gpi, d_bzero, d_bslot;  // [ng][nbaby] plaintext index (-1 absent); per-baby flags
   double scale = 0;
   // device arrays of key / permutation pointers (baby and giant rotations), built on first use
   DevArray<const u64*> d_bkey, d_gkey; DevArray<const uint32_t*> d_bperm, d_gperm; DevArray<int> d_tg;
@@ -246,7 +246,7 @@ struct Scheme {
   std::vector<u64> mod;
   hipStream_t st = nullptr;
   DevArray<ModC> d_mods;
-  DU64 w, wp, iw, iwp, ninv, ninvp;
+  DU64 tw2, itw2, ninv, ninvp;  // interleaved (w, w') twiddle pairs [mod][N][2]
   NttTables tw{};
   std::vector<ModC> hmods;
   // per-modulus constants (Shoup pairs indexed by modulus)
@@ -281,9 +281,9 @@ void sync() { HCHECK(hipStreamSynchronize(sch().st)); }
 template <class T> void upload(T* d, const T* h, size_t n) { HCHECK(hipMemcpyAsync(d, h, n * sizeof(T), hipMemcpyHostToDevice, sch().st)); HCHECK(hipStreamSynchronize(sch().st)); }
 template <class T> void download(T* h, const T* d, size_t n) { HCHECK(hipMemcpyAsync(h, d, n * sizeof(T), hipMemcpyDeviceToHost, sch().st)); HCHECK(hipStreamSynchronize(sch().st)); }
 void d2d(void* dst, const void* src, size_t bytes) { if (bytes) HCHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, sch().st)); }
-void d2d_2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width, size_t height) {
-  if (height == 1) { d2d(dst, src, width); return; }
-  if (width && height) HCHECK(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height, hipMemcpyDeviceToDevice, sch().st));
+// batched strided copy of `words` u64 per batch entry (own kernel: one launch, 16 B per lane)
+void copy_rows(u64* dst, size_t dstride, const u64* src, size_t sstride, size_t words, int batch) {
+  launch_copy(dst, dstride, src, sstride, words, batch, sch().st);
 }
 
 RowMap rows_q(int l) { return RowMap{l + 1, l + 1, 0, 0, 0, 0}; }
@@ -293,6 +293,10 @@ RowMap rows_all() { Scheme& s = sch(); return RowMap{s.L + s.K, s.L + s.K, 0, 0,
 inline int qp_mod(int l, int k) { Scheme& s = sch(); return k <= l ? k : s.L + (k - l - 1); }
 
 void ntt(u64* d, size_t bstride, int batch, RowMap rm, bool fwd) { Scheme& s = sch(); launch_ntt(d, bstride, batch, rm, s.logN, fwd, s.tw, s.st); }
+void ntt_oop(const u64* src, size_t sstride, u64* dst, size_t dstride, int batch, RowMap rm, bool fwd) {
+  Scheme& s = sch();
+  launch_ntt(src, sstride, dst, dstride, batch, rm, s.logN, fwd, s.tw, s.st);
+}
 
 // timing of named launches (HIP events on the scheme stream)
 template <class F> void timed(const char* name, F&& f) {
@@ -382,8 +386,7 @@ void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* di
   const int N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
   const size_t dstride = (size_t)dn * nqp * N;
   DU64 coef((size_t)batch * (l + 1) * N);
-  d2d_2d(coef.p, (size_t)(l + 1) * N * 8, c1, c1_bstride * 8, (size_t)(l + 1) * N * 8, batch);
-  ntt(coef.p, (size_t)(l + 1) * N, batch, rows_q(l), false);
+  ntt_oop(c1, c1_bstride, coef.p, (size_t)(l + 1) * N, batch, rows_q(l), false);
   for (int d = 0; d < dn; d++) {
     int st0 = d * K, en = std::min(st0 + K, l + 1), ns = en - st0;
     BConvHost& bt = bconv_table(st0, en);
@@ -391,7 +394,7 @@ void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* di
     for (int k = 0; k < nqp; k++) if (k < st0 || k >= en) { rl.row[rl.n] = (short)k; rl.mod[rl.n] = (short)qp_mod(l, k); rl.n++; }
     u64* D = digits + (size_t)d * nqp * N;
     launch_bconv(coef.p + (size_t)st0 * N, (size_t)(l + 1) * N, ns, bt.tab, D, dstride, batch, rl, s.d_mods.p, N, ns == 1, s.st);
-    d2d_2d(D + (size_t)st0 * N, dstride * 8, c1 + (size_t)st0 * N, c1_bstride * 8, (size_t)ns * N * 8, batch);
+    copy_rows(D + (size_t)st0 * N, dstride, c1 + (size_t)st0 * N, c1_bstride, (size_t)ns * N, batch);
     RowMap rm{nqp, l + 1, 0, s.L, st0, en};
     ntt(D, dstride, batch, rm, true);
   }
@@ -402,8 +405,8 @@ void mod_down(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t
   Scheme& s = sch();
   const int N = s.N, K = s.K;
   DU64 pc((size_t)batch * K * N), ext((size_t)batch * (l + 1) * N);
-  d2d_2d(pc.p, (size_t)K * N * 8, x + (size_t)(l + 1) * N, x_bstride * 8, (size_t)K * N * 8, batch);
-  ntt(pc.p, (size_t)K * N, batch, rows_p(), false);
+  // P rows of x (rows l+1.. of each batch entry) -> coefficient domain in pc
+  ntt_oop(x + (size_t)(l + 1) * N, x_bstride, pc.p, (size_t)K * N, batch, rows_p(), false);
   BConvHost& bt = bconv_table(s.L, s.L + K);
   RowList rl{}; rl.n = l + 1;
   for (int i = 0; i <= l; i++) { rl.row[i] = (short)i; rl.mod[i] = (short)i; }
@@ -684,7 +687,7 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
       s.hmods[m] = ModC{qq, (u64)0 - inv, mulmod(rmod, rmod, qq), rmod};
     }
     s.d_mods = DevArray<ModC>(nm); upload(s.d_mods.p, s.hmods.data(), nm);
-    std::vector<u64> hw((size_t)nm * N), hwp((size_t)nm * N), hiw((size_t)nm * N), hiwp((size_t)nm * N), hn(nm), hnp(nm);
+    std::vector<u64> htw((size_t)nm * N * 2), hitw((size_t)nm * N * 2), hn(nm), hnp(nm);
     for (int m = 0; m < nm; m++) {
       u64 qq = s.mod[m];
       u64 g = smallest_generator(qq);
@@ -694,14 +697,15 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
       for (int i = 1; i < N; i++) { pw[i] = mulmod(pw[i - 1], psi, qq); ipw[i] = mulmod(ipw[i - 1], ipsi, qq); }
       for (int i = 0; i < N; i++) {
         int r = brv(i, logN);
-        hw[(size_t)m * N + i] = pw[r]; hwp[(size_t)m * N + i] = shoup(pw[r], qq);
-        hiw[(size_t)m * N + i] = ipw[r]; hiwp[(size_t)m * N + i] = shoup(ipw[r], qq);
+        const size_t o = ((size_t)m * N + i) * 2;
+        htw[o] = pw[r]; htw[o + 1] = shoup(pw[r], qq);
+        hitw[o] = ipw[r]; hitw[o + 1] = shoup(ipw[r], qq);
       }
       hn[m] = invmod((u64)N, qq); hnp[m] = shoup(hn[m], qq);
     }
     auto up = [&](DU64& d, const std::vector<u64>& h) { d = DU64(h.size()); upload(d.p, h.data(), h.size()); };
-    up(s.w, hw); up(s.wp, hwp); up(s.iw, hiw); up(s.iwp, hiwp); up(s.ninv, hn); up(s.ninvp, hnp);
-    s.tw = NttTables{s.d_mods.p, s.w.p, s.wp.p, s.iw.p, s.iwp.p, s.ninv.p, s.ninvp.p};
+    up(s.tw2, htw); up(s.itw2, hitw); up(s.ninv, hn); up(s.ninvp, hnp);
+    s.tw = NttTables{s.d_mods.p, s.tw2.p, s.itw2.p, s.ninv.p, s.ninvp.p};
     std::vector<u64> pm(nm), pmp(nm), pin(nm), pinp(nm), p0i(nm), p0ip(nm), pmr(nm);
     for (int m = 0; m < nm; m++) {
       u64 qq = s.mod[m], P = 1;
@@ -750,7 +754,7 @@ void ct_drop_to(Cipher& c, int level) {
   Scheme& s = sch();
   if (c.level == level) return;
   DU64 d((size_t)2 * (level + 1) * s.N);
-  d2d_2d(d.p, (size_t)(level + 1) * s.N * 8, c.d.p, (size_t)(c.level + 1) * s.N * 8, (size_t)(level + 1) * s.N * 8, 2);
+  copy_rows(d.p, (size_t)(level + 1) * s.N, c.d.p, (size_t)(c.level + 1) * s.N, (size_t)(level + 1) * s.N, 2);
   c.d = std::move(d); c.level = level;
 }
 
@@ -779,8 +783,7 @@ std::unique_ptr<Cipher> rescale_ct(const Cipher& ct) {
   const int l = ct.level, N = s.N;
   REQUIRE(l >= 1, "cannot rescale: ciphertext already at level 0");
   DU64 u((size_t)2 * N), t((size_t)2 * l * N);
-  d2d_2d(u.p, (size_t)N * 8, ct.d.p + (size_t)l * N, (size_t)(l + 1) * N * 8, (size_t)N * 8, 2);
-  ntt(u.p, N, 2, RowMap{1, 1, l, 0, 0, 0}, false);
+  ntt_oop(ct.d.p + (size_t)l * N, (size_t)(l + 1) * N, u.p, N, 2, RowMap{1, 1, l, 0, 0, 0}, false);
   launch_rescale_spread(t.p, u.p, l, s.mod[l] >> 1, s.d_mods.p, N, s.st);
   ntt(t.p, (size_t)l * N, 2, rows_q(l - 1), true);
   auto out = new_ct(l - 1, ct.scale / (double)s.mod[l]); out->logslots = ct.logslots;
@@ -900,16 +903,16 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
   for (auto& o : order) t->plain_idx.push_back(o.first);
   if (!t->naive) {
     const int ng = (int)t->giant.size(), nb = (int)t->rot2.size();
-    std::vector<uint64_t> gmask(ng, 0); std::vector<int> gpidx(ng, 0), bzero(nb, 0), bslot(nb, 0);
+    std::vector<int> gpi((size_t)ng * nb, -1), bzero(nb, 0), bslot(nb, 0);
     int pidx = 0;
-    for (int g = 0; g < ng; g++) {
-      gpidx[g] = pidx;
-      for (int b : t->baby[g]) { int pos = (int)(std::lower_bound(t->rot2.begin(), t->rot2.end(), b) - t->rot2.begin()); gmask[g] |= 1ULL << pos; pidx++; }
-    }
+    for (int g = 0; g < ng; g++)
+      for (int b : t->baby[g]) {
+        int pos = (int)(std::lower_bound(t->rot2.begin(), t->rot2.end(), b) - t->rot2.begin());
+        gpi[(size_t)g * nb + pos] = pidx++;
+      }
     int slot = 0;
     for (int i = 0; i < nb; i++) { bzero[i] = t->rot2[i] == 0; bslot[i] = t->rot2[i] == 0 ? 0 : slot++; }
-    t->d_gmask = DevArray<uint64_t>(ng); upload(t->d_gmask.p, gmask.data(), ng);
-    t->d_gpidx = DevArray<int>(ng); upload(t->d_gpidx.p, gpidx.data(), ng);
+    t->d_gpi = DevArray<int>(gpi.size()); upload(t->d_gpi.p, gpi.data(), gpi.size());
     t->d_bzero = DevArray<int>(nb); upload(t->d_bzero.p, bzero.data(), nb);
     t->d_bslot = DevArray<int>(nb); upload(t->d_bslot.p, bslot.data(), nb);
   }
@@ -973,7 +976,7 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct) {
     a.diag = t.diags.p; a.diag_stride = (size_t)(t.level + 1 + K) * N;
     a.R = R.p; a.R_bstride = 2 * qp; a.R_pstride = qp;
     a.pc = pc.p; a.pc_pstride = (size_t)(l + 1) * N;
-    a.baby_is_zero = t.d_bzero.p; a.baby_slot = t.d_bslot.p; a.gmask = t.d_gmask.p; a.gpidx = t.d_gpidx.p;
+    a.baby_is_zero = t.d_bzero.p; a.baby_slot = t.d_bslot.p; a.gpi = t.d_gpi.p;
     a.T = T.p; a.T_gstride = 2 * qp; a.T_pstride = qp; a.mods = s.d_mods.p;
     a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.lt_level = t.level; a.ng = ng; a.nbaby = nb;
     for (int b0 = 0; b0 < nb; b0 += 32) {
