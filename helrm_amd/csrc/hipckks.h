@@ -63,6 +63,37 @@ __device__ __forceinline__ void mac_lazy(u64& lo, u64& hi, u64 a, u64 b, u64 q) 
   lo = nlo;
   hi = hi >= q ? hi - q : hi;
 }
+// Exact sum of up to 16 products of words below 2^62, in column form:
+//   sum = s0 + s1*2^32 + (s2 + c0)*2^64 + c1*2^96
+// s0 collects a0*b0, s1 collects a0*b1 + a1*b0, s2 collects a1*b1 (32-bit
+// halves); c0 and c1 count the carries out of s0 and s1, taken from the
+// carry-out of v_mad_u64_u32.  Seven VALU instructions per product (the
+// carry reads sit three or more instructions after their writes).  s2 cannot
+// overflow: a1, b1 < 2^30, so 16 products stay below 2^64.
+struct Acc128 { u64 s0, s1, s2; uint32_t c0, c1; };
+__device__ __forceinline__ void acc_zero(Acc128& A) { A.s0 = A.s1 = A.s2 = 0; A.c0 = A.c1 = 0; }
+__device__ __forceinline__ void acc_mac(Acc128& A, u64 a, u64 b) {
+  const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32), b0 = (uint32_t)b, b1 = (uint32_t)(b >> 32);
+  u64 ca, cb, cc, cd;
+  // not volatile: a pure function of its operands, free to be scheduled
+  asm(
+      "v_mad_u64_u32 %[s0], %[ca], %[a0], %[b0], %[s0]\n\t"
+      "v_mad_u64_u32 %[s1], %[cb], %[a0], %[b1], %[s1]\n\t"
+      "v_mad_u64_u32 %[s1], %[cc], %[a1], %[b0], %[s1]\n\t"
+      "v_mad_u64_u32 %[s2], %[cd], %[a1], %[b1], %[s2]\n\t"
+      "v_addc_co_u32_e64 %[c0], %[cd], 0, %[c0], %[ca]\n\t"
+      "v_addc_co_u32_e64 %[c1], %[cd], 0, %[c1], %[cb]\n\t"
+      "v_addc_co_u32_e64 %[c1], %[cd], 0, %[c1], %[cc]"
+      : [s0] "+v"(A.s0), [s1] "+v"(A.s1), [s2] "+v"(A.s2), [c0] "+v"(A.c0), [c1] "+v"(A.c1),
+        [ca] "=&s"(ca), [cb] "=&s"(cb), [cc] "=&s"(cc), [cd] "=&s"(cd)
+      : [a0] "v"(a0), [a1] "v"(a1), [b0] "v"(b0), [b1] "v"(b1));
+}
+// the 128-bit value (lo, hi) of an accumulator
+__device__ __forceinline__ void acc_value(const Acc128& A, u64& lo, u64& hi) {
+  const u64 t = A.s1 << 32;
+  lo = A.s0 + t;
+  hi = A.s2 + A.c0 + (A.s1 >> 32) + ((u64)A.c1 << 32) + (lo < t ? 1 : 0);
+}
 // Montgomery reduction of T = hi*2^64 + lo < q*2^64: returns T * 2^-64 mod q.
 __device__ __forceinline__ u64 redc(u64 lo, u64 hi, u64 q, u64 qinv) {
   u64 m = lo * qinv;

@@ -28,6 +28,8 @@ struct KeyMacArgs {
   const u64* key1;         // single-batch key
   const uint32_t* perm1;   // single-batch permutation (nullptr: identity)
   const u64* add0;         // Q rows added to part 0 before the gather (mode 1)
+  const u64* own;          // the decomposed polynomial (NTT, Q rows; per batch if digits_per_batch): a
+  size_t own_bstride;      // digit's own rows are read from it (nullptr: from the digit buffer)
   u64 *out0, *out1;
   size_t out_bstride;
   const ModC* mods;
@@ -41,6 +43,8 @@ struct GiantAccArgs {
   const uint32_t* const* perm; // [ng]
   const int* tg;               // giant-group index into T per key-switched group
   int ng;
+  const u64* own;              // [ng][l+1][N] decomposed polynomials (own digit rows), or nullptr
+  size_t own_bstride;
   const u64* T;                // [ngroups][2][nqp][N]
   size_t T_gstride, T_pstride;
   int t_zero;                  // index of the rotation-0 group in T, or -1
@@ -58,7 +62,9 @@ struct DiagMacArgs {
   size_t pc_pstride;
   const int* baby_is_zero;  // [nbaby]
   const int* baby_slot;     // [nbaby]
-  const int* gpi;           // [ng][nbaby] plaintext index of baby b in group g, -1 if absent
+  const int* gpi;           // [ng][nbaby] plaintext index of baby b in group g (absent: a zero plaintext)
+  int dense;                // every group holds every baby: index = g * nbaby + b
+  int zero_pidx;            // index of the all-zero plaintext (babies past nbaby in a chunk use it)
   u64* T;                   // [ng][2][nqp][N]
   size_t T_gstride, T_pstride;
   const ModC* mods;

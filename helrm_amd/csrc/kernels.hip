@@ -118,10 +118,13 @@ void launch_copy(u64* dst, size_t dstride, const u64* src, size_t sstride, size_
 // exact in 128 bits (folded below 4t after every 16 products), then one
 // Montgomery REDC removes the 2^64 the (S/s_i mod t) table carries.
 // ---------------------------------------------------------------------------
-template <int MAXS>
-__global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, size_t in_bstride, int ns,
+// NS > 0: exactly NS sources (the constants of a destination row are one
+// scalar load); NS == 0: ns sources at run time, at most MAXS.
+template <int MAXS, int NS>
+__global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, size_t in_bstride, int ns_rt,
                                                     BConvTable tab, u64* __restrict__ out, size_t out_bstride,
                                                     RowList rl, const ModC* __restrict__ mods, int N, int force_v0) {
+  const int ns = NS > 0 ? NS : ns_rt;
   const int x = blockIdx.x * blockDim.x + threadIdx.x;
   const u64* inb = in + (size_t)blockIdx.z * in_bstride;
   u64* outb = out + (size_t)blockIdx.z * out_bstride;
@@ -142,14 +145,16 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
   for (int r = r0; r < r1; r++) {
     const int m = rl.mod[r];
     const ModC mc = mods[m];
-    const u64* h = tab.hat + (size_t)m * ns;
+    const u64* __restrict__ h = tab.hat + (size_t)m * ns;
+    // exact 128-bit sums of 16 products (words < 2^62), folded below q
     u128 acc = 0;
 #pragma unroll
-    for (int i = 0; i < MAXS; i++) {
-      if (i < ns) {
-        if (i > 0 && (i & 15) == 0) acc = ((u128)fold_hi4((u64)(acc >> 64), mc.q) << 64) | (u64)acc;
-        acc += (u128)y[i] * h[i];
-      }
+    for (int i0 = 0; i0 < MAXS; i0 += 16) {
+      u128 part = 0;
+#pragma unroll
+      for (int i = i0; i < i0 + 16 && i < MAXS; i++)
+        if (i < ns) part += (u128)y[i] * h[i];
+      acc += ((u128)fold_hi4((u64)(part >> 64), mc.q) << 64) | (u64)part;
     }
     u64 res = redc((u64)acc, fold_hi4((u64)(acc >> 64), mc.q), mc.q, mc.qinv);
     res = sub_mod(res, tab.vS[(size_t)m * (ns + 1) + v], mc.q);
@@ -167,12 +172,15 @@ void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable& ta
   t.rows_per_block = (rl.n + ny - 1) / ny;
   ny = (rl.n + t.rows_per_block - 1) / t.rows_per_block;
   dim3 grid(cols, ny, batch);
-  if (ns <= 8)
-    hipLaunchKernelGGL((bconv_kernel<8>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, force_v0 ? 1 : 0);
+  const int fv = force_v0 ? 1 : 0;
+  if (ns == 8)
+    hipLaunchKernelGGL((bconv_kernel<8, 8>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, fv);
+  else if (ns < 8)
+    hipLaunchKernelGGL((bconv_kernel<8, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, fv);
   else if (ns <= 16)
-    hipLaunchKernelGGL((bconv_kernel<16>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, force_v0 ? 1 : 0);
+    hipLaunchKernelGGL((bconv_kernel<16, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, fv);
   else
-    hipLaunchKernelGGL((bconv_kernel<HCK_MAXSRC>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, force_v0 ? 1 : 0);
+    hipLaunchKernelGGL((bconv_kernel<HCK_MAXSRC, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, fv);
 }
 
 // ModDown combine: out = (x - ext) * P^-1 (+ add) [gathered through perm]
@@ -208,29 +216,38 @@ void launch_moddown_combine(u64* out, size_t o_bstride, const u64* x, size_t x_b
 // Keys are in Montgomery form; the sum is accumulated lazily in 128 bits.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void keymac_kernel(KeyMacArgs a) {
-  int i = blockIdx.x * blockDim.x + threadIdx.x;
-  int k = blockIdx.y, b = blockIdx.z;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int k = blockIdx.y, b = blockIdx.z;
   const int N = a.N;
   const uint32_t* perm = a.perm ? a.perm[b] : a.perm1;
   const u64* key = a.key ? a.key[b] : a.key1;
-  int src = perm ? (int)perm[i] : i;
-  int kl = k <= a.l ? k : a.L + (k - a.l - 1);
-  ModC mc = a.mods[kl];
-  const u64* dg = a.digits + (size_t)(a.digits_per_batch ? b : 0) * a.dig_bstride;
-  u64 lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+  const int src = perm ? (int)perm[i] : i;
+  const int kl = k <= a.l ? k : a.L + (k - a.l - 1);
+  const ModC mc = a.mods[kl];
+  const size_t db = (size_t)(a.digits_per_batch ? b : 0);
+  const u64* dg = a.digits + db * a.dig_bstride;
+  // the digit owning Q row k reads it from the decomposed polynomial itself
+  const int own_d = (a.own && k <= a.l) ? k / a.K : -1;
+  const u64* own = a.own ? a.own + db * a.own_bstride + (size_t)k * N : nullptr;
   const size_t kstride = (size_t)(a.L + a.K) * N;
+  Acc128 A0, A1;
+  acc_zero(A0); acc_zero(A1);
   for (int d = 0; d < a.dn; d++) {
-    u64 x = dg[((size_t)d * a.nqp + k) * N + src];
+    const u64 x = d == own_d ? own[src] : dg[((size_t)d * a.nqp + k) * N + src];
     const u64* kb = key + (size_t)d * 2 * kstride + (size_t)kl * N + src;
-    mac_lazy(lo0, hi0, x, kb[0], mc.q);
-    mac_lazy(lo1, hi1, x, kb[kstride], mc.q);
+    acc_mac(A0, x, kb[0]);
+    acc_mac(A1, x, kb[kstride]);
   }
+  u64 lo0, hi0, lo1, hi1;
+  acc_value(A0, lo0, hi0);
+  acc_value(A1, lo1, hi1);
+  hi0 = fold_hi4(hi0, mc.q);
+  hi1 = fold_hi4(hi1, mc.q);
   // add0 enters the high word (v*2^64 == v*R mod q), so the REDC below returns sum + add0
   if (a.add0 && k <= a.l) hi0 = add_mod(hi0, a.add0[(size_t)k * N + src], mc.q);
-  u64 r0 = redc(lo0, hi0, mc.q, mc.qinv), r1 = redc(lo1, hi1, mc.q, mc.qinv);
-  size_t o = (size_t)b * a.out_bstride + (size_t)k * N + i;
-  a.out0[o] = r0;
-  a.out1[o] = r1;
+  const size_t o = (size_t)b * a.out_bstride + (size_t)k * N + i;
+  a.out0[o] = redc(lo0, hi0, mc.q, mc.qinv);
+  a.out1[o] = redc(lo1, hi1, mc.q, mc.qinv);
 }
 void launch_keymac(const KeyMacArgs& a, int batch, hipStream_t st) {
   if (batch <= 0) return;
@@ -244,36 +261,61 @@ void launch_keymac(const KeyMacArgs& a, int batch, hipStream_t st) {
 // plus the untransformed group (rotation 0) if present.  Everything folds
 // into one lazy 128-bit accumulator per part: T0 is added to the high word
 // (value*2^64 == value*R), so a single REDC finishes the row.
+// running sum (lo, hi < q) += 128-bit column accumulator A, then A = 0
+__device__ __forceinline__ void acc_flush(Acc128& A, u64& tlo, u64& thi, u64 q) {
+  u64 lo, hi;
+  acc_value(A, lo, hi);
+  hi = fold_hi4(hi, q);
+  tlo += lo;
+  const u64 c = tlo < lo ? 1 : 0;
+  thi = csub64(add_mod(thi, hi, q) + c, q);
+  acc_zero(A);
+}
 __global__ __launch_bounds__(256) void giant_acc_kernel(GiantAccArgs a) {
-  int i = blockIdx.x * blockDim.x + threadIdx.x;
-  int k = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int k = blockIdx.y;
   const int N = a.N;
-  int kl = k <= a.l ? k : a.L + (k - a.l - 1);
-  ModC mc = a.mods[kl];
-  u64 lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+  const int kl = k <= a.l ? k : a.L + (k - a.l - 1);
+  const ModC mc = a.mods[kl];
+  const int own_d = (a.own && k <= a.l) ? k / a.K : -1;
   const size_t kstride = (size_t)(a.L + a.K) * N;
+  Acc128 A0, A1;
+  acc_zero(A0); acc_zero(A1);
+  u64 tlo0 = 0, thi0 = 0, tlo1 = 0, thi1 = 0, t0 = 0;
+  int cnt = 0;
   for (int g = 0; g < a.ng; g++) {
+    if (cnt + a.dn > 16) {
+      acc_flush(A0, tlo0, thi0, mc.q);
+      acc_flush(A1, tlo1, thi1, mc.q);
+      cnt = 0;
+    }
     const uint32_t* perm = a.perm[g];
     const u64* key = a.key[g];
-    int src = (int)perm[i];
+    const int src = (int)perm[i];
     const u64* dg = a.digits + (size_t)g * a.dig_bstride;
+    const u64* own = a.own ? a.own + (size_t)g * a.own_bstride + (size_t)k * N : nullptr;
     for (int d = 0; d < a.dn; d++) {
-      u64 x = dg[((size_t)d * a.nqp + k) * N + src];
+      const u64 x = d == own_d ? own[src] : dg[((size_t)d * a.nqp + k) * N + src];
       const u64* kb = key + (size_t)d * 2 * kstride + (size_t)kl * N + src;
-      mac_lazy(lo0, hi0, x, kb[0], mc.q);
-      mac_lazy(lo1, hi1, x, kb[kstride], mc.q);
+      acc_mac(A0, x, kb[0]);
+      acc_mac(A1, x, kb[kstride]);
     }
+    cnt += a.dn;
     const u64* T0 = a.T + (size_t)a.tg[g] * a.T_gstride;
-    hi0 = add_mod(hi0, T0[(size_t)k * N + src], mc.q);
+    t0 = add_mod(t0, T0[(size_t)k * N + src], mc.q);
   }
+  acc_flush(A0, tlo0, thi0, mc.q);
+  acc_flush(A1, tlo1, thi1, mc.q);
+  // T0 terms enter the high word (v*2^64 == v*R mod q)
+  thi0 = add_mod(thi0, t0, mc.q);
   if (a.t_zero >= 0) {
-    const u64* T0 = a.T + (size_t)a.t_zero * a.T_gstride;
-    hi0 = add_mod(hi0, T0[(size_t)k * N + i], mc.q);
-    hi1 = add_mod(hi1, T0[a.T_pstride + (size_t)k * N + i], mc.q);
+    const u64* Tz = a.T + (size_t)a.t_zero * a.T_gstride;
+    thi0 = add_mod(thi0, Tz[(size_t)k * N + i], mc.q);
+    thi1 = add_mod(thi1, Tz[a.T_pstride + (size_t)k * N + i], mc.q);
   }
-  size_t o = (size_t)k * N + i;
-  a.out0[o] = redc(lo0, hi0, mc.q, mc.qinv);
-  a.out1[o] = redc(lo1, hi1, mc.q, mc.qinv);
+  const size_t o = (size_t)k * N + i;
+  a.out0[o] = redc(tlo0, thi0, mc.q, mc.qinv);
+  a.out1[o] = redc(tlo1, thi1, mc.q, mc.qinv);
 }
 void launch_giant_acc(const GiantAccArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(giant_acc_kernel, dim3(a.N / 256, a.nqp, 1), dim3(256), 0, st, a);
@@ -293,7 +335,48 @@ void launch_giant_acc(const GiantAccArgs& a, hipStream_t st) {
 // diagonals carry.
 // ---------------------------------------------------------------------------
 
+// Plaintext index of baby b (chunk-relative) of group g: dense transforms
+// (every group holds every baby of the chunk) store them group-major; the
+// others use the index table, where an absent baby points at a zero plaintext.
+template <bool DENSE>
+__device__ __forceinline__ int mac_pidx(const DiagMacArgs& a, int g, int b) {
+  if (DENSE) return g * a.nbaby + a.b0 + b;  // launched only when b0 + NB <= nbaby
+  const int bb = a.b0 + b;
+  return bb < a.nbaby ? a.gpi[(size_t)g * a.nbaby + bb] : a.zero_pidx;
+}
+template <int NB, bool DENSE>
+__device__ __forceinline__ void mac_load(const DiagMacArgs& a, const u64* dbase, int g, u64 (&d)[NB]) {
+#pragma unroll
+  for (int b = 0; b < NB; b++) d[b] = dbase[(size_t)mac_pidx<DENSE>(a, g, b) * a.diag_stride];
+}
 template <int NB>
+__device__ __forceinline__ void mac_group(const DiagMacArgs& a, const u64 (&d)[NB], const u64 (&s0)[NB], const u64 (&s1)[NB],
+                                          const ModC& mc, u64* T) {
+  // exact column sums of 16 products; chunks of 16 are reduced to (lo, hi < q)
+  u128 tot0 = 0, tot1 = 0;
+#pragma unroll
+  for (int c = 0; c < NB; c += 16) {
+    Acc128 A0, A1;
+    acc_zero(A0); acc_zero(A1);
+#pragma unroll
+    for (int b = c; b < c + 16 && b < NB; b++) {
+      acc_mac(A0, d[b], s0[b]);
+      acc_mac(A1, d[b], s1[b]);
+    }
+    u64 lo0, hi0, lo1, hi1;
+    acc_value(A0, lo0, hi0);
+    acc_value(A1, lo1, hi1);
+    tot0 += ((u128)fold_hi4(hi0, mc.q) << 64) | lo0;
+    tot1 += ((u128)fold_hi4(hi1, mc.q) << 64) | lo1;
+  }
+  u64 r0 = redc((u64)tot0, fold_hi4((u64)(tot0 >> 64), mc.q), mc.q, mc.qinv);
+  u64 r1 = redc((u64)tot1, fold_hi4((u64)(tot1 >> 64), mc.q), mc.q, mc.qinv);
+  if (a.b0 > 0) { r0 = add_mod(r0, T[0], mc.q); r1 = add_mod(r1, T[a.T_pstride], mc.q); }
+  T[0] = r0;
+  T[a.T_pstride] = r1;
+}
+
+template <int NB, bool DENSE>
 __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
   const int x = blockIdx.x * blockDim.x + threadIdx.x;
   const int k = blockIdx.y;
@@ -317,47 +400,25 @@ __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
       }
     }
   }
-  u64 dc[NB], dn[NB];
-#pragma unroll
-  for (int b = 0; b < NB; b++) {
-    const int bb = a.b0 + b;
-    const int pi = bb < a.nbaby ? a.gpi[bb] : -1;
-    dc[b] = pi >= 0 ? dbase[(size_t)pi * a.diag_stride] : 0;
-  }
-  for (int g = 0; g < a.ng; g++) {
-    if (g + 1 < a.ng) {
-#pragma unroll
-      for (int b = 0; b < NB; b++) {
-        const int bb = a.b0 + b;
-        const int pi = bb < a.nbaby ? a.gpi[(size_t)(g + 1) * a.nbaby + bb] : -1;
-        dn[b] = pi >= 0 ? dbase[(size_t)pi * a.diag_stride] : 0;
-      }
-    }
-    u128 acc0 = 0, acc1 = 0;
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-      if (b > 0 && (b & 15) == 0) {
-        acc0 = ((u128)fold_hi4((u64)(acc0 >> 64), mc.q) << 64) | (u64)acc0;
-        acc1 = ((u128)fold_hi4((u64)(acc1 >> 64), mc.q) << 64) | (u64)acc1;
-      }
-      acc0 += (u128)dc[b] * s0[b];
-      acc1 += (u128)dc[b] * s1[b];
-    }
-    u64 r0 = redc((u64)acc0, fold_hi4((u64)(acc0 >> 64), mc.q), mc.q, mc.qinv);
-    u64 r1 = redc((u64)acc1, fold_hi4((u64)(acc1 >> 64), mc.q), mc.q, mc.qinv);
-    u64* T = a.T + (size_t)g * a.T_gstride + (size_t)k * N + x;
-    if (a.b0 > 0) { r0 = add_mod(r0, T[0], mc.q); r1 = add_mod(r1, T[a.T_pstride], mc.q); }
-    T[0] = r0;
-    T[a.T_pstride] = r1;
-#pragma unroll
-    for (int b = 0; b < NB; b++) dc[b] = dn[b];
+  // ping-pong: the next group's NB diagonals are in flight while a group is multiplied
+  u64 dA[NB], dB[NB];
+  u64* Tb = a.T + (size_t)k * N + x;
+  mac_load<NB, DENSE>(a, dbase, 0, dA);
+  for (int g = 0; g < a.ng; g += 2) {
+    if (g + 1 < a.ng) mac_load<NB, DENSE>(a, dbase, g + 1, dB);
+    mac_group<NB>(a, dA, s0, s1, mc, Tb + (size_t)g * a.T_gstride);
+    if (g + 1 >= a.ng) break;
+    if (g + 2 < a.ng) mac_load<NB, DENSE>(a, dbase, g + 2, dA);
+    mac_group<NB>(a, dB, s0, s1, mc, Tb + (size_t)(g + 1) * a.T_gstride);
   }
 }
 void launch_diag_mac(const DiagMacArgs& a, hipStream_t st) {
   dim3 grid(a.N / 256, a.nqp, 1);
-  if (a.nb_chunk <= 8) hipLaunchKernelGGL((diag_mac_kernel<8>), grid, dim3(256), 0, st, a);
-  else if (a.nb_chunk <= 16) hipLaunchKernelGGL((diag_mac_kernel<16>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((diag_mac_kernel<32>), grid, dim3(256), 0, st, a);
+  const bool dense = a.dense && a.nb_chunk == 16 && a.b0 + 16 <= a.nbaby;
+  if (dense) hipLaunchKernelGGL((diag_mac_kernel<16, true>), grid, dim3(256), 0, st, a);
+  else if (a.nb_chunk <= 8) hipLaunchKernelGGL((diag_mac_kernel<8, false>), grid, dim3(256), 0, st, a);
+  else if (a.nb_chunk <= 16) hipLaunchKernelGGL((diag_mac_kernel<16, false>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((diag_mac_kernel<32, false>), grid, dim3(256), 0, st, a);
 }
 
 // ---------------------------------------------------------------------------

@@ -229,7 +229,8 @@ struct LinTrans {
   std::vector<std::vector<int>> baby;    // sorted babies per group
   std::vector<int> plain_idx;            // diagonal index of each stored plaintext
   DU64 diags;                            // [np][level+1+K][N], Montgomery form
-  DevArray<int> d_gpi, d_bzero, d_bslot;  // [ng][nbaby] plaintext index (-1 absent); per-baby flags
+  DevArray<int> d_gpi, d_bzero, d_bslot;  // [ng][nbaby] plaintext index (absent: the zero plaintext); per-baby flags
+  bool dense = false;                     // every giant group holds every baby step
   double scale = 0;
   // device arrays of key / permutation pointers (baby and giant rotations), built on first use
   DevArray<const u64*> d_bkey, d_gkey; DevArray<const uint32_t*> d_bperm, d_gperm; DevArray<int> d_tg;
@@ -381,7 +382,8 @@ u64 galois_element(int k) { Scheme& s = sch(); u64 M = 2 * (u64)s.N; return powm
 // key switching building blocks
 // ============================================================================
 // digits[b][d][nqp][N] from c1 (NTT, Q rows 0..l) of batch b (stride c1_bstride)
-void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* digits) {
+// copy_own: also copy each digit's own rows (the key-product kernels can instead read them from c1)
+void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* digits, bool copy_own = true) {
   Scheme& s = sch();
   const int N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
   const size_t dstride = (size_t)dn * nqp * N;
@@ -394,7 +396,7 @@ void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* di
     for (int k = 0; k < nqp; k++) if (k < st0 || k >= en) { rl.row[rl.n] = (short)k; rl.mod[rl.n] = (short)qp_mod(l, k); rl.n++; }
     u64* D = digits + (size_t)d * nqp * N;
     launch_bconv(coef.p + (size_t)st0 * N, (size_t)(l + 1) * N, ns, bt.tab, D, dstride, batch, rl, s.d_mods.p, N, ns == 1, s.st);
-    copy_rows(D + (size_t)st0 * N, dstride, c1 + (size_t)st0 * N, c1_bstride, (size_t)ns * N, batch);
+    if (copy_own) copy_rows(D + (size_t)st0 * N, dstride, c1 + (size_t)st0 * N, c1_bstride, (size_t)ns * N, batch);
     RowMap rm{nqp, l + 1, 0, s.L, st0, en};
     ntt(D, dstride, batch, rm, true);
   }
@@ -668,6 +670,7 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
   s.logN = logN; s.N = 1 << logN; s.L = (int)q.size(); s.K = (int)p.size();
   s.dnum = (s.L + s.K - 1) / s.K; s.logscale = logscale; s.h = h; s.seed = seed;
   REQUIRE(s.K <= HCK_MAXSRC, "too many special primes");
+  REQUIRE(s.dnum <= 16, "at most 16 decomposition digits (len(Q) <= 16 * len(P))");
   s.mod = q; s.mod.insert(s.mod.end(), p.begin(), p.end());
   for (u64 m : s.mod) {
     REQUIRE(m < (1ULL << 62) && m > 2, "moduli must be < 2^62");
@@ -766,11 +769,12 @@ std::unique_ptr<Cipher> automorphism(const Cipher& ct, u64 galel, bool lt_keyset
   const int l = ct.level, N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
   const u64* key = key_ptr(galel, lt_keyset);
   DU64 digits((size_t)dn * nqp * N);
-  decompose_modup(l, ct.d.p + (size_t)(l + 1) * N, 0, 1, digits.p);
+  decompose_modup(l, ct.d.p + (size_t)(l + 1) * N, 0, 1, digits.p, false);
   DU64 dd((size_t)2 * nqp * N);
   KeyMacArgs a{};
   a.digits = digits.p; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = nullptr; a.perm = nullptr;
   a.key1 = key; a.perm1 = nullptr; a.add0 = nullptr;
+  a.own = ct.d.p + (size_t)(l + 1) * N; a.own_bstride = 0;
   a.out0 = dd.p; a.out1 = dd.p + (size_t)nqp * N; a.out_bstride = 0; a.mods = s.d_mods.p;
   a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
   launch_keymac(a, 1, s.st);
@@ -881,7 +885,9 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
       for (int b : t->baby[g]) { int di = t->giant[g] + b; order.push_back({di, src_of(di)}); rotv.push_back((-t->giant[g]) & (slots - 1)); }
   }
   const int np = (int)order.size(), nqp_lt = level + 1 + K;
-  t->diags = DU64((size_t)np * nqp_lt * N);
+  // one extra all-zero plaintext after the np diagonals: absent (group, baby) pairs point at it
+  t->diags = DU64((size_t)(np + 1) * nqp_lt * N);
+  HCHECK(hipMemsetAsync(t->diags.p + (size_t)np * nqp_lt * N, 0, (size_t)nqp_lt * N * 8, s.st));
   RowMap rm{nqp_lt, level + 1, 0, s.L, 0, 0};
   // host FFT in parallel, device residues + NTT + Montgomery conversion per batch
   const int chunk = 16;
@@ -903,13 +909,15 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
   for (auto& o : order) t->plain_idx.push_back(o.first);
   if (!t->naive) {
     const int ng = (int)t->giant.size(), nb = (int)t->rot2.size();
-    std::vector<int> gpi((size_t)ng * nb, -1), bzero(nb, 0), bslot(nb, 0);
+    std::vector<int> gpi((size_t)ng * nb, np), bzero(nb, 0), bslot(nb, 0);
     int pidx = 0;
     for (int g = 0; g < ng; g++)
       for (int b : t->baby[g]) {
         int pos = (int)(std::lower_bound(t->rot2.begin(), t->rot2.end(), b) - t->rot2.begin());
         gpi[(size_t)g * nb + pos] = pidx++;
       }
+    t->dense = true;
+    for (size_t i = 0; i < gpi.size(); i++) if (gpi[i] != (int)i) t->dense = false;
     int slot = 0;
     for (int i = 0; i < nb; i++) { bzero[i] = t->rot2[i] == 0; bslot[i] = t->rot2[i] == 0 ? 0 : slot++; }
     t->d_gpi = DevArray<int>(gpi.size()); upload(t->d_gpi.p, gpi.data(), gpi.size());
@@ -935,7 +943,7 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct) {
   const u64* c1 = ct.d.p + (size_t)(ct.level + 1) * N;
   // 1. decomposition of c1 and P*c
   DU64 digits((size_t)dn * qp);
-  decompose_modup(l, c1, 0, 1, digits.p);
+  decompose_modup(l, c1, 0, 1, digits.p, false);
   DU64 pc((size_t)2 * (l + 1) * N);
   launch_mul_const(pc.p, c0, 0, 1, rows_q(l), s.pmod_w.p, s.pmod_wp.p, s.d_mods.p, N, s.st);
   launch_mul_const(pc.p + (size_t)(l + 1) * N, c1, 0, 1, rows_q(l), s.pmod_w.p, s.pmod_wp.p, s.d_mods.p, N, s.st);
@@ -965,6 +973,7 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct) {
   if (nbr > 0) {
     KeyMacArgs a{};
     a.digits = digits.p; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = t.d_bkey.p; a.perm = t.d_bperm.p; a.add0 = pc.p;
+    a.own = c1; a.own_bstride = 0;
     a.out0 = R.p; a.out1 = R.p + qp; a.out_bstride = 2 * qp; a.mods = s.d_mods.p;
     a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
     timed("keymac_baby", [&] { launch_keymac(a, nbr, s.st); });
@@ -976,7 +985,8 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct) {
     a.diag = t.diags.p; a.diag_stride = (size_t)(t.level + 1 + K) * N;
     a.R = R.p; a.R_bstride = 2 * qp; a.R_pstride = qp;
     a.pc = pc.p; a.pc_pstride = (size_t)(l + 1) * N;
-    a.baby_is_zero = t.d_bzero.p; a.baby_slot = t.d_bslot.p; a.gpi = t.d_gpi.p;
+    a.baby_is_zero = t.d_bzero.p; a.baby_slot = t.d_bslot.p; a.gpi = t.d_gpi.p; a.dense = t.dense ? 1 : 0;
+    a.zero_pidx = (int)t.plain_idx.size();
     a.T = T.p; a.T_gstride = 2 * qp; a.T_pstride = qp; a.mods = s.d_mods.p;
     a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.lt_level = t.level; a.ng = ng; a.nbaby = nb;
     for (int b0 = 0; b0 < nb; b0 += 32) {
@@ -990,9 +1000,10 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct) {
     DU64 t1q((size_t)ngk * (l + 1) * N);
     mod_down(l, T.p + (size_t)gs * 2 * qp + qp, 2 * qp, ngk, t1q.p, (size_t)(l + 1) * N);
     DU64 dg2((size_t)ngk * dn * qp);
-    decompose_modup(l, t1q.p, (size_t)(l + 1) * N, ngk, dg2.p);
+    decompose_modup(l, t1q.p, (size_t)(l + 1) * N, ngk, dg2.p, false);
     GiantAccArgs a{};
     a.digits = dg2.p; a.dig_bstride = (size_t)dn * qp; a.key = t.d_gkey.p; a.perm = t.d_gperm.p; a.tg = t.d_tg.p; a.ng = ngk;
+    a.own = t1q.p; a.own_bstride = (size_t)(l + 1) * N;
     a.T = T.p; a.T_gstride = 2 * qp; a.T_pstride = qp; a.t_zero = gs ? 0 : -1;
     a.out0 = acc.p; a.out1 = acc.p + qp; a.mods = s.d_mods.p;
     a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
@@ -1014,7 +1025,7 @@ std::unique_ptr<Cipher> eval_lt_naive(const LinTrans& t, const Cipher& ct) {
   const u64* c0 = ct.d.p;
   const u64* c1 = ct.d.p + (size_t)(ct.level + 1) * N;
   DU64 digits((size_t)dn * qp);
-  decompose_modup(l, c1, 0, 1, digits.p);
+  decompose_modup(l, c1, 0, 1, digits.p, false);
   DU64 pc((size_t)(l + 1) * N);
   launch_mul_const(pc.p, c0, 0, 1, rows_q(l), s.pmod_w.p, s.pmod_wp.p, s.d_mods.p, N, s.st);
   std::vector<int> nz; int zero_p = -1;
@@ -1031,6 +1042,7 @@ std::unique_ptr<Cipher> eval_lt_naive(const LinTrans& t, const Cipher& ct) {
     DU64 R((size_t)n * 2 * qp);
     KeyMacArgs a{};
     a.digits = digits.p; a.key = kp.p; a.perm = pp.p; a.add0 = pc.p;
+    a.own = c1; a.own_bstride = 0;
     a.out0 = R.p; a.out1 = R.p + qp; a.out_bstride = 2 * qp; a.mods = s.d_mods.p;
     a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
     launch_keymac(a, n, s.st);
