@@ -41,11 +41,6 @@ struct RowMap {
   __host__ __device__ int mod(int row) const { return row < split ? m0 + row : m1 + (row - split); }
 };
 
-struct RowList {
-  int n;
-  short row[HCK_MAXMOD];
-  short mod[HCK_MAXMOD];
-};
 
 #if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
 __device__ __forceinline__ u64 add_mod(u64 a, u64 b, u64 q) { u64 r = a + b; return r >= q ? r - q : r; }
@@ -87,6 +82,22 @@ __device__ __forceinline__ void acc_mac(Acc128& A, u64 a, u64 b) {
       : [s0] "+v"(A.s0), [s1] "+v"(A.s1), [s2] "+v"(A.s2), [c0] "+v"(A.c0), [c1] "+v"(A.c1),
         [ca] "=&s"(ca), [cb] "=&s"(cb), [cc] "=&s"(cc), [cd] "=&s"(cd)
       : [a0] "v"(a0), [a1] "v"(a1), [b0] "v"(b0), [b1] "v"(b1));
+}
+// The same with b uniform across the wave (held in SGPRs: the constant of a
+// basis conversion); each v_mad_u64_u32 reads one SGPR.
+__device__ __forceinline__ void acc_mac_s(Acc128& A, u64 a, u64 b) {
+  const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32), b0 = (uint32_t)b, b1 = (uint32_t)(b >> 32);
+  u64 ca, cb, cc, cd;
+  asm("v_mad_u64_u32 %[s0], %[ca], %[b0], %[a0], %[s0]\n\t"
+      "v_mad_u64_u32 %[s1], %[cb], %[b1], %[a0], %[s1]\n\t"
+      "v_mad_u64_u32 %[s1], %[cc], %[b0], %[a1], %[s1]\n\t"
+      "v_mad_u64_u32 %[s2], %[cd], %[b1], %[a1], %[s2]\n\t"
+      "v_addc_co_u32_e64 %[c0], %[cd], 0, %[c0], %[ca]\n\t"
+      "v_addc_co_u32_e64 %[c1], %[cd], 0, %[c1], %[cb]\n\t"
+      "v_addc_co_u32_e64 %[c1], %[cd], 0, %[c1], %[cc]"
+      : [s0] "+v"(A.s0), [s1] "+v"(A.s1), [s2] "+v"(A.s2), [c0] "+v"(A.c0), [c1] "+v"(A.c1),
+        [ca] "=&s"(ca), [cb] "=&s"(cb), [cc] "=&s"(cc), [cd] "=&s"(cd)
+      : [a0] "v"(a0), [a1] "v"(a1), [b0] "s"(b0), [b1] "s"(b1));
 }
 // the 128-bit value (lo, hi) of an accumulator
 __device__ __forceinline__ void acc_value(const Acc128& A, u64& lo, u64& hi) {

@@ -5,8 +5,13 @@
 struct NttTables {
   const ModC* mods;
   const u64 *tw, *itw;     // [mod][N][2]: (psi^brv(k), Shoup companion) and the same for psi^-1
+  const u64 *twr, *itwr;   // [mod][R][slots][P][2]: row-pass consecutive-round twiddles, lane-interleaved
   const u64 *ninv, *ninvp; // [mod]
 };
+// N = R x C, R = 2^SA, C = 2^SB (the transform's column / row split)
+void ntt_split(int logN, int* SA, int* SB);
+// twiddle slots per lane of the row pass's consecutive round
+int ntt_row_round_slots(int logN);
 
 struct BConvSrc {
   u64 q, hinv, hinvp;  // source modulus, (S/s_i)^-1 mod s_i and its Shoup companion
@@ -83,7 +88,8 @@ void launch_mul_const(u64* out, const u64* in, size_t bstride, int batch, RowMap
 void launch_mont_mul(u64* out, size_t obstride, const u64* a, size_t abstride, const u64* bR, size_t bbstride, int batch, RowMap rm, const ModC* mods, int N, bool acc, hipStream_t st);
 void launch_mont_convert(u64* data, size_t bstride, int batch, RowMap rm, const ModC* mods, int N, bool to, hipStream_t st);
 void launch_permute(u64* out, const u64* in, size_t bstride, int batch, int rows, const uint32_t* perm, int N, hipStream_t st);
-void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable& tab, u64* out, size_t out_bstride, int batch, const RowList& rl, const ModC* mods, int N, bool force_v0, hipStream_t st);
+// Basis extension of the ns source rows of `in` into the target rows rm of `out`.
+void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable& tab, u64* out, size_t out_bstride, int batch, const RowMap& rm, const ModC* mods, int N, bool force_v0, hipStream_t st);
 void launch_moddown_combine(u64* out, size_t o_bstride, const u64* x, size_t x_bstride, const u64* ext, size_t e_bstride, const u64* add, size_t a_bstride, int add_batches, const uint32_t* perm, const u64* pinv, const u64* pinvp, int qrows, int batch, const ModC* mods, int N, hipStream_t st);
 void launch_keymac(const KeyMacArgs& a, int batch, hipStream_t st);
 void launch_giant_acc(const GiantAccArgs& a, hipStream_t st);

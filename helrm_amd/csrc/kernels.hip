@@ -123,7 +123,7 @@ void launch_copy(u64* dst, size_t dstride, const u64* src, size_t sstride, size_
 template <int MAXS, int NS>
 __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, size_t in_bstride, int ns_rt,
                                                     BConvTable tab, u64* __restrict__ out, size_t out_bstride,
-                                                    RowList rl, const ModC* __restrict__ mods, int N, int force_v0) {
+                                                    RowMap rm, const ModC* __restrict__ mods, int N, int force_v0) {
   const int ns = NS > 0 ? NS : ns_rt;
   const int x = blockIdx.x * blockDim.x + threadIdx.x;
   const u64* inb = in + (size_t)blockIdx.z * in_bstride;
@@ -141,46 +141,51 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
   }
   const int v = force_v0 ? 0 : (int)(u64)vf;
   const int r0 = blockIdx.y * tab.rows_per_block;
-  const int r1 = min(r0 + tab.rows_per_block, rl.n);
+  const int r1 = min(r0 + tab.rows_per_block, rm.nact());
   for (int r = r0; r < r1; r++) {
-    const int m = rl.mod[r];
+    const int row = rm.row(r);
+    const int m = rm.mod(row);
     const ModC mc = mods[m];
     const u64* __restrict__ h = tab.hat + (size_t)m * ns;
-    // exact 128-bit sums of 16 products (words < 2^62), folded below q
+    // exact column sums of 16 products (words < 2^62), folded below q
     u128 acc = 0;
 #pragma unroll
     for (int i0 = 0; i0 < MAXS; i0 += 16) {
-      u128 part = 0;
+      Acc128 A;
+      acc_zero(A);
 #pragma unroll
       for (int i = i0; i < i0 + 16 && i < MAXS; i++)
-        if (i < ns) part += (u128)y[i] * h[i];
-      acc += ((u128)fold_hi4((u64)(part >> 64), mc.q) << 64) | (u64)part;
+        if (i < ns) acc_mac_s(A, y[i], h[i]);
+      u64 lo, hi;
+      acc_value(A, lo, hi);
+      acc += ((u128)fold_hi4(hi, mc.q) << 64) | lo;
     }
     u64 res = redc((u64)acc, fold_hi4((u64)(acc >> 64), mc.q), mc.q, mc.qinv);
     res = sub_mod(res, tab.vS[(size_t)m * (ns + 1) + v], mc.q);
-    outb[(size_t)rl.row[r] * N + x] = res;
+    outb[(size_t)row * N + x] = res;
   }
 }
 void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable& tab, u64* out, size_t out_bstride, int batch,
-                  const RowList& rl, const ModC* mods, int N, bool force_v0, hipStream_t st) {
-  if (rl.n <= 0 || batch <= 0) return;
+                  const RowMap& rm, const ModC* mods, int N, bool force_v0, hipStream_t st) {
+  const int nrows = rm.nact();
+  if (nrows <= 0 || batch <= 0) return;
   BConvTable t = tab;
   // all destination rows in one thread unless that leaves too few workgroups
   const int cols = N / 256;
   int ny = 1;
-  while (ny < rl.n && (long)cols * batch * ny < 2048) ny *= 2;
-  t.rows_per_block = (rl.n + ny - 1) / ny;
-  ny = (rl.n + t.rows_per_block - 1) / t.rows_per_block;
+  while (ny < nrows && (long)cols * batch * ny < 2048) ny *= 2;
+  t.rows_per_block = (nrows + ny - 1) / ny;
+  ny = (nrows + t.rows_per_block - 1) / t.rows_per_block;
   dim3 grid(cols, ny, batch);
   const int fv = force_v0 ? 1 : 0;
   if (ns == 8)
-    hipLaunchKernelGGL((bconv_kernel<8, 8>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, fv);
+    hipLaunchKernelGGL((bconv_kernel<8, 8>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rm, mods, N, fv);
   else if (ns < 8)
-    hipLaunchKernelGGL((bconv_kernel<8, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, fv);
+    hipLaunchKernelGGL((bconv_kernel<8, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rm, mods, N, fv);
   else if (ns <= 16)
-    hipLaunchKernelGGL((bconv_kernel<16, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, fv);
+    hipLaunchKernelGGL((bconv_kernel<16, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rm, mods, N, fv);
   else
-    hipLaunchKernelGGL((bconv_kernel<HCK_MAXSRC, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rl, mods, N, fv);
+    hipLaunchKernelGGL((bconv_kernel<HCK_MAXSRC, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rm, mods, N, fv);
 }
 
 // ModDown combine: out = (x - ext) * P^-1 (+ add) [gathered through perm]

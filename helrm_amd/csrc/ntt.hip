@@ -64,6 +64,45 @@ __device__ __forceinline__ void ntt_round(u64 (&v)[16], u64 A, int ls, u64 Nn, c
   }
 }
 
+// Slots of a round of NST stages over 16 consecutive words: 8 + 4 + ... twiddles.
+__host__ __device__ constexpr int ntt_round_slots(int nst) { return nst == 0 ? 0 : (16 >> nst) + ntt_round_slots(nst - 1); }
+
+// The same round as ntt_round with ls = 0 (16 consecutive words of a row),
+// reading its twiddles from a lane-interleaved table: tab points at entry
+// [r][0][j] of a [R][slots][P] table, slot sl of lane j is tab[sl * P], so
+// each twiddle load of a wave is one contiguous read.  Slot order: stages in
+// execution order, twiddles k = 0 .. within a stage.
+template <bool FWD, int NST>
+__device__ __forceinline__ void ntt_round_tab(u64 (&v)[16], const uint4* __restrict__ tab, int P, u64 q) {
+  const u64 q2 = q + q;
+  int sl = 0;
+#pragma unroll
+  for (int s = 0; s < NST; s++) {
+    const int lrd = FWD ? NST - 1 - s : s;
+    const int rd = 1 << lrd;
+    const int sh = lrd + 1;
+#pragma unroll
+    for (int k = 0; k < (16 >> sh); k++, sl++) {
+      const uint4 t4 = tab[(size_t)sl * P];
+      const u64 w = ((u64)t4.y << 32) | t4.x, wp = ((u64)t4.w << 32) | t4.z;
+#pragma unroll
+      for (int r = 0; r < rd; r++) {
+        const int i = (k << sh) + r;
+        u64 X = v[i], Y = v[i + rd];
+        if (FWD) {
+          const u64 x = csub(X, q2);
+          const u64 t = shoup_lazy(Y, w, wp, q);
+          v[i] = x + t;
+          v[i + rd] = x - t + q2;
+        } else {
+          v[i] = csub(X + Y, q2);
+          v[i + rd] = shoup_lazy(X - Y + q2, w, wp, q);
+        }
+      }
+    }
+  }
+}
+
 // LDS column swizzle for the row pass: conflict-free both for the strided
 // (j + P*i) and the consecutive (16*j + i) access patterns.
 __device__ __forceinline__ int swz(int col) { return col ^ ((col >> 4) & 15); }
@@ -75,6 +114,7 @@ struct NttArgs {
   size_t bstride;
   RowMap rm;
   const uint4* tw;   // [mod][N] (w, w') pairs, forward or inverse table
+  const uint4* twr;  // [mod][R][slots][P] lane-interleaved twiddles of the row pass's consecutive round
   const ModC* mods;
   const u64 *ninv, *ninvp;  // [mod]
   int logN, SA, SB, nsub;   // nsub: sub-transforms per workgroup
@@ -149,6 +189,8 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
   u64* poly = a.data + (size_t)blockIdx.z * a.bstride + (size_t)row * Nn + (size_t)r * C;
   u64* srow = sm + rho * C;
   const uint4* tw = a.tw + (size_t)m * Nn;
+  constexpr int NSL = ntt_round_slots(S - 4);
+  const uint4* twr = a.twr + (((size_t)m * (Nn >> S) + r) * NSL) * P + j;
   const u64 A = (u64)r * C;
   u64 v[16];
   if (FWD) {
@@ -160,7 +202,7 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = srow[swz(16 * j + i)];
-    ntt_round<true, S - 4>(v, A + 16 * j, 0, Nn, tw, q);
+    ntt_round_tab<true, S - 4>(v, twr, P, q);
     const u64 q2 = q + q;
 #pragma unroll
     for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = csub(csub(v[i], q2), q);
@@ -174,7 +216,7 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = srow[swz(16 * j + i)];
-    ntt_round<false, S - 4>(v, A + 16 * j, 0, Nn, tw, q);
+    ntt_round_tab<false, S - 4>(v, twr, P, q);
 #pragma unroll
     for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = v[i];
     __syncthreads();
@@ -207,6 +249,12 @@ void launch_row(int S, dim3 grid, dim3 block, const NttArgs& a, hipStream_t st) 
 
 }  // namespace
 
+int ntt_row_round_slots(int logN) {
+  int SA, SB;
+  ntt_split(logN, &SA, &SB);
+  return ntt_round_slots(SB - 4);
+}
+
 // Split of logN into column (SA) and row (SB) sub-transform sizes.
 void ntt_split(int logN, int* SA, int* SB) {
   *SA = logN / 2;
@@ -228,6 +276,7 @@ void launch_ntt(const u64* src, size_t sstride, u64* data, size_t bstride, int b
   a.src = src; a.sstride = sstride; a.data = data; a.bstride = bstride; a.rm = rm; a.mods = tw.mods;
   a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN; a.SA = SA; a.SB = SB;
   a.tw = reinterpret_cast<const uint4*>(forward ? tw.tw : tw.itw);
+  a.twr = reinterpret_cast<const uint4*>(forward ? tw.twr : tw.itwr);
   // column pass: P = 2^(SA-4) threads per column, nsub columns per workgroup
   const int PA = 1 << (SA - 4), C = 1 << SB, R = 1 << SA;
   const int nsubA = std::min(NTT_TPB / PA, C);

@@ -248,6 +248,7 @@ struct Scheme {
   hipStream_t st = nullptr;
   DevArray<ModC> d_mods;
   DU64 tw2, itw2, ninv, ninvp;  // interleaved (w, w') twiddle pairs [mod][N][2]
+  DU64 twr2, itwr2;             // row-pass consecutive-round twiddles, lane-interleaved
   NttTables tw{};
   std::vector<ModC> hmods;
   // per-modulus constants (Shoup pairs indexed by modulus)
@@ -392,10 +393,10 @@ void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* di
   for (int d = 0; d < dn; d++) {
     int st0 = d * K, en = std::min(st0 + K, l + 1), ns = en - st0;
     BConvHost& bt = bconv_table(st0, en);
-    RowList rl{}; rl.n = 0;
-    for (int k = 0; k < nqp; k++) if (k < st0 || k >= en) { rl.row[rl.n] = (short)k; rl.mod[rl.n] = (short)qp_mod(l, k); rl.n++; }
+    // targets: every QP row except the digit's own [st0, en)
+    RowMap trm{nqp, l + 1, 0, s.L, st0, en};
     u64* D = digits + (size_t)d * nqp * N;
-    launch_bconv(coef.p + (size_t)st0 * N, (size_t)(l + 1) * N, ns, bt.tab, D, dstride, batch, rl, s.d_mods.p, N, ns == 1, s.st);
+    launch_bconv(coef.p + (size_t)st0 * N, (size_t)(l + 1) * N, ns, bt.tab, D, dstride, batch, trm, s.d_mods.p, N, ns == 1, s.st);
     if (copy_own) copy_rows(D + (size_t)st0 * N, dstride, c1 + (size_t)st0 * N, c1_bstride, (size_t)ns * N, batch);
     RowMap rm{nqp, l + 1, 0, s.L, st0, en};
     ntt(D, dstride, batch, rm, true);
@@ -410,9 +411,7 @@ void mod_down(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t
   // P rows of x (rows l+1.. of each batch entry) -> coefficient domain in pc
   ntt_oop(x + (size_t)(l + 1) * N, x_bstride, pc.p, (size_t)K * N, batch, rows_p(), false);
   BConvHost& bt = bconv_table(s.L, s.L + K);
-  RowList rl{}; rl.n = l + 1;
-  for (int i = 0; i <= l; i++) { rl.row[i] = (short)i; rl.mod[i] = (short)i; }
-  launch_bconv(pc.p, (size_t)K * N, K, bt.tab, ext.p, (size_t)(l + 1) * N, batch, rl, s.d_mods.p, N, false, s.st);
+  launch_bconv(pc.p, (size_t)K * N, K, bt.tab, ext.p, (size_t)(l + 1) * N, batch, rows_q(l), s.d_mods.p, N, false, s.st);
   ntt(ext.p, (size_t)(l + 1) * N, batch, rows_q(l), true);
   launch_moddown_combine(out, o_bstride, x, x_bstride, ext.p, (size_t)(l + 1) * N, add, a_bstride, add_batches, perm,
                          s.pinv_w.p, s.pinv_wp.p, l + 1, batch, s.d_mods.p, N, s.st);
@@ -707,8 +706,33 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
       hn[m] = invmod((u64)N, qq); hnp[m] = shoup(hn[m], qq);
     }
     auto up = [&](DU64& d, const std::vector<u64>& h) { d = DU64(h.size()); upload(d.p, h.data(), h.size()); };
-    up(s.tw2, htw); up(s.itw2, hitw); up(s.ninv, hn); up(s.ninvp, hnp);
-    s.tw = NttTables{s.d_mods.p, s.tw2.p, s.itw2.p, s.ninv.p, s.ninvp.p};
+    // lane-interleaved copies of the twiddles of the row pass's round over 16
+    // consecutive words: [mod][R][slot][lane], slots in the kernel's order
+    int SA, SB;
+    ntt_split(logN, &SA, &SB);
+    const int C = 1 << SB, R = 1 << SA, PB = 1 << (SB - 4), NST = SB - 4, NSL = ntt_row_round_slots(logN);
+    std::vector<u64> htwr((size_t)nm * R * NSL * PB * 2), hitwr(htwr.size());
+    for (int m = 0; m < nm; m++)
+      for (int r = 0; r < R; r++)
+        for (int j = 0; j < PB; j++) {
+          const u64 A = (u64)r * C + 16 * (u64)j;
+          for (int dir = 0; dir < 2; dir++) {
+            const std::vector<u64>& src = dir == 0 ? htw : hitw;
+            std::vector<u64>& dst = dir == 0 ? htwr : hitwr;
+            int sl = 0;
+            for (int st = 0; st < NST; st++) {
+              const int lrd = dir == 0 ? NST - 1 - st : st, sh = lrd + 1;
+              const u64 tb = ((u64)N + A) >> sh;
+              for (int k = 0; k < (16 >> sh); k++, sl++) {
+                const size_t o = ((((size_t)m * R + r) * NSL + sl) * PB + j) * 2, si = ((size_t)m * N + tb + k) * 2;
+                dst[o] = src[si];
+                dst[o + 1] = src[si + 1];
+              }
+            }
+          }
+        }
+    up(s.tw2, htw); up(s.itw2, hitw); up(s.twr2, htwr); up(s.itwr2, hitwr); up(s.ninv, hn); up(s.ninvp, hnp);
+    s.tw = NttTables{s.d_mods.p, s.tw2.p, s.itw2.p, s.twr2.p, s.itwr2.p, s.ninv.p, s.ninvp.p};
     std::vector<u64> pm(nm), pmp(nm), pin(nm), pinp(nm), p0i(nm), p0ip(nm), pmr(nm);
     for (int m = 0; m < nm; m++) {
       u64 qq = s.mod[m], P = 1;
@@ -1093,9 +1117,7 @@ std::unique_ptr<Cipher> encrypt_pt(const Plain& pt) {
   // ModDown from Q + {p_0} in the coefficient domain
   DU64 ext((size_t)2 * (l + 1) * N);
   BConvHost& bt = bconv_table(s.L, s.L + 1);
-  RowList rl{}; rl.n = l + 1;
-  for (int i = 0; i <= l; i++) { rl.row[i] = (short)i; rl.mod[i] = (short)i; }
-  launch_bconv(tt.p + (size_t)(l + 1) * N, (size_t)nr * N, 1, bt.tab, ext.p, (size_t)(l + 1) * N, 2, rl, s.d_mods.p, N, false, s.st);
+  launch_bconv(tt.p + (size_t)(l + 1) * N, (size_t)nr * N, 1, bt.tab, ext.p, (size_t)(l + 1) * N, 2, rows_q(l), s.d_mods.p, N, false, s.st);
   auto out = new_ct(l, pt.scale); out->logslots = pt.logslots;
   launch_moddown_combine(out->d.p, (size_t)(l + 1) * N, tt.p, (size_t)nr * N, ext.p, (size_t)(l + 1) * N, nullptr, 0, 0, nullptr,
                          s.p0inv_w.p, s.p0inv_wp.p, l + 1, 2, s.d_mods.p, N, s.st);
