@@ -51,7 +51,7 @@ def read_traffic(kernel="diag_mac"):
         return None
 
 
-def cpu_baseline(q, p, h, key_seed, diagonals, selector, level, logscale, threads, max_groups=2):
+def cpu_baseline(q, p, h, key_seed, diagonals, selector, level, logscale, threads, per_step=26, max_groups=2):
     """Bounded sample of the same PCMM on the CPU restatement (oracle/):
     all baby-step rotations, the rotation-0 giant group and one key-switched
     giant group, the final ModDown, rescale, 6-rotation fold and bias add;
@@ -94,9 +94,63 @@ def cpu_baseline(q, p, h, key_seed, diagonals, selector, level, logscale, thread
                   f"{len(babies)} hoisted baby rotations, giant groups 0 and 1 of {ng}, final ModDown, rescale, "
                   f"6-rotation fold and bias; the other {ng - 2} key-switched giant groups extrapolated from "
                   f"group 1 ({tm['gks']:.3f} s); estimated {t_pcmm:.2f} s per PCMM")
-        return 26.0 / t_pcmm, t_pcmm, sample, tm
+        return per_step / t_pcmm, t_pcmm, sample, tm
     finally:
         orc.close()
+
+
+def describe(cfg):
+    if cfg["kind"] == "pcmm":
+        return (f"{cfg['fields']}-table embedding PCMM, tables {cfg['rows']}x{cfg['dim']} as base-{cfg['base']} "
+                f"digit sub-tables")
+    return f"encrypted dense layer {cfg['out_features']}x{cfg['in_features']}"
+
+
+def ntt_microbench(lib, reps=5):
+    """Batched negacyclic NTT / inverse NTT and RNS multiply-accumulate at the
+    kernel-microbenchmark shape (N=2^16, 24 limbs of 50-bit primes, 64
+    polynomials), data resident in HBM; per-launch times from HIP events on
+    the library's stream.  Replaces the current scheme."""
+    from oracle import oracle as O  # prime generator only (the same chain rule as the library)
+    logn, nl, npoly = 16, 24, 64
+    q, p = O.gen_primes(logn, [50] * nl, [61])
+    lib.NewSchemeWithModuli(logn, q, p, 50, 192, 5)
+    N = 1 << logn
+    rng = np.random.default_rng(1)
+    x = np.stack([rng.integers(0, qq, size=(npoly, N), dtype=np.uint64) for qq in q], axis=1)
+    d = lib.device_upload(x)
+    d2 = lib.device_upload(np.stack([rng.integers(0, qq, size=(npoly, N), dtype=np.uint64) for qq in q], axis=1))
+    out = lib.device_empty((nl, N))
+    lib.NttDevice(d.ptr, npoly, nl, 1)
+    lib.NttDevice(d.ptr, npoly, nl, 0)
+    lib.Synchronize()
+    lib.KernelTimingEnable(1)
+    for _ in range(reps):
+        lib.NttDevice(d.ptr, npoly, nl, 1)
+        lib.NttDevice(d.ptr, npoly, nl, 0)
+        lib.MulAccDevice(d.ptr, d2.ptr, out.ptr, npoly, nl)
+    lib.Synchronize()
+    res = {}
+    for name in ("ntt_batch", "intt_batch", "mulacc"):
+        c, tot = lib.kernel_time(name)
+        res[name + "_ms"] = tot / c if c else None
+    lib.KernelTimingEnable(0)
+    ok = np.array_equal(d.download(), x)
+    d.free(); d2.free(); out.free()
+    butterflies = npoly * nl * (N // 2) * logn
+    limb_bytes = npoly * nl * N * 8
+    res.update({
+        "config": "N=2^16, 24 limbs of 50-bit primes, 64 polynomials, u64 words",
+        "butterflies_per_transform": butterflies,
+        "ntt_Gbutterflies_per_s": butterflies / (res["ntt_batch_ms"] / 1e3) / 1e9,
+        "intt_Gbutterflies_per_s": butterflies / (res["intt_batch_ms"] / 1e3) / 1e9,
+        # two passes, each reading and writing every word once
+        "ntt_hbm_GBs": 4 * limb_bytes / (res["ntt_batch_ms"] / 1e3) / 1e9,
+        # multiply-accumulate reads two batches and writes one sum
+        "mulacc_hbm_GBs": (2 * limb_bytes + nl * N * 8) / (res["mulacc_ms"] / 1e3) / 1e9,
+        "roundtrip_exact": bool(ok),
+    })
+    return res
 
 
 def copy_calibration(mib):
@@ -126,6 +180,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="pcmm26")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ntt-microbench", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -141,11 +196,11 @@ def main():
         sys.exit(2)
 
     from helrm_amd.backend import HipLibrary
-    from helrm_amd.workloads import PCMMWorkload, CONFIGS
+    from helrm_amd.workloads import make_workload, CONFIGS
 
     lib = HipLibrary()
     t_setup = time.perf_counter()
-    w = PCMMWorkload(lib, args.workload, seed=args.seed, key_seed=1).setup()
+    w = make_workload(lib, args.workload, seed=args.seed, key_seed=1).setup()
     t_setup = time.perf_counter() - t_setup
     info = w.shape_info()
     cfg = CONFIGS[args.workload]
@@ -155,24 +210,24 @@ def main():
     err = float(np.abs(w.decrypt_output(out) - w.expected).max())
     out.free()
 
-    try:
-        import torch
-        sync_torch = torch.cuda.synchronize if torch.cuda.is_available() else (lambda: None)
-    except Exception:
-        sync_torch = lambda: None
-
     for _ in range(args.warmup):
         o = w.run()
         o.free()
-    lib.Synchronize(); sync_torch()
+    lib.Synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         o = w.run()
         o.free()
-    lib.Synchronize(); sync_torch()
+    lib.Synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1000.0 / args.steps
-    lookups = 26.0 / (ms / 1000.0) if args.workload.startswith("pcmm26") else cfg["fields"] / (ms / 1000.0)
+    # one step = one query: one lookup per table for the embedding PCMM, one forward of the dense layer
+    per_step = cfg["fields"] if cfg["kind"] == "pcmm" else 1
+    lookups = per_step / (ms / 1000.0)
+    if cfg["kind"] == "pcmm":
+        metric, unit = (METRIC if args.workload == "pcmm26" else f"encrypted embedding lookups/sec ({args.workload})"), "lookups/s"
+    else:
+        metric, unit = f"encrypted dense-layer forwards/sec ({args.workload})", "forwards/s"
 
     # per-kernel HIP-event timings (separate, untimed passes)
     lib.KernelTimingEnable(1)
@@ -203,14 +258,16 @@ def main():
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         d = w.layer.diagonals[(0, 0)]
         v, t_cpu, sample, tm = cpu_baseline(lib.GetModuliChain(), lib.GetAuxModuliChain(), cfg["h"], 1, d,
-                                             w.selector, w.layer.level, cfg["logscale"], threads)
-        cpu = {"value": v, "unit": "lookups/s", "cores": threads, "kind": "port", "sample": sample,
+                                             w.input, w.layer.level, cfg["logscale"], threads, per_step)
+        cpu = {"value": v, "unit": unit, "cores": threads, "kind": "port", "sample": sample,
                "seconds_per_pcmm": t_cpu}
 
+    ntt = None if args.no_ntt_microbench else ntt_microbench(lib)
+
     line = {
-        "metric": METRIC,
+        "metric": metric,
         "value": lookups,
-        "unit": "lookups/s",
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -219,10 +276,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u64",
-        "data": "synthetic (seeded tables N(0,0.05), uniform indices, seeded keys and encryption randomness)",
-        "config": {"workload": f"{args.workload}: 26-table embedding PCMM, N=2^{cfg['logn']}, "
-                               f"L={L} (60+50x{L - 1} bit), K={K} (61 bit), dnum={(L + K - 1) // K}, scale 2^{cfg['logscale']}, "
-                               f"tables 4096x16 as 3 base-16 digit sub-tables",
+        "data": "synthetic (seeded tables / weights and inputs, seeded keys and encryption randomness)",
+        "config": {"workload": f"{args.workload}: {describe(cfg)}, N=2^{cfg['logn']}, "
+                               f"L={L} (60+50x{L - 1} bit), K={K} (61 bit), dnum={(L + K - 1) // K}, scale 2^{cfg['logscale']}",
                    "diagonals": info["diagonals"], "baby_steps": lti["baby"], "giant_steps": lti["giant"],
                    "fold_rotations": info["output_rotations"], "matrix": info["matrix"]},
         "pcmm_ms": ms,
@@ -233,6 +289,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "max_abs_err_vs_plaintext": err,
+        "ntt_microbench": ntt,
         "setup_s": t_setup,
     }
     print(json.dumps(line), flush=True)

@@ -193,6 +193,12 @@ _SIGNATURES = {
     "GetLinearTransformInfo": ([_I, _PI, _I], _I),
     "GetSchemeInfo": ([_PI, _I], _I),
     "Synchronize": ([], _I),
+    "DeviceAlloc": ([_c.c_size_t], _c.c_void_p),
+    "DeviceFree": ([_c.c_void_p], _I),
+    "CopyToDevice": ([_c.c_void_p, _c.c_void_p, _c.c_size_t], _I),
+    "CopyToHost": ([_c.c_void_p, _c.c_void_p, _c.c_size_t], _I),
+    "NttDevice": ([_c.c_void_p, _I, _I, _I], _I),
+    "MulAccDevice": ([_c.c_void_p, _c.c_void_p, _c.c_void_p, _I, _I], _I),
     "GetStream": ([], _c.c_void_p),
     "KernelTimingEnable": ([_I], _I),
     "KernelTimingGet": ([_c.c_char_p, _c.POINTER(_c.c_long), _c.POINTER(_c.c_double)], _I),
@@ -215,6 +221,27 @@ def load_library():
         _lib_handle.FreeCArray.argtypes = [ctypes.c_void_p]
         _lib_handle.FreeCArray.restype = None
     return _lib_handle
+
+
+class DeviceBuffer:
+    """A device allocation of uint64 words owned by libhelrm_hip.so."""
+
+    def __init__(self, lib, ptr, shape):
+        self.lib, self.ptr, self.shape = lib, ptr, tuple(shape)
+
+    @property
+    def nbytes(self):
+        return int(np.prod(self.shape)) * 8
+
+    def download(self):
+        out = np.empty(self.shape, dtype=np.uint64)
+        self.lib.CopyToHost(out.ctypes.data_as(ctypes.c_void_p), self.ptr, self.nbytes)
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.lib.DeviceFree(self.ptr)
+            self.ptr = None
 
 
 class HipLibrary:
@@ -303,6 +330,24 @@ class HipLibrary:
         buf = np.zeros(n, dtype=np.float64)
         self.DecodeDouble(pt_id, buf.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), n)
         return buf
+
+    # device buffers from the library's allocator (one HIP runtime per process)
+    def device_upload(self, arr):
+        """Copy a uint64 numpy array to a new device buffer; returns DeviceBuffer."""
+        a = np.ascontiguousarray(arr, dtype=np.uint64)
+        ptr = self.DeviceAlloc(a.nbytes)
+        if not ptr:
+            raise HipError(self.GetLastError().decode() or "DeviceAlloc failed")
+        buf = DeviceBuffer(self, ptr, a.shape)
+        self.CopyToDevice(ptr, a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
+        return buf
+
+    def device_empty(self, shape):
+        n = int(np.prod(shape)) * 8
+        ptr = self.DeviceAlloc(n)
+        if not ptr:
+            raise HipError(self.GetLastError().decode() or "DeviceAlloc failed")
+        return DeviceBuffer(self, ptr, tuple(shape))
 
     def kernel_time(self, name):
         cnt = ctypes.c_long(0)

@@ -81,6 +81,9 @@ void launch_ntt(u64* data, size_t bstride, int batch, RowMap rm, int logN, bool 
 // Out-of-place: the transform of src's rows is written to the same rows of dst.
 void launch_ntt(const u64* src, size_t sstride, u64* dst, size_t dstride, int batch, RowMap rm, int logN, bool forward,
                 const NttTables& tw, hipStream_t st);
+// In-place NTT / inverse NTT of an explicit list of limbs: list is a device
+// array of nlimbs {int64 word offset from data, int modulus index, int pad}.
+void launch_ntt_list(u64* data, const void* list, int nlimbs, int logN, bool forward, const NttTables& tw, hipStream_t st);
 // dst[b][0..words) = src[b][0..words) for b < batch.
 void launch_copy(u64* dst, size_t dstride, const u64* src, size_t sstride, size_t words, int batch, hipStream_t st);
 void launch_add(u64* out, const u64* a, const u64* b, size_t bstride, int batch, RowMap rm, const ModC* mods, int N, bool sub, hipStream_t st);
@@ -101,3 +104,5 @@ void launch_sample_cbd(u64* out, RowMap rm, u64 seed, u64 stream, const ModC* mo
 void launch_signed_rows(u64* out, RowMap rm, const int8_t* v, const ModC* mods, int N, hipStream_t st);
 void launch_gk_combine(u64* b, const u64* a, const u64* soR, const u64* sR, int own0, int own1, const u64* pmod, int rows, const ModC* mods, int N, hipStream_t st);
 void launch_encode_residues(u64* out, RowMap rm, const u64* rec, const ModC* mods, int N, hipStream_t st);
+// out[r][x] = sum_{p < npoly} a[p][r][x] * b[p][r][x] mod q_r, rows r < nrows of the modulus table
+void launch_mulacc(const u64* a, const u64* b, u64* out, int npoly, int nrows, const ModC* mods, int N, hipStream_t st);

@@ -426,6 +426,32 @@ void launch_diag_mac(const DiagMacArgs& a, hipStream_t st) {
   else hipLaunchKernelGGL((diag_mac_kernel<32, false>), grid, dim3(256), 0, st, a);
 }
 
+// RNS multiply-accumulate over a batch: out[r][x] = sum_p a[p][r][x] * b[p][r][x]
+// mod q_r (canonical inputs and output).  Exact 128-bit column sums of 16
+// products, then REDC and a Montgomery multiplication by R^2 mod q undo the
+// 2^-64 of the REDC.
+__global__ __launch_bounds__(256) void mulacc_kernel(const u64* __restrict__ a, const u64* __restrict__ b,
+                                                     u64* __restrict__ out, int npoly, int nrows,
+                                                     const ModC* __restrict__ mods, int N) {
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
+  const int r = blockIdx.y;
+  const ModC mc = mods[r];
+  const size_t pstride = (size_t)nrows * N, o = (size_t)r * N + x;
+  Acc128 A;
+  acc_zero(A);
+  u64 tlo = 0, thi = 0;
+  for (int p0 = 0; p0 < npoly; p0 += 16) {
+    const int p1 = min(p0 + 16, npoly);
+    for (int p = p0; p < p1; p++) acc_mac(A, a[(size_t)p * pstride + o], b[(size_t)p * pstride + o]);
+    acc_flush(A, tlo, thi, mc.q);
+  }
+  out[o] = mont_mul(redc(tlo, thi, mc.q, mc.qinv), mc.r2, mc.q, mc.qinv);
+}
+void launch_mulacc(const u64* a, const u64* b, u64* out, int npoly, int nrows, const ModC* mods, int N, hipStream_t st) {
+  if (npoly <= 0 || nrows <= 0) return;
+  hipLaunchKernelGGL(mulacc_kernel, dim3(N / 256, nrows), dim3(256), 0, st, a, b, out, npoly, nrows, mods, N);
+}
+
 // ---------------------------------------------------------------------------
 // Rescale helpers (DivRoundByLastModulus): u = iNTT(x_l) per polynomial;
 // t_i = ((u + h) mod q_l - h) mod q_i for i < l; out_i = (x_i - NTT(t_i)) * q_l^-1

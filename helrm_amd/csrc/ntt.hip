@@ -28,62 +28,51 @@ __device__ __forceinline__ u64 shoup_lazy(u64 x, u64 w, u64 wp, u64 q) {  // x*w
 }
 __device__ __forceinline__ u64 csub(u64 x, u64 m) { return x >= m ? x - m : x; }
 
-// One register round of NST butterfly stages on v[16].  Element i stands for
-// global index g_i = A + B + (i << ls) with B < 2^ls and A a multiple of
-// 2^(ls+4); the pair at register distance rd has index distance rd << ls and
+// Twiddle slots of a round of NST stages over 16 registers: 8 + 4 + ...
+__host__ __device__ constexpr int ntt_round_slots(int nst) { return nst == 0 ? 0 : (16 >> nst) + ntt_round_slots(nst - 1); }
+
+// The twiddles of one register round, loaded ahead of its butterflies so the
+// loads are in flight together (slot order: stages in execution order,
+// twiddles k = 0 .. within a stage).
+template <int NST>
+struct RoundTw { uint4 t[ntt_round_slots(NST)]; };
+
+// Element i of the round stands for global index g_i = A + B + (i << ls) with
+// B < 2^ls and A a multiple of 2^(ls+4): the pair at register distance rd
 // uses twiddle ((N + A) >> (ls + log2(rd) + 1)) + (i >> (log2(rd) + 1)).
 template <bool FWD, int NST>
-__device__ __forceinline__ void ntt_round(u64 (&v)[16], u64 A, int ls, u64 Nn, const uint4* __restrict__ tw,
-                                          u64 q) {
+__device__ __forceinline__ void round_tw_load(RoundTw<NST>& T, u64 A, int ls, u64 Nn, const uint4* __restrict__ tw) {
+  int sl = 0;
+#pragma unroll
+  for (int s = 0; s < NST; s++) {
+    const int lrd = FWD ? NST - 1 - s : s;
+    const int sh = lrd + 1;
+    const u64 tb = (Nn + A) >> (ls + sh);
+#pragma unroll
+    for (int k = 0; k < (16 >> sh); k++, sl++) T.t[sl] = tw[tb + k];
+  }
+}
+// A round over 16 consecutive words of a row, from the lane-interleaved
+// table: tab points at entry [r][0][j] of a [R][slots][P] table, slot sl of
+// lane j is tab[sl * P], so each load of a wave is one contiguous read.
+template <int NST>
+__device__ __forceinline__ void round_tw_load_tab(RoundTw<NST>& T, const uint4* __restrict__ tab, int P) {
+#pragma unroll
+  for (int sl = 0; sl < ntt_round_slots(NST); sl++) T.t[sl] = tab[(size_t)sl * P];
+}
+// NST butterfly stages on v[16] with the preloaded twiddles.
+template <bool FWD, int NST>
+__device__ __forceinline__ void ntt_round(u64 (&v)[16], const RoundTw<NST>& T, u64 q) {
   const u64 q2 = q + q;
+  int sl = 0;
 #pragma unroll
   for (int s = 0; s < NST; s++) {
     const int lrd = FWD ? NST - 1 - s : s;  // log2 of the register distance
     const int rd = 1 << lrd;
     const int sh = lrd + 1;
-    const u64 tb = (Nn + A) >> (ls + sh);
-#pragma unroll
-    for (int k = 0; k < (16 >> sh); k++) {
-      const uint4 t4 = tw[tb + k];
-      const u64 w = ((u64)t4.y << 32) | t4.x, wp = ((u64)t4.w << 32) | t4.z;
-#pragma unroll
-      for (int r = 0; r < rd; r++) {
-        const int i = (k << sh) + r;
-        u64 X = v[i], Y = v[i + rd];
-        if (FWD) {
-          const u64 x = csub(X, q2);
-          const u64 t = shoup_lazy(Y, w, wp, q);
-          v[i] = x + t;
-          v[i + rd] = x - t + q2;
-        } else {
-          v[i] = csub(X + Y, q2);
-          v[i + rd] = shoup_lazy(X - Y + q2, w, wp, q);
-        }
-      }
-    }
-  }
-}
-
-// Slots of a round of NST stages over 16 consecutive words: 8 + 4 + ... twiddles.
-__host__ __device__ constexpr int ntt_round_slots(int nst) { return nst == 0 ? 0 : (16 >> nst) + ntt_round_slots(nst - 1); }
-
-// The same round as ntt_round with ls = 0 (16 consecutive words of a row),
-// reading its twiddles from a lane-interleaved table: tab points at entry
-// [r][0][j] of a [R][slots][P] table, slot sl of lane j is tab[sl * P], so
-// each twiddle load of a wave is one contiguous read.  Slot order: stages in
-// execution order, twiddles k = 0 .. within a stage.
-template <bool FWD, int NST>
-__device__ __forceinline__ void ntt_round_tab(u64 (&v)[16], const uint4* __restrict__ tab, int P, u64 q) {
-  const u64 q2 = q + q;
-  int sl = 0;
-#pragma unroll
-  for (int s = 0; s < NST; s++) {
-    const int lrd = FWD ? NST - 1 - s : s;
-    const int rd = 1 << lrd;
-    const int sh = lrd + 1;
 #pragma unroll
     for (int k = 0; k < (16 >> sh); k++, sl++) {
-      const uint4 t4 = tab[(size_t)sl * P];
+      const uint4 t4 = T.t[sl];
       const u64 w = ((u64)t4.y << 32) | t4.x, wp = ((u64)t4.w << 32) | t4.z;
 #pragma unroll
       for (int r = 0; r < rd; r++) {
@@ -107,7 +96,13 @@ __device__ __forceinline__ void ntt_round_tab(u64 (&v)[16], const uint4* __restr
 // (j + P*i) and the consecutive (16*j + i) access patterns.
 __device__ __forceinline__ int swz(int col) { return col ^ ((col >> 4) & 15); }
 
+// One limb of a batched transform: word offset from the data base and
+// modulus index.  Either listed explicitly (rows of several digits of a
+// decomposition in one launch) or derived from (RowMap, batch stride).
+struct LimbRef { int64_t off; int mod; int pad; };
+
 struct NttArgs {
+  const LimbRef* list;  // nullptr: limb y = (batch y / rows, row y % rows) of rm
   const u64* src;  // input of the first pass (src == data: in place)
   size_t sstride;
   u64* data;       // output; the second pass works in place on it
@@ -118,7 +113,23 @@ struct NttArgs {
   const ModC* mods;
   const u64 *ninv, *ninvp;  // [mod]
   int logN, SA, SB, nsub;   // nsub: sub-transforms per workgroup
+  int rows;                 // rm.nact()
 };
+
+__device__ __forceinline__ LimbRef limb_ref(const NttArgs& a, int y) {
+  if (a.list) return a.list[y];
+  const int b = y / a.rows, r = a.rm.row(y - b * a.rows);
+  LimbRef l;
+  l.off = (int64_t)b * (int64_t)a.bstride + ((int64_t)r << a.logN);
+  l.mod = a.rm.mod(r);
+  l.pad = b;
+  return l;
+}
+// src offset of the same limb (first pass of an out-of-place transform)
+__device__ __forceinline__ int64_t limb_src_off(const NttArgs& a, int y, const LimbRef& l) {
+  if (a.list) return l.off;
+  return (int64_t)l.pad * (int64_t)a.sstride + (l.off - (int64_t)l.pad * (int64_t)a.bstride);
+}
 
 // Column pass (pass A): workgroup = nsub columns x R rows.
 template <bool FWD, int S>
@@ -130,42 +141,50 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_col_kernel(NttArgs a) {
   const int tid = threadIdx.x;
   const int c = tid & (nsub - 1);
   const int j = tid / nsub;  // in [0, P)
-  const int row = a.rm.row(blockIdx.y);
-  const int m = a.rm.mod(row);
+  const LimbRef lr = limb_ref(a, blockIdx.y);
+  const int m = lr.mod;
   const u64 q = a.mods[m].q;
   const u64 Nn = 1ull << a.logN;
   const int SB = a.SB;
   const size_t C = (size_t)1 << SB;
   const int col = blockIdx.x * nsub + c;
-  u64* poly = a.data + (size_t)blockIdx.z * a.bstride + (size_t)row * Nn + col;
+  u64* poly = a.data + lr.off + col;
   const uint4* tw = a.tw + (size_t)m * Nn;
   u64 v[16];
   if (FWD) {
-    const u64* in = a.src + (size_t)blockIdx.z * a.sstride + (size_t)row * Nn + col;
+    const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + col;
     // round 1: rows j + P*i, distances R/2 .. R/16 rows
+    RoundTw<4> T1;
+    round_tw_load<true, 4>(T1, 0, S - 4 + SB, Nn, tw);
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = in[(size_t)(j + P * i) * C];
-    ntt_round<true, 4>(v, 0, S - 4 + SB, Nn, tw, q);
+    ntt_round<true, 4>(v, T1, q);
+    RoundTw<S - 4> T2;
+    round_tw_load<true, S - 4>(T2, (u64)(16 * j) << SB, SB, Nn, tw);
 #pragma unroll
     for (int i = 0; i < 16; i++) sm[(j + P * i) * nsub + c] = v[i];
     __syncthreads();
     // round 2: rows 16*j + i, the remaining S-4 stages
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = sm[(16 * j + i) * nsub + c];
-    ntt_round<true, S - 4>(v, (u64)(16 * j) << SB, SB, Nn, tw, q);
+    ntt_round<true, S - 4>(v, T2, q);
 #pragma unroll
     for (int i = 0; i < 16; i++) poly[(size_t)(16 * j + i) * C] = v[i];
   } else {
     // round 1: rows 16*j + i, distances C .. 2^(S-5) C
+    RoundTw<S - 4> T1;
+    round_tw_load<false, S - 4>(T1, (u64)(16 * j) << SB, SB, Nn, tw);
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = poly[(size_t)(16 * j + i) * C];
-    ntt_round<false, S - 4>(v, (u64)(16 * j) << SB, SB, Nn, tw, q);
+    ntt_round<false, S - 4>(v, T1, q);
+    RoundTw<4> T2;
+    round_tw_load<false, 4>(T2, 0, S - 4 + SB, Nn, tw);
 #pragma unroll
     for (int i = 0; i < 16; i++) sm[(16 * j + i) * nsub + c] = v[i];
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = sm[(j + P * i) * nsub + c];
-    ntt_round<false, 4>(v, 0, S - 4 + SB, Nn, tw, q);
+    ntt_round<false, 4>(v, T2, q);
     const u64 ni = a.ninv[m], nip = a.ninvp[m];
 #pragma unroll
     for (int i = 0; i < 16; i++) poly[(size_t)(j + P * i) * C] = csub(shoup_lazy(v[i], ni, nip, q), q);
@@ -181,12 +200,12 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
   const int tid = threadIdx.x;
   const int j = tid & (P - 1);
   const int rho = tid >> (S - 4);
-  const int row = a.rm.row(blockIdx.y);
-  const int m = a.rm.mod(row);
+  const LimbRef lr = limb_ref(a, blockIdx.y);
+  const int m = lr.mod;
   const u64 q = a.mods[m].q;
   const u64 Nn = 1ull << a.logN;
   const int r = blockIdx.x * a.nsub + rho;  // row of the R x C view
-  u64* poly = a.data + (size_t)blockIdx.z * a.bstride + (size_t)row * Nn + (size_t)r * C;
+  u64* poly = a.data + lr.off + (size_t)r * C;
   u64* srow = sm + rho * C;
   const uint4* tw = a.tw + (size_t)m * Nn;
   constexpr int NSL = ntt_round_slots(S - 4);
@@ -194,15 +213,20 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
   const u64 A = (u64)r * C;
   u64 v[16];
   if (FWD) {
+    RoundTw<4> T1;
+    round_tw_load<true, 4>(T1, A, S - 4, Nn, tw);
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = poly[j + P * i];
-    ntt_round<true, 4>(v, A, S - 4, Nn, tw, q);
+    ntt_round<true, 4>(v, T1, q);
 #pragma unroll
     for (int i = 0; i < 16; i++) srow[swz(j + P * i)] = v[i];
     __syncthreads();
+    // second round's twiddles issued after the barrier (fewer live registers)
+    RoundTw<S - 4> T2;
+    round_tw_load_tab<S - 4>(T2, twr, P);
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = srow[swz(16 * j + i)];
-    ntt_round_tab<true, S - 4>(v, twr, P, q);
+    ntt_round<true, S - 4>(v, T2, q);
     const u64 q2 = q + q;
 #pragma unroll
     for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = csub(csub(v[i], q2), q);
@@ -210,19 +234,26 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) poly[j + P * i] = srow[swz(j + P * i)];
   } else {
-    const u64* in = a.src + (size_t)blockIdx.z * a.sstride + (size_t)row * Nn + (size_t)r * C;
+    const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + (size_t)r * C;
+    // all 16 loads (and the first round's twiddles) in flight before the LDS writes
+    RoundTw<S - 4> T1;
+    round_tw_load_tab<S - 4>(T1, twr, P);
 #pragma unroll
-    for (int i = 0; i < 16; i++) srow[swz(j + P * i)] = in[j + P * i];
+    for (int i = 0; i < 16; i++) v[i] = in[j + P * i];
+#pragma unroll
+    for (int i = 0; i < 16; i++) srow[swz(j + P * i)] = v[i];
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = srow[swz(16 * j + i)];
-    ntt_round_tab<false, S - 4>(v, twr, P, q);
+    ntt_round<false, S - 4>(v, T1, q);
+    RoundTw<4> T2;
+    round_tw_load<false, 4>(T2, A, S - 4, Nn, tw);
 #pragma unroll
     for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = v[i];
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = srow[swz(j + P * i)];
-    ntt_round<false, 4>(v, A, S - 4, Nn, tw, q);
+    ntt_round<false, 4>(v, T2, q);
 #pragma unroll
     for (int i = 0; i < 16; i++) poly[j + P * i] = v[i];
   }
@@ -266,28 +297,21 @@ void launch_ntt(u64* data, size_t bstride, int batch, RowMap rm, int logN, bool 
   launch_ntt(data, bstride, data, bstride, batch, rm, logN, forward, tw, st);
 }
 
-void launch_ntt(const u64* src, size_t sstride, u64* data, size_t bstride, int batch, RowMap rm, int logN, bool forward,
-                const NttTables& tw, hipStream_t st) {
-  const int rows = rm.nact();
-  if (rows <= 0 || batch <= 0) return;
+// Workgroup shape: 256-thread tiles (narrower tiles lose coalescing and
+// measured slower even for launches of a few limbs).
+static void ntt_launch(NttArgs a, int nlimbs, bool forward, hipStream_t st) {
   int SA, SB;
-  ntt_split(logN, &SA, &SB);
-  NttArgs a{};
-  a.src = src; a.sstride = sstride; a.data = data; a.bstride = bstride; a.rm = rm; a.mods = tw.mods;
-  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN; a.SA = SA; a.SB = SB;
-  a.tw = reinterpret_cast<const uint4*>(forward ? tw.tw : tw.itw);
-  a.twr = reinterpret_cast<const uint4*>(forward ? tw.twr : tw.itwr);
-  // column pass: P = 2^(SA-4) threads per column, nsub columns per workgroup
+  ntt_split(a.logN, &SA, &SB);
+  a.SA = SA; a.SB = SB;
   const int PA = 1 << (SA - 4), C = 1 << SB, R = 1 << SA;
-  const int nsubA = std::min(NTT_TPB / PA, C);
   const int PB = 1 << (SB - 4);
-  const int nsubB = std::min(NTT_TPB / PB, R);
+  const int nsubA = std::min(NTT_TPB / PA, C), nsubB = std::min(NTT_TPB / PB, R);
   NttArgs aA = a; aA.nsub = nsubA;
   NttArgs aB = a; aB.nsub = nsubB;
   // only the first pass reads src
-  if (forward) { aB.src = data; aB.sstride = bstride; } else { aA.src = data; aA.sstride = bstride; }
-  dim3 gridA(C / nsubA, rows, batch), blockA(PA * nsubA);
-  dim3 gridB(R / nsubB, rows, batch), blockB(PB * nsubB);
+  if (forward) { aB.src = a.data; aB.sstride = a.bstride; } else { aA.src = a.data; aA.sstride = a.bstride; }
+  dim3 gridA(C / nsubA, nlimbs), blockA(PA * nsubA);
+  dim3 gridB(R / nsubB, nlimbs), blockB(PB * nsubB);
   if (forward) {
     launch_col<true>(SA, gridA, blockA, aA, st);
     launch_row<true>(SB, gridB, blockB, aB, st);
@@ -295,4 +319,28 @@ void launch_ntt(const u64* src, size_t sstride, u64* data, size_t bstride, int b
     launch_row<false>(SB, gridB, blockB, aB, st);
     launch_col<false>(SA, gridA, blockA, aA, st);
   }
+}
+
+void launch_ntt(const u64* src, size_t sstride, u64* data, size_t bstride, int batch, RowMap rm, int logN, bool forward,
+                const NttTables& tw, hipStream_t st) {
+  const int rows = rm.nact();
+  if (rows <= 0 || batch <= 0) return;
+  NttArgs a{};
+  a.list = nullptr;
+  a.src = src; a.sstride = sstride; a.data = data; a.bstride = bstride; a.rm = rm; a.rows = rows; a.mods = tw.mods;
+  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN;
+  a.tw = reinterpret_cast<const uint4*>(forward ? tw.tw : tw.itw);
+  a.twr = reinterpret_cast<const uint4*>(forward ? tw.twr : tw.itwr);
+  ntt_launch(a, rows * batch, forward, st);
+}
+
+void launch_ntt_list(u64* data, const void* list, int nlimbs, int logN, bool forward, const NttTables& tw, hipStream_t st) {
+  if (nlimbs <= 0) return;
+  NttArgs a{};
+  a.list = reinterpret_cast<const LimbRef*>(list);
+  a.src = data; a.data = data; a.mods = tw.mods; a.rows = 1;
+  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN;
+  a.tw = reinterpret_cast<const uint4*>(forward ? tw.tw : tw.itw);
+  a.twr = reinterpret_cast<const uint4*>(forward ? tw.twr : tw.itwr);
+  ntt_launch(a, nlimbs, forward, st);
 }

@@ -15,6 +15,7 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <tuple>
 #include <memory>
 #include <mutex>
 #include <queue>
@@ -256,6 +257,7 @@ struct Scheme {
   DU64 rs_inv, rs_invp;  // [l][i] q_l^-1 mod q_i
   std::map<std::pair<int, int>, std::unique_ptr<BConvHost>> bconv;
   std::map<u64, DevArray<uint32_t>> perms;
+  std::map<std::tuple<int, int, size_t>, std::unique_ptr<struct DigitRows>> digit_rows;
   // keys
   bool has_sk = false, has_pk = false;
   std::vector<int8_t> s;
@@ -383,6 +385,33 @@ u64 galois_element(int k) { Scheme& s = sch(); u64 M = 2 * (u64)s.N; return powm
 // key switching building blocks
 // ============================================================================
 // digits[b][d][nqp][N] from c1 (NTT, Q rows 0..l) of batch b (stride c1_bstride)
+// The extended rows of every digit of a decomposition at level l for `batch`
+// entries of stride dstride: {word offset, modulus} per limb, built once.
+struct LimbRefH { int64_t off; int mod; int pad; };
+struct DigitRows { DevArray<LimbRefH> list; int n = 0; };
+const DigitRows& digit_rows(int l, int batch, size_t dstride) {
+  Scheme& s = sch();
+  const auto key = std::make_tuple(l, batch, dstride);
+  auto it = s.digit_rows.find(key);
+  if (it != s.digit_rows.end()) return *it->second;
+  const int N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
+  std::vector<LimbRefH> v;
+  for (int b = 0; b < batch; b++)
+    for (int d = 0; d < dn; d++) {
+      const int st0 = d * K, en = std::min(st0 + K, l + 1);
+      for (int k = 0; k < nqp; k++)
+        if (k < st0 || k >= en)
+          v.push_back(LimbRefH{(int64_t)((size_t)b * dstride + ((size_t)d * nqp + k) * N), qp_mod(l, k), 0});
+    }
+  auto dr = std::make_unique<DigitRows>();
+  dr->n = (int)v.size();
+  dr->list = DevArray<LimbRefH>(v.size());
+  upload(dr->list.p, v.data(), v.size());
+  const DigitRows& ref = *dr;
+  s.digit_rows[key] = std::move(dr);
+  return ref;
+}
+
 // copy_own: also copy each digit's own rows (the key-product kernels can instead read them from c1)
 void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* digits, bool copy_own = true) {
   Scheme& s = sch();
@@ -398,9 +427,10 @@ void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* di
     u64* D = digits + (size_t)d * nqp * N;
     launch_bconv(coef.p + (size_t)st0 * N, (size_t)(l + 1) * N, ns, bt.tab, D, dstride, batch, trm, s.d_mods.p, N, ns == 1, s.st);
     if (copy_own) copy_rows(D + (size_t)st0 * N, dstride, c1 + (size_t)st0 * N, c1_bstride, (size_t)ns * N, batch);
-    RowMap rm{nqp, l + 1, 0, s.L, st0, en};
-    ntt(D, dstride, batch, rm, true);
   }
+  // one forward transform over the extended rows of every digit of every batch entry
+  const DigitRows& dr = digit_rows(l, batch, dstride);
+  launch_ntt_list(digits, dr.list.p, dr.n, s.logN, true, s.tw, s.st);
 }
 // out[b] (Q rows, stride o_bstride) = ModDown(x[b]) (QP rows, stride x_bstride) [+ add[b<add_batches]] [gathered by perm]
 void mod_down(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t o_bstride, const u64* add = nullptr,
@@ -460,6 +490,8 @@ void ensure_galois_key(u64 galel) {
   Scheme& s = sch();
   if (s.gkeys.count(galel)) return;
   REQUIRE(s.has_sk, "secret key not generated");
+  // the key-product kernels sum at most 16 digit products per accumulator
+  REQUIRE(s.dnum <= 16, "key switching needs at most 16 decomposition digits (len(Q) <= 16 * len(P))");
   const int N = s.N, nm = s.L + s.K, K = s.K;
   u64 M = 2 * (u64)N, ginv = invmod_odd(galel, M);
   std::vector<int8_t> so(N, 0);
@@ -669,7 +701,6 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
   s.logN = logN; s.N = 1 << logN; s.L = (int)q.size(); s.K = (int)p.size();
   s.dnum = (s.L + s.K - 1) / s.K; s.logscale = logscale; s.h = h; s.seed = seed;
   REQUIRE(s.K <= HCK_MAXSRC, "too many special primes");
-  REQUIRE(s.dnum <= 16, "at most 16 decomposition digits (len(Q) <= 16 * len(P))");
   s.mod = q; s.mod.insert(s.mod.end(), p.begin(), p.end());
   for (u64 m : s.mod) {
     REQUIRE(m < (1ULL << 62) && m > 2, "moduli must be < 2^62");
@@ -1470,6 +1501,56 @@ int GetSchemeInfo(int* out, int len) {
     Scheme& s = sch();
     REQUIRE(len >= 6, "buffer too small");
     out[0] = s.logN; out[1] = s.L; out[2] = s.K; out[3] = s.dnum; out[4] = s.logscale; out[5] = s.h;
+    return 0;
+  });
+}
+
+// ---- device buffers owned by the library (callers without their own HIP runtime) ----
+void* DeviceAlloc(size_t bytes) {
+  void* p = nullptr;
+  guard([&] {
+    if (!g_pool) g_pool = new Pool();
+    p = g_pool->get(bytes);
+    return 0;
+  });
+  return p;
+}
+int DeviceFree(void* ptr) {
+  return guard([&] {
+    REQUIRE(g_pool, "no device pool");
+    if (S) sync();
+    g_pool->put(ptr);
+    return 0;
+  });
+}
+int CopyToDevice(void* dst, const void* src, size_t bytes) {
+  return guard([&] { HCHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice)); return 0; });
+}
+int CopyToHost(void* dst, const void* src, size_t bytes) {
+  return guard([&] {
+    if (S) sync();
+    HCHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return 0;
+  });
+}
+
+// ---- batched NTT and RNS multiply-accumulate on device buffers ----
+int NttDevice(uint64_t* data, int npoly, int nrows, int forward) {
+  return guard([&] {
+    Scheme& s = sch();
+    REQUIRE(data && npoly > 0 && nrows > 0 && nrows <= s.L + s.K, "NttDevice: bad arguments");
+    const RowMap rm{nrows, nrows, 0, 0, 0, 0};
+    timed(forward ? "ntt_batch" : "intt_batch", [&] { ntt(data, (size_t)nrows * s.N, npoly, rm, forward != 0); });
+    HCHECK(hipGetLastError());
+    return 0;
+  });
+}
+int MulAccDevice(const uint64_t* a, const uint64_t* b, uint64_t* out, int npoly, int nrows) {
+  return guard([&] {
+    Scheme& s = sch();
+    REQUIRE(a && b && out && npoly > 0 && nrows > 0 && nrows <= s.L + s.K, "MulAccDevice: bad arguments");
+    timed("mulacc", [&] { launch_mulacc(a, b, out, npoly, nrows, s.d_mods.p, s.N, s.st); });
+    HCHECK(hipGetLastError());
     return 0;
   });
 }

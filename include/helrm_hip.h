@@ -131,6 +131,21 @@ int ExportLinearTransformDiagonal(int transformID, int diag, uint64_t* buf, size
 int GetLinearTransformInfo(int transformID, int* out, int len);  /* N1, giant, baby, plaintexts */
 int GetSchemeInfo(int* out, int len);  /* logN, L, K, dnum, logScale, h */
 
+/* ---- [ext] device buffers from the library's allocator (for callers that have
+ *      no HIP runtime of their own; one process should use one HIP runtime) ---- */
+void* DeviceAlloc(size_t bytes);                           /* NULL on failure */
+int DeviceFree(void* ptr);
+int CopyToDevice(void* dst, const void* src, size_t bytes);  /* synchronous */
+int CopyToHost(void* dst, const void* src, size_t bytes);    /* waits for the scheme stream first */
+
+/* ---- [ext] batched transforms on device buffers (kernel microbenchmark) ----------
+ * `data`, `a`, `b`, `out` are device pointers to npoly polynomials of nrows limbs
+ * (limb-major u64[npoly][nrows][N], canonical residues; limb r uses modulus r
+ * of the chain q_0..q_{L-1}, p_0..).  Work is queued on the scheme stream;
+ * Synchronize() waits for it. */
+int NttDevice(uint64_t* data, int npoly, int nrows, int forward);  /* in place; forward != 0: NTT, else inverse */
+int MulAccDevice(const uint64_t* a, const uint64_t* b, uint64_t* out, int npoly, int nrows); /* out = sum_p a_p*b_p */
+
 /* ---- [ext] stream and measurement ------------------------------------------------ */
 int Synchronize(void);
 void* GetStream(void);                                            /* hipStream_t of the scheme */
