@@ -99,7 +99,19 @@ __device__ __forceinline__ int swz(int col) { return col ^ ((col >> 4) & 15); }
 // One limb of a batched transform: word offset from the data base and
 // modulus index.  Either listed explicitly (rows of several digits of a
 // decomposition in one launch) or derived from (RowMap, batch stride).
-struct LimbRef { int64_t off; int mod; int pad; };
+struct LimbRef { int64_t off; int mod; int pad; };  // pad: batch entry (RowMap path)
+
+// ModDown epilogue of a forward transform (the transform of the extension of
+// [x]_P to Q): instead of the transform v, the row pass writes
+//   out[b][row][perm^-1(pos)] = (x[b][row][pos] - v) * P^-1 (+ add[b][row][pos])
+// so the extension never goes back to memory.
+struct ModDownEpi {
+  const u64* x; size_t x_bstride;       // Q rows of the QP polynomial
+  u64* out; size_t o_bstride;
+  const u64* add; size_t a_bstride; int add_batches;
+  const uint32_t* perm_inv;             // nullptr: identity
+  const u64 *pinv, *pinvp;              // [mod] P^-1 mod q and its Shoup companion
+};
 
 struct NttArgs {
   const LimbRef* list;  // nullptr: limb y = (batch y / rows, row y % rows) of rm
@@ -114,6 +126,8 @@ struct NttArgs {
   const u64 *ninv, *ninvp;  // [mod]
   int logN, SA, SB, nsub;   // nsub: sub-transforms per workgroup
   int rows;                 // rm.nact()
+  int epi;                  // forward row pass ends with the ModDown epilogue
+  ModDownEpi e;
 };
 
 __device__ __forceinline__ LimbRef limb_ref(const NttArgs& a, int y) {
@@ -231,8 +245,26 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = csub(csub(v[i], q2), q);
     __syncthreads();
+    if (a.epi) {
+      // ModDown epilogue: limb (batch b, Q row) of the extension
+      const int b = lr.pad, row = (int)((lr.off - (int64_t)b * (int64_t)a.bstride) >> a.logN);
+      const size_t rowoff = ((size_t)row << a.logN) + (size_t)r * C;
+      const u64* xr = a.e.x + (size_t)b * a.e.x_bstride + rowoff;
+      const u64* ar = (a.e.add && b < a.e.add_batches) ? a.e.add + (size_t)b * a.e.a_bstride + rowoff : nullptr;
+      u64* orow = a.e.out + (size_t)b * a.e.o_bstride + ((size_t)row << a.logN);
+      const u64 pi = a.e.pinv[m], pip = a.e.pinvp[m];
 #pragma unroll
-    for (int i = 0; i < 16; i++) poly[j + P * i] = srow[swz(j + P * i)];
+      for (int i = 0; i < 16; i++) {
+        const int pos = j + P * i;
+        u64 o = shoup_mul(sub_mod(xr[pos], srow[swz(pos)], q), pi, pip, q);
+        if (ar) o = add_mod(o, ar[pos], q);
+        const uint32_t gpos = (uint32_t)(r * C + pos);
+        orow[a.e.perm_inv ? a.e.perm_inv[gpos] : gpos] = o;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; i++) poly[j + P * i] = srow[swz(j + P * i)];
+    }
   } else {
     const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + (size_t)r * C;
     // all 16 loads (and the first round's twiddles) in flight before the LDS writes
@@ -332,6 +364,21 @@ void launch_ntt(const u64* src, size_t sstride, u64* data, size_t bstride, int b
   a.tw = reinterpret_cast<const uint4*>(forward ? tw.tw : tw.itw);
   a.twr = reinterpret_cast<const uint4*>(forward ? tw.twr : tw.itwr);
   ntt_launch(a, rows * batch, forward, st);
+}
+
+void launch_ntt_moddown(u64* ext, size_t ext_bstride, int batch, int l, int logN, const u64* x, size_t x_bstride,
+                        u64* out, size_t o_bstride, const u64* add, size_t a_bstride, int add_batches,
+                        const uint32_t* perm_inv, const u64* pinv, const u64* pinvp, const NttTables& tw, hipStream_t st) {
+  const RowMap rm{l + 1, l + 1, 0, 0, 0, 0};
+  NttArgs a{};
+  a.list = nullptr;
+  a.src = ext; a.sstride = ext_bstride; a.data = ext; a.bstride = ext_bstride; a.rm = rm; a.rows = l + 1; a.mods = tw.mods;
+  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN;
+  a.tw = reinterpret_cast<const uint4*>(tw.tw);
+  a.twr = reinterpret_cast<const uint4*>(tw.twr);
+  a.epi = 1;
+  a.e = ModDownEpi{x, x_bstride, out, o_bstride, add, a_bstride, add_batches, perm_inv, pinv, pinvp};
+  ntt_launch(a, (l + 1) * batch, true, st);
 }
 
 void launch_ntt_list(u64* data, const void* list, int nlimbs, int logN, bool forward, const NttTables& tw, hipStream_t st) {

@@ -256,7 +256,7 @@ struct Scheme {
   DU64 pmod_w, pmod_wp, pinv_w, pinv_wp, p0inv_w, p0inv_wp, pmod_plain;
   DU64 rs_inv, rs_invp;  // [l][i] q_l^-1 mod q_i
   std::map<std::pair<int, int>, std::unique_ptr<BConvHost>> bconv;
-  std::map<u64, DevArray<uint32_t>> perms;
+  std::map<u64, DevArray<uint32_t>> perms, perm_invs;
   std::map<std::tuple<int, int, size_t>, std::unique_ptr<struct DigitRows>> digit_rows;
   // keys
   bool has_sk = false, has_pk = false;
@@ -379,6 +379,24 @@ const uint32_t* perm_for(u64 galel) {
   s.perms[galel] = std::move(d);
   return p;
 }
+// inverse of perm_for(galel): out[inv[p]] = in[p]
+const uint32_t* perm_inv_for(u64 galel) {
+  Scheme& s = sch();
+  auto it = s.perm_invs.find(galel);
+  if (it != s.perm_invs.end()) return it->second.p;
+  std::vector<uint32_t> idx(s.N), inv(s.N);
+  u64 mask = 2 * (u64)s.N - 1;
+  for (int i = 0; i < s.N; i++) {
+    u64 e = 2 * (u64)brv(i, s.logN) + 1;
+    u64 t = ((galel * e) & mask) - 1;
+    idx[i] = (uint32_t)brv((int)(t >> 1), s.logN);
+  }
+  for (int i = 0; i < s.N; i++) inv[idx[i]] = (uint32_t)i;
+  DevArray<uint32_t> d(s.N); upload(d.p, inv.data(), inv.size());
+  const uint32_t* p = d.p;
+  s.perm_invs[galel] = std::move(d);
+  return p;
+}
 u64 galois_element(int k) { Scheme& s = sch(); u64 M = 2 * (u64)s.N; return powmod(5, (u64)(i64)k & (M - 1), M); }
 
 // ============================================================================
@@ -432,9 +450,10 @@ void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* di
   const DigitRows& dr = digit_rows(l, batch, dstride);
   launch_ntt_list(digits, dr.list.p, dr.n, s.logN, true, s.tw, s.st);
 }
-// out[b] (Q rows, stride o_bstride) = ModDown(x[b]) (QP rows, stride x_bstride) [+ add[b<add_batches]] [gathered by perm]
+// out[b] (Q rows, stride o_bstride) = ModDown(x[b]) (QP rows, stride x_bstride) [+ add[b<add_batches]],
+// written through perm_inv (out[perm_inv[p]] takes position p; nullptr: identity)
 void mod_down(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t o_bstride, const u64* add = nullptr,
-              size_t a_bstride = 0, int add_batches = 0, const uint32_t* perm = nullptr) {
+              size_t a_bstride = 0, int add_batches = 0, const uint32_t* perm_inv = nullptr) {
   Scheme& s = sch();
   const int N = s.N, K = s.K;
   DU64 pc((size_t)batch * K * N), ext((size_t)batch * (l + 1) * N);
@@ -442,9 +461,9 @@ void mod_down(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t
   ntt_oop(x + (size_t)(l + 1) * N, x_bstride, pc.p, (size_t)K * N, batch, rows_p(), false);
   BConvHost& bt = bconv_table(s.L, s.L + K);
   launch_bconv(pc.p, (size_t)K * N, K, bt.tab, ext.p, (size_t)(l + 1) * N, batch, rows_q(l), s.d_mods.p, N, false, s.st);
-  ntt(ext.p, (size_t)(l + 1) * N, batch, rows_q(l), true);
-  launch_moddown_combine(out, o_bstride, x, x_bstride, ext.p, (size_t)(l + 1) * N, add, a_bstride, add_batches, perm,
-                         s.pinv_w.p, s.pinv_wp.p, l + 1, batch, s.d_mods.p, N, s.st);
+  // forward transform of the extension fused with (x - ext) * P^-1 (+ add), gathered through perm
+  launch_ntt_moddown(ext.p, (size_t)(l + 1) * N, batch, l, s.logN, x, x_bstride, out, o_bstride, add, a_bstride,
+                     add_batches, perm_inv, s.pinv_w.p, s.pinv_wp.p, s.tw, s.st);
 }
 
 const u64* key_ptr(u64 galel, bool for_lt) {
@@ -834,7 +853,7 @@ std::unique_ptr<Cipher> automorphism(const Cipher& ct, u64 galel, bool lt_keyset
   a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
   launch_keymac(a, 1, s.st);
   auto out = new_ct(l, ct.scale); out->logslots = ct.logslots;
-  mod_down(l, dd.p, (size_t)nqp * N, 2, out->d.p, (size_t)(l + 1) * N, ct.d.p, 0, 1, perm_for(galel));
+  mod_down(l, dd.p, (size_t)nqp * N, 2, out->d.p, (size_t)(l + 1) * N, ct.d.p, 0, 1, perm_inv_for(galel));
   return out;
 }
 std::unique_ptr<Cipher> rescale_ct(const Cipher& ct) {
