@@ -101,6 +101,8 @@ def cpu_baseline(q, p, h, key_seed, diagonals, selector, level, logscale, thread
 
 def describe(cfg):
     if cfg["kind"] == "pcmm":
+        if cfg.get("sizes"):
+            return f"{len(cfg['sizes'])}-table embedding PCMM, tables of {cfg['sizes']} rows x {cfg['dim']}"
         return (f"{cfg['fields']}-table embedding PCMM, tables {cfg['rows']}x{cfg['dim']} as base-{cfg['base']} "
                 f"digit sub-tables")
     return f"encrypted dense layer {cfg['out_features']}x{cfg['in_features']}"
@@ -222,7 +224,7 @@ def main():
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1000.0 / args.steps
     # one step = one query: one lookup per table for the embedding PCMM, one forward of the dense layer
-    per_step = cfg["fields"] if cfg["kind"] == "pcmm" else 1
+    per_step = len(cfg.get("sizes") or [0] * cfg.get("fields", 1)) if cfg["kind"] == "pcmm" else 1
     lookups = per_step / (ms / 1000.0)
     if cfg["kind"] == "pcmm":
         metric, unit = (METRIC if args.workload == "pcmm26" else f"encrypted embedding lookups/sec ({args.workload})"), "lookups/s"

@@ -23,8 +23,10 @@ namespace {
 
 constexpr int NTT_TPB = 256;
 
-__device__ __forceinline__ u64 shoup_lazy(u64 x, u64 w, u64 wp, u64 q) {  // x*w mod q in [0, 2q)
-  return x * w - __umul64hi(x, wp) * q;
+// x*w mod q in [0, 2q): x*w - floor(x*wp / 2^64)*q, the subtraction written as
+// an addition of the precomputed 2^64 - q (one carry chain fewer).
+__device__ __forceinline__ u64 shoup_lazy(u64 x, u64 w, u64 wp, u64 q) {
+  return x * w + __umul64hi(x, wp) * (0 - q);
 }
 __device__ __forceinline__ u64 csub(u64 x, u64 m) { return x >= m ? x - m : x; }
 

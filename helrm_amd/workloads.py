@@ -7,6 +7,10 @@
                 block-diagonally packed so the 416 outputs share one ciphertext
   pcmm26_n13    the pcmm26 structure (26 tables, dnum 3, 512 diagonals) at
                 N=2^13 with 9 Q limbs, small enough for the CPU restatement
+  pcmm_ragged_n13  HE-LRM's mixed packing at N=2^13: 10 tables of 3 .. 65536
+                rows, the ones at or below the compression threshold (16) as
+                plain one-hots (FullTable), the others digit-decomposed
+                (RadixTable), so the block-diagonal matrix has ragged blocks
   dense_lt      encrypted dense layer, W 512 outputs x 256 inputs
                 U[-1/sqrt(512), 1/sqrt(512)], input 512 values U[-1, 1];
                 N=2^16, 16 Q limbs, P=[61x6] (dnum 3): 512 diagonals,
@@ -29,6 +33,9 @@ CONFIGS = {
                        fields=26, rows=4096, dim=16, base=16, init="normal", init_arg=0.05),
     "pcmm26": dict(kind="pcmm", logn=16, logq=[60] + [50] * 23, logp=[61] * 8, logscale=50, h=192,
                    fields=26, rows=4096, dim=16, base=16, init="normal", init_arg=0.05),
+    "pcmm_ragged_n13": dict(kind="pcmm", logn=13, logq=[60] + [50] * 6, logp=[61] * 3, logscale=50, h=192,
+                            sizes=[3, 7, 16, 17, 100, 255, 256, 1000, 4096, 65536], threshold=16,
+                            dim=16, base=16, init="uniform_bound"),
     "dense_lt": dict(kind="dense", logn=16, logq=[60] + [50] * 15, logp=[61] * 6, logscale=50, h=192,
                      out_features=512, in_features=256, inputs=512),
     "dense_lt_n13": dict(kind="dense", logn=13, logq=[60] + [50] * 15, logp=[61] * 6, logscale=50, h=192,
@@ -83,22 +90,35 @@ class PCMMWorkload(LinearWorkload):
         super().__init__(backend, name, key_seed)
         c = self.cfg
         rng = np.random.default_rng(seed)
-        width = oh.radix_width(c["rows"], c["base"])
-        self.width = width
+        base, dim = c["base"], c["dim"]
+        sizes = c.get("sizes") or [c["rows"]] * c["fields"]
+        threshold = c.get("threshold", 0)
+        self.sizes, self.threshold = sizes, threshold
         self.tables = []
-        for _ in range(c["fields"]):
+        for size in sizes:
+            if size <= threshold:
+                # FullTable (dlrm.py:85-96): one row per category, plain one-hot selector
+                bound = 1.0 / np.sqrt(max(size, 5))
+                self.tables.append([rng.uniform(-bound, bound, (size, dim)).astype(np.float32)])
+                continue
+            # RadixTable (dlrm.py:99-124): one base x dim table per digit
+            width = oh.radix_width(size, base)
             if c["init"] == "uniform":
-                ts = [rng.uniform(-c["init_arg"], c["init_arg"], (c["base"], c["dim"])).astype(np.float32) for _ in range(width)]
+                ts = [rng.uniform(-c["init_arg"], c["init_arg"], (base, dim)).astype(np.float32) for _ in range(width)]
+            elif c["init"] == "uniform_bound":
+                bound = 1.0 / np.sqrt(size)
+                ts = [rng.uniform(-bound, bound, (base, dim)).astype(np.float32) for _ in range(width)]
             else:
-                ts = [rng.normal(0.0, c["init_arg"], (c["base"], c["dim"])).astype(np.float32) for _ in range(width)]
+                ts = [rng.normal(0.0, c["init_arg"], (base, dim)).astype(np.float32) for _ in range(width)]
             self.tables.append(ts)
-        self.indices = rng.integers(0, c["rows"], c["fields"])
-        sizes = [c["rows"]] * c["fields"]
-        # every table is above the compression threshold: digit one-hots
-        self.selector = oh.expanded_sparse(self.indices, sizes, 0, c["base"])
+        self.indices = np.array([rng.integers(0, s) for s in sizes])
+        self.fields = len(sizes)
+        self.selector = oh.expanded_sparse(self.indices, sizes, threshold, base)
         self.input = self.selector
         self.matrix = oh.block_diag_matrix(self.tables)
-        self.expected = np.concatenate([oh.radix_lookup(t, int(i), c["base"]) for t, i in zip(self.tables, self.indices)])
+        self.expected = np.concatenate([
+            t[0][int(i)] if s <= threshold else oh.radix_lookup(t, int(i), base)
+            for t, i, s in zip(self.tables, self.indices, sizes)])
 
 
 class DenseLTWorkload(LinearWorkload):

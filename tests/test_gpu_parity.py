@@ -127,19 +127,36 @@ def test_add(ctx):
     assert_equal_u64(ctx.lib.export_ciphertext(c), ctx.orc.add(ra, rb, level), "add")
 
 
-@pytest.mark.parametrize("case", ["dense16", "sparse", "ratio1", "above_level"])
+LT_CASES = ["dense16", "sparse", "ratio1", "above_level", "naive", "identity", "shift", "wrap"]
+
+
+@pytest.mark.parametrize("case", LT_CASES)
 def test_linear_transform(ctx, case):
+    """Bit-exact with the oracle; numerically out[i] = sum_k diag_k[i] * in[(i + k) mod S]
+    (tests/oracle/test_linear_transform.py:10-199 closed forms: identity, scale, a single
+    diagonal k is a cyclic left shift by k, several diagonals, input above the LT level)."""
     S = ctx.slots
-    rng = np.random.default_rng({"dense16": 1, "sparse": 2, "ratio1": 3, "above_level": 4}[case])
+    rng = np.random.default_rng(LT_CASES.index(case) + 1)
+    top = ctx.L - 1
     if case == "dense16":
-        idx, ratio, lt_level, ct_level = list(range(16)), 2.0, ctx.L - 1, ctx.L - 1
+        idx, ratio, lt_level, ct_level = list(range(16)), 2.0, top, top
     elif case == "sparse":
-        idx, ratio, lt_level, ct_level = [0, 1, 2, 5, 8, 37, S // 2 + 3], 2.0, ctx.L - 1, ctx.L - 1
+        idx, ratio, lt_level, ct_level = [0, 1, 2, 5, 8, 37, S // 2 + 3], 2.0, top, top
     elif case == "ratio1":
-        idx, ratio, lt_level, ct_level = list(range(0, 40, 3)), 1.0, ctx.L - 1, ctx.L - 1
-    else:
-        idx, ratio, lt_level, ct_level = [0, 1, 2, 5, 8], 2.0, 1, ctx.L - 1
+        idx, ratio, lt_level, ct_level = list(range(0, 40, 3)), 1.0, top, top
+    elif case == "above_level":
+        idx, ratio, lt_level, ct_level = [0, 1, 2, 5, 8], 2.0, 1, top
+    elif case == "naive":  # int(ln 0.1) = -2 < 0: one hoisted rotation per diagonal, no BSGS
+        idx, ratio, lt_level, ct_level = [0, 3, 9, 17], 0.1, top, top
+    elif case == "identity":
+        idx, ratio, lt_level, ct_level = [0], 2.0, top, top
+    elif case == "shift":
+        idx, ratio, lt_level, ct_level = [5], 2.0, top, top
+    else:  # wrap: the last diagonal index shifts by S - 1 (one to the right)
+        idx, ratio, lt_level, ct_level = [S - 1], 2.0, top, top
     data = rng.uniform(-1, 1, (len(idx), S)).astype(np.float32)
+    if case in ("identity", "shift", "wrap"):
+        data[:] = 1.0
     tid = ctx.lib.GenerateLinearTransform(idx, data.reshape(-1), lt_level, ratio, "none")
     t = ctx.orc.lt_new(idx, data, lt_level, ratio)
     assert ctx.lib.lt_info(tid)["N1"] == ctx.orc.lt_n1(t)
@@ -159,4 +176,6 @@ def test_linear_transform(ctx, case):
     dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(r)))
     exp = sum(data[n].astype(np.float64) * np.roll(vals.astype(np.float64), -k) for n, k in enumerate(idx))
     assert np.abs(dec - exp).max() < 0.05
+    if case in ("identity", "shift", "wrap"):
+        np.testing.assert_allclose(dec, np.roll(vals.astype(np.float64), -idx[0]), atol=1e-3)
     ctx.lib.DeleteLinearTransform(tid)

@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 TOL = 2.0 ** -20
 
 
-@pytest.mark.parametrize("name", ["single_table", "pcmm26_n13"])
+@pytest.mark.parametrize("name", ["single_table", "pcmm26_n13", "pcmm_ragged_n13"])
 def test_pcmm_bitexact_vs_oracle(hip_lib, name):
     print(f"[pcmm] {name}: building", flush=True)
     w = PCMMWorkload(hip_lib, name, seed=3, key_seed=17).setup()

@@ -89,3 +89,17 @@ def test_encode_padding_matches_orion():
     pt = s.encode(np.ones(5000), 1)
     assert [c[0] for c in s.backend.calls] == [4096, 4096] and pt.n == 5000
     assert s.backend.calls[0][2] == 1 << 40
+
+
+def test_ragged_selector_and_matrix():
+    """Mixed FullTable / RadixTable packing (dlrm.py:85-124, 202-221, 241-247):
+    the block-diagonal matrix times the selector is the fp32 lookup."""
+    from helrm_amd.workloads import PCMMWorkload
+    w = PCMMWorkload(None, "pcmm_ragged_n13", seed=5)
+    widths = [oh.expanded_width(s, w.threshold, 16) for s in w.sizes]
+    assert widths == [3, 7, 16, 32, 32, 32, 32, 48, 48, 64]
+    assert w.matrix.shape == (16 * len(w.sizes), sum(widths)) and len(w.selector) == sum(widths)
+    assert w.selector.sum() == sum(1 if s <= 16 else oh.radix_width(s, 16) for s in w.sizes)
+    np.testing.assert_allclose(w.matrix.astype(np.float64) @ w.selector, w.expected, atol=1e-6)
+    d, r = oh.diagonalize(w.matrix, 4096)
+    assert r == 4  # block height 256 for 160 outputs
