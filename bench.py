@@ -25,17 +25,18 @@ METRIC = "encrypted embedding lookups/sec (26-table PCMM, N=2^16)"
 HBM_PEAK_GBS = 8000.0
 
 
-def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=8):
+def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=8, chunks=1):
     """Per-PCMM and per-diag-MAC-launch algorithmic HBM bytes (every word once).
 
     PCMM: the diagonals, each of the R rotation keys, the input and the output
-    ciphertext.  Diagonal MAC: the diagonals, the n1-1 hoisted baby rotations
-    (2 QP polys each), P*c (2 Q polys, baby step 0) read, one QP accumulator
-    pair per giant group written."""
+    ciphertext.  Diagonal MAC launch (the giant groups split evenly over
+    `chunks` launches): its share of the diagonals, the n1-1 hoisted baby
+    rotations (2 QP polys each) and P*c (2 Q polys, baby step 0) read, one QP
+    accumulator pair per giant group of the launch written."""
     R = (n1 - 1) + (n2 - 1) + f
     pcmm = D * (L + K) * N * w + R * dnum * 2 * (L + K) * N * w + 2 * L * N * w + 2 * (L - 1) * N * w
-    diag_mac = (D * (L + K) * N * w + (n1 - 1) * 2 * (L + K) * N * w + 2 * L * N * w
-                + n2 * 2 * (L + K) * N * w)
+    diag_mac = (D * (L + K) * N * w + n2 * 2 * (L + K) * N * w) // chunks \
+        + (n1 - 1) * 2 * (L + K) * N * w + 2 * L * N * w
     return pcmm, diag_mac
 
 
@@ -247,13 +248,15 @@ def main():
     L, K = len(cfg["logq"]), len(cfg["logp"])
     N = 1 << cfg["logn"]
     lti = lib.lt_info(list(w.layer.transform_ids.values())[0])
+    # the giant groups are split over this many diagonal-MAC launches per PCMM
+    chunks = max(1, round(kt["diag_mac"]["launches"] / nprof)) if kt["diag_mac"]["launches"] else 1
     pcmm_bytes, mac_bytes = algorithmic_bytes(N=N, L=L, K=K, D=info["diagonals"], n1=lti["baby"], n2=lti["giant"],
-                                              f=info["output_rotations"], dnum=(L + K - 1) // K)
+                                              f=info["output_rotations"], dnum=(L + K - 1) // K, chunks=chunks)
     mac_ms = kt["diag_mac"]["avg_ms"]
     achieved = mac_bytes / (mac_ms / 1000.0) / 1e9 if mac_ms else None
     roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": (achieved / HBM_PEAK_GBS) if achieved else None, "traffic": read_traffic("diag_mac"),
-                "kernel": "diag_mac_kernel", "algorithmic_bytes_per_launch": mac_bytes}
+                "kernel": "diag_mac_kernel", "algorithmic_bytes_per_launch": mac_bytes, "launches_per_pcmm": chunks}
 
     cpu = None
     if not args.no_cpu_baseline:

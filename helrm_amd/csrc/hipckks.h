@@ -50,6 +50,44 @@ __device__ __forceinline__ u64 shoup_mul(u64 x, u64 w, u64 wp, u64 q) {
   u64 r = x * w - qh * q;
   return r >= q ? r - q : r;
 }
+// x >= m ? x - m : x, selecting on the borrow of the 64-bit subtraction
+// (four VALU instructions; the compiler's own form adds a 64-bit compare).
+__device__ __forceinline__ u64 csub_b(u64 x, u64 m) {
+  uint32_t dl, dh;
+  u64 b;
+  asm("v_sub_co_u32_e64 %[dl], %[b], %[xl], %[ml]\n\t"
+      "v_subb_co_u32_e64 %[dh], %[b], %[xh], %[mh], %[b]\n\t"
+      "v_cndmask_b32_e64 %[dl], %[dl], %[xl], %[b]\n\t"
+      "v_cndmask_b32_e64 %[dh], %[dh], %[xh], %[b]"
+      : [dl] "=&v"(dl), [dh] "=&v"(dh), [b] "=&s"(b)
+      : [xl] "v"((uint32_t)x), [xh] "v"((uint32_t)(x >> 32)), [ml] "v"((uint32_t)m), [mh] "v"((uint32_t)(m >> 32)));
+  return ((u64)dh << 32) | dl;
+}
+// High 64 bits of y*p in six VALU instructions: the middle column
+// yl*ph + yh*pl + hi(yl*pl) is summed with the carry-out of v_mad_u64_u32
+// instead of being split into zero-extended halves.
+__device__ __forceinline__ u64 mulhi64(u64 y, u64 p) {
+  const uint32_t yl = (uint32_t)y, yh = (uint32_t)(y >> 32), pl = (uint32_t)p, ph = (uint32_t)(p >> 32);
+  const u64 m1 = (u64)yl * ph + __umulhi(yl, pl);  // < 2^64
+  u64 m2, c;
+  asm("v_mad_u64_u32 %0, %1, %2, %3, %4" : "=v"(m2), "=s"(c) : "v"(yh), "v"(pl), "v"(m1));
+  const u64 r = (u64)yh * ph + (m2 >> 32);  // < 2^64
+  uint32_t rh;
+  u64 c2;
+  asm("v_addc_co_u32_e64 %0, %1, 0, %2, %3" : "=v"(rh), "=s"(c2) : "v"((uint32_t)(r >> 32)), "s"(c));
+  return ((u64)rh << 32) | (uint32_t)r;
+}
+// Shoup product in [0, 2q) for any y < 2^64: y*w + floor(y*wp / 2^64) * nq
+// mod 2^64 with nq = 2^64 - q, the low product added through the addend of
+// v_mad_u64_u32 (no separate 64-bit subtraction).
+__device__ __forceinline__ u64 shoup_lazy(u64 y, u64 w, u64 wp, u64 nq) {
+  const u64 Q = mulhi64(y, wp);
+  const u64 yw = y * w;
+  u64 t, c;
+  asm("v_mad_u64_u32 %0, %1, %2, %3, %4" : "=v"(t), "=s"(c) : "v"((uint32_t)Q), "s"((uint32_t)nq), "v"(yw));
+  const uint32_t th = (uint32_t)(t >> 32) + (uint32_t)Q * (uint32_t)(nq >> 32) + (uint32_t)(Q >> 32) * (uint32_t)nq;
+  return ((u64)th << 32) | (uint32_t)t;
+}
 // 128-bit lazy accumulator: (hi, lo) += a*b, keeping hi < q (needs q < 2^62).
 __device__ __forceinline__ void mac_lazy(u64& lo, u64& hi, u64 a, u64 b, u64 q) {
   u64 plo = a * b, phi = __umul64hi(a, b);

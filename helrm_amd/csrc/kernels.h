@@ -74,6 +74,7 @@ struct DiagMacArgs {
   size_t T_gstride, T_pstride;
   const ModC* mods;
   int N, l, L, K, nqp, lt_level, ng, nbaby, b0, nb_chunk;
+  int g0, g1;               // giant groups [g0, g1) of this launch
 };
 
 // In-place NTT (forward) / inverse NTT of rows rm of `batch` polynomials.

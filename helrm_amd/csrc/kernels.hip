@@ -148,19 +148,33 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
     const ModC mc = mods[m];
     const u64* __restrict__ h = tab.hat + (size_t)m * ns;
     // exact column sums of 16 products (words < 2^62), folded below q
-    u128 acc = 0;
-#pragma unroll
-    for (int i0 = 0; i0 < MAXS; i0 += 16) {
+    u64 res;
+    if (MAXS <= 8) {
+      // y[i] < 2^62 and h[i] < q: at most 8 products sum below 2^65 * q, so
+      // hi < 2q and a single subtraction brings it below q for the REDC
       Acc128 A;
       acc_zero(A);
 #pragma unroll
-      for (int i = i0; i < i0 + 16 && i < MAXS; i++)
+      for (int i = 0; i < MAXS; i++)
         if (i < ns) acc_mac_s(A, y[i], h[i]);
       u64 lo, hi;
       acc_value(A, lo, hi);
-      acc += ((u128)fold_hi4(hi, mc.q) << 64) | lo;
+      res = redc(lo, csub64(hi, mc.q), mc.q, mc.qinv);
+    } else {
+      u128 acc = 0;
+#pragma unroll
+      for (int i0 = 0; i0 < MAXS; i0 += 16) {
+        Acc128 A;
+        acc_zero(A);
+#pragma unroll
+        for (int i = i0; i < i0 + 16 && i < MAXS; i++)
+          if (i < ns) acc_mac_s(A, y[i], h[i]);
+        u64 lo, hi;
+        acc_value(A, lo, hi);
+        acc += ((u128)fold_hi4(hi, mc.q) << 64) | lo;
+      }
+      res = redc((u64)acc, fold_hi4((u64)(acc >> 64), mc.q), mc.q, mc.qinv);
     }
-    u64 res = redc((u64)acc, fold_hi4((u64)(acc >> 64), mc.q), mc.q, mc.qinv);
     res = sub_mod(res, tab.vS[(size_t)m * (ns + 1) + v], mc.q);
     outb[(size_t)row * N + x] = res;
   }
@@ -376,8 +390,9 @@ __device__ __forceinline__ void mac_group(const DiagMacArgs& a, const u64 (&d)[N
     tot0 += ((u128)fold_hi4(hi0, mc.q) << 64) | lo0;
     tot1 += ((u128)fold_hi4(hi1, mc.q) << 64) | lo1;
   }
-  u64 r0 = redc((u64)tot0, fold_hi4((u64)(tot0 >> 64), mc.q), mc.q, mc.qinv);
-  u64 r1 = redc((u64)tot1, fold_hi4((u64)(tot1 >> 64), mc.q), mc.q, mc.qinv);
+  // one chunk: hi < 4q was already folded below q
+  u64 r0 = redc((u64)tot0, NB <= 16 ? (u64)(tot0 >> 64) : fold_hi4((u64)(tot0 >> 64), mc.q), mc.q, mc.qinv);
+  u64 r1 = redc((u64)tot1, NB <= 16 ? (u64)(tot1 >> 64) : fold_hi4((u64)(tot1 >> 64), mc.q), mc.q, mc.qinv);
   if (a.b0 > 0) { r0 = add_mod(r0, T[0], mc.q); r1 = add_mod(r1, T[a.T_pstride], mc.q); }
   __builtin_nontemporal_store(r0, &T[0]);
   __builtin_nontemporal_store(r1, &T[a.T_pstride]);
@@ -410,16 +425,17 @@ __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
   // ping-pong: the next group's NB diagonals are in flight while a group is multiplied
   u64 dA[NB], dB[NB];
   u64* Tb = a.T + (size_t)k * N + x;
-  mac_load<NB, DENSE>(a, dbase, 0, dA);
-  for (int g = 0; g < a.ng; g += 2) {
-    if (g + 1 < a.ng) mac_load<NB, DENSE>(a, dbase, g + 1, dB);
+  mac_load<NB, DENSE>(a, dbase, a.g0, dA);
+  for (int g = a.g0; g < a.g1; g += 2) {
+    if (g + 1 < a.g1) mac_load<NB, DENSE>(a, dbase, g + 1, dB);
     mac_group<NB>(a, dA, s0, s1, mc, Tb + (size_t)g * a.T_gstride);
-    if (g + 1 >= a.ng) break;
-    if (g + 2 < a.ng) mac_load<NB, DENSE>(a, dbase, g + 2, dA);
+    if (g + 1 >= a.g1) break;
+    if (g + 2 < a.g1) mac_load<NB, DENSE>(a, dbase, g + 2, dA);
     mac_group<NB>(a, dB, s0, s1, mc, Tb + (size_t)(g + 1) * a.T_gstride);
   }
 }
 void launch_diag_mac(const DiagMacArgs& a, hipStream_t st) {
+  if (a.g1 <= a.g0) return;
   dim3 grid(a.N / 256, a.nqp, 1);
   const bool dense = a.dense && a.nb_chunk == 16 && a.b0 + 16 <= a.nbaby;
   if (dense) hipLaunchKernelGGL((diag_mac_kernel<16, true>), grid, dim3(256), 0, st, a);

@@ -23,12 +23,7 @@ namespace {
 
 constexpr int NTT_TPB = 256;
 
-// x*w mod q in [0, 2q): x*w - floor(x*wp / 2^64)*q, the subtraction written as
-// an addition of the precomputed 2^64 - q (one carry chain fewer).
-__device__ __forceinline__ u64 shoup_lazy(u64 x, u64 w, u64 wp, u64 q) {
-  return x * w + __umul64hi(x, wp) * (0 - q);
-}
-__device__ __forceinline__ u64 csub(u64 x, u64 m) { return x >= m ? x - m : x; }
+__device__ __forceinline__ u64 csub(u64 x, u64 m) { return csub_b(x, m); }
 
 // Twiddle slots of a round of NST stages over 16 registers: 8 + 4 + ...
 __host__ __device__ constexpr int ntt_round_slots(int nst) { return nst == 0 ? 0 : (16 >> nst) + ntt_round_slots(nst - 1); }
@@ -65,7 +60,7 @@ __device__ __forceinline__ void round_tw_load_tab(RoundTw<NST>& T, const uint4* 
 // NST butterfly stages on v[16] with the preloaded twiddles.
 template <bool FWD, int NST>
 __device__ __forceinline__ void ntt_round(u64 (&v)[16], const RoundTw<NST>& T, u64 q) {
-  const u64 q2 = q + q;
+  const u64 q2 = q + q, nq = 0 - q;
   int sl = 0;
 #pragma unroll
   for (int s = 0; s < NST; s++) {
@@ -82,12 +77,12 @@ __device__ __forceinline__ void ntt_round(u64 (&v)[16], const RoundTw<NST>& T, u
         u64 X = v[i], Y = v[i + rd];
         if (FWD) {
           const u64 x = csub(X, q2);
-          const u64 t = shoup_lazy(Y, w, wp, q);
+          const u64 t = shoup_lazy(Y, w, wp, nq);
           v[i] = x + t;
-          v[i + rd] = x - t + q2;
+          v[i + rd] = x + q2 - t;
         } else {
           v[i] = csub(X + Y, q2);
-          v[i + rd] = shoup_lazy(X - Y + q2, w, wp, q);
+          v[i + rd] = shoup_lazy(X + q2 - Y, w, wp, nq);
         }
       }
     }
@@ -116,7 +111,7 @@ struct ModDownEpi {
 };
 
 struct NttArgs {
-  const LimbRef* list;  // nullptr: limb y = (batch y / rows, row y % rows) of rm
+  const LimbRef* list;  // nullptr: limb y = (row y / batch of rm, batch entry y % batch)
   const u64* src;  // input of the first pass (src == data: in place)
   size_t sstride;
   u64* data;       // output; the second pass works in place on it
@@ -128,13 +123,16 @@ struct NttArgs {
   const u64 *ninv, *ninvp;  // [mod]
   int logN, SA, SB, nsub;   // nsub: sub-transforms per workgroup
   int rows;                 // rm.nact()
+  int batch;
   int epi;                  // forward row pass ends with the ModDown epilogue
   ModDownEpi e;
 };
 
+// Limbs of one modulus are consecutive (row-major over the batch) so that
+// the workgroups in flight share few twiddle tables and those stay in L2.
 __device__ __forceinline__ LimbRef limb_ref(const NttArgs& a, int y) {
   if (a.list) return a.list[y];
-  const int b = y / a.rows, r = a.rm.row(y - b * a.rows);
+  const int ri = y / a.batch, b = y - ri * a.batch, r = a.rm.row(ri);
   LimbRef l;
   l.off = (int64_t)b * (int64_t)a.bstride + ((int64_t)r << a.logN);
   l.mod = a.rm.mod(r);
@@ -203,7 +201,7 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_col_kernel(NttArgs a) {
     ntt_round<false, 4>(v, T2, q);
     const u64 ni = a.ninv[m], nip = a.ninvp[m];
 #pragma unroll
-    for (int i = 0; i < 16; i++) poly[(size_t)(j + P * i) * C] = csub(shoup_lazy(v[i], ni, nip, q), q);
+    for (int i = 0; i < 16; i++) poly[(size_t)(j + P * i) * C] = csub(shoup_lazy(v[i], ni, nip, 0 - q), q);
   }
 }
 
@@ -361,7 +359,8 @@ void launch_ntt(const u64* src, size_t sstride, u64* data, size_t bstride, int b
   if (rows <= 0 || batch <= 0) return;
   NttArgs a{};
   a.list = nullptr;
-  a.src = src; a.sstride = sstride; a.data = data; a.bstride = bstride; a.rm = rm; a.rows = rows; a.mods = tw.mods;
+  a.src = src; a.sstride = sstride; a.data = data; a.bstride = bstride; a.rm = rm; a.rows = rows; a.batch = batch;
+  a.mods = tw.mods;
   a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN;
   a.tw = reinterpret_cast<const uint4*>(forward ? tw.tw : tw.itw);
   a.twr = reinterpret_cast<const uint4*>(forward ? tw.twr : tw.itwr);
@@ -374,7 +373,8 @@ void launch_ntt_moddown(u64* ext, size_t ext_bstride, int batch, int l, int logN
   const RowMap rm{l + 1, l + 1, 0, 0, 0, 0};
   NttArgs a{};
   a.list = nullptr;
-  a.src = ext; a.sstride = ext_bstride; a.data = ext; a.bstride = ext_bstride; a.rm = rm; a.rows = l + 1; a.mods = tw.mods;
+  a.src = ext; a.sstride = ext_bstride; a.data = ext; a.bstride = ext_bstride; a.rm = rm; a.rows = l + 1; a.batch = batch;
+  a.mods = tw.mods;
   a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN;
   a.tw = reinterpret_cast<const uint4*>(tw.tw);
   a.twr = reinterpret_cast<const uint4*>(tw.twr);
@@ -387,7 +387,7 @@ void launch_ntt_list(u64* data, const void* list, int nlimbs, int logN, bool for
   if (nlimbs <= 0) return;
   NttArgs a{};
   a.list = reinterpret_cast<const LimbRef*>(list);
-  a.src = data; a.data = data; a.mods = tw.mods; a.rows = 1;
+  a.src = data; a.data = data; a.mods = tw.mods; a.rows = 1; a.batch = 1;
   a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN;
   a.tw = reinterpret_cast<const uint4*>(forward ? tw.tw : tw.itw);
   a.twr = reinterpret_cast<const uint4*>(forward ? tw.twr : tw.itwr);

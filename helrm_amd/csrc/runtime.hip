@@ -246,7 +246,7 @@ struct Scheme {
   int logN = 0, N = 0, L = 0, K = 0, dnum = 0, logscale = 0, h = 0;
   u64 seed = 0;
   std::vector<u64> mod;
-  hipStream_t st = nullptr;
+  hipStream_t st = nullptr;  // every public call is ordered on st
   DevArray<ModC> d_mods;
   DU64 tw2, itw2, ninv, ninvp;  // interleaved (w, w') twiddle pairs [mod][N][2]
   DU64 twr2, itwr2;             // row-pass consecutive-round twiddles, lane-interleaved
@@ -275,6 +275,9 @@ struct Scheme {
   std::vector<int> rotgroup;
   Timing timing;
   bool encoder = false, encryptor = false, decryptor = false, evaluator = false, lteval = false;
+  ~Scheme() {
+    if (st) { (void)hipStreamSynchronize(st); (void)hipStreamDestroy(st); }
+  }
 };
 Scheme* S = nullptr;
 u64 g_seed_override = 0;
@@ -413,14 +416,15 @@ const DigitRows& digit_rows(int l, int batch, size_t dstride) {
   auto it = s.digit_rows.find(key);
   if (it != s.digit_rows.end()) return *it->second;
   const int N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
+  // modulus-major, so that consecutive limbs share their twiddle tables in L2
   std::vector<LimbRefH> v;
-  for (int b = 0; b < batch; b++)
-    for (int d = 0; d < dn; d++) {
-      const int st0 = d * K, en = std::min(st0 + K, l + 1);
-      for (int k = 0; k < nqp; k++)
+  for (int k = 0; k < nqp; k++)
+    for (int b = 0; b < batch; b++)
+      for (int d = 0; d < dn; d++) {
+        const int st0 = d * K, en = std::min(st0 + K, l + 1);
         if (k < st0 || k >= en)
           v.push_back(LimbRefH{(int64_t)((size_t)b * dstride + ((size_t)d * nqp + k) * N), qp_mod(l, k), 0});
-    }
+      }
   auto dr = std::make_unique<DigitRows>();
   dr->n = (int)v.size();
   dr->list = DevArray<LimbRefH>(v.size());
@@ -802,7 +806,7 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
     S = old;
     throw;
   }
-  if (old) { HCHECK(hipStreamSynchronize(old->st)); (void)hipStreamDestroy(old->st); delete old; }
+  delete old;
   sp.release();
 }
 
@@ -1054,19 +1058,18 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct) {
   }
   // 3. fused diagonal MAC -> T[g][2][nqp][N]
   DU64 T((size_t)ng * 2 * qp);
-  {
-    DiagMacArgs a{};
-    a.diag = t.diags.p; a.diag_stride = (size_t)(t.level + 1 + K) * N;
-    a.R = R.p; a.R_bstride = 2 * qp; a.R_pstride = qp;
-    a.pc = pc.p; a.pc_pstride = (size_t)(l + 1) * N;
-    a.baby_is_zero = t.d_bzero.p; a.baby_slot = t.d_bslot.p; a.gpi = t.d_gpi.p; a.dense = t.dense ? 1 : 0;
-    a.zero_pidx = (int)t.plain_idx.size();
-    a.T = T.p; a.T_gstride = 2 * qp; a.T_pstride = qp; a.mods = s.d_mods.p;
-    a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.lt_level = t.level; a.ng = ng; a.nbaby = nb;
-    for (int b0 = 0; b0 < nb; b0 += 32) {
-      a.b0 = b0; a.nb_chunk = std::min(32, nb - b0);
-      timed("diag_mac", [&] { launch_diag_mac(a, s.st); });
-    }
+  DiagMacArgs dm{};
+  dm.diag = t.diags.p; dm.diag_stride = (size_t)(t.level + 1 + K) * N;
+  dm.R = R.p; dm.R_bstride = 2 * qp; dm.R_pstride = qp;
+  dm.pc = pc.p; dm.pc_pstride = (size_t)(l + 1) * N;
+  dm.baby_is_zero = t.d_bzero.p; dm.baby_slot = t.d_bslot.p; dm.gpi = t.d_gpi.p; dm.dense = t.dense ? 1 : 0;
+  dm.zero_pidx = (int)t.plain_idx.size();
+  dm.T = T.p; dm.T_gstride = 2 * qp; dm.T_pstride = qp; dm.mods = s.d_mods.p;
+  dm.N = N; dm.l = l; dm.L = s.L; dm.K = K; dm.nqp = nqp; dm.lt_level = t.level; dm.ng = ng; dm.nbaby = nb;
+  dm.g0 = 0; dm.g1 = ng;
+  for (int b0 = 0; b0 < nb; b0 += 32) {
+    dm.b0 = b0; dm.nb_chunk = std::min(32, nb - b0);
+    timed("diag_mac", [&] { launch_diag_mac(dm, s.st); });
   }
   // 4. giant groups with a nonzero rotation: ModDown of part 1, decomposition, key product + automorphism + accumulate
   DU64 acc((size_t)2 * qp);
@@ -1252,7 +1255,7 @@ int NewSchemeWithModuli(int logN, const uint64_t* q, int lenQ, const uint64_t* p
 }
 int DeleteScheme(void) {
   return guard([&] {
-    if (S) { (void)hipStreamSynchronize(S->st); (void)hipStreamDestroy(S->st); delete S; S = nullptr; }
+    if (S) { delete S; S = nullptr; }
     if (g_pool) g_pool->release_all();
     return 0;
   });
