@@ -206,7 +206,7 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_col_kernel(NttArgs a) {
 }
 
 // Row pass (pass B): workgroup = nsub rows x C columns.
-template <bool FWD, int S>
+template <bool FWD, int S, bool EPI = false>
 __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
   __shared__ u64 sm[4096];
   constexpr int P = 1 << (S - 4);
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = csub(csub(v[i], q2), q);
     __syncthreads();
-    if (a.epi) {
+    if (EPI) {
       // ModDown epilogue: limb (batch b, Q row) of the extension
       const int b = lr.pad, row = (int)((lr.off - (int64_t)b * (int64_t)a.bstride) >> a.logN);
       const size_t rowoff = ((size_t)row << a.logN) + (size_t)r * C;
@@ -253,13 +253,31 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
       const u64* ar = (a.e.add && b < a.e.add_batches) ? a.e.add + (size_t)b * a.e.a_bstride + rowoff : nullptr;
       u64* orow = a.e.out + (size_t)b * a.e.o_bstride + ((size_t)row << a.logN);
       const u64 pi = a.e.pinv[m], pip = a.e.pinvp[m];
+      // every load of the epilogue is issued before the first use, so the
+      // latencies overlap instead of adding up word by word
+      u64 xv[16], av[16];
+      uint32_t dst[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) xv[i] = xr[j + P * i];
+      if (ar) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) av[i] = ar[j + P * i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) av[i] = 0;
+      }
+      if (a.e.perm_inv) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) dst[i] = a.e.perm_inv[r * C + j + P * i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) dst[i] = (uint32_t)(r * C + j + P * i);
+      }
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         const int pos = j + P * i;
-        u64 o = shoup_mul(sub_mod(xr[pos], srow[swz(pos)], q), pi, pip, q);
-        if (ar) o = add_mod(o, ar[pos], q);
-        const uint32_t gpos = (uint32_t)(r * C + pos);
-        orow[a.e.perm_inv ? a.e.perm_inv[gpos] : gpos] = o;
+        const u64 o = shoup_mul(sub_mod(xv[i], srow[swz(pos)], q), pi, pip, q);
+        orow[dst[i]] = add_mod(o, av[i], q);
       }
     } else {
 #pragma unroll
@@ -267,13 +285,14 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
     }
   } else {
     const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + (size_t)r * C;
-    // all 16 loads (and the first round's twiddles) in flight before the LDS writes
-    RoundTw<S - 4> T1;
-    round_tw_load_tab<S - 4>(T1, twr, P);
+    // all 16 loads in flight before the LDS writes; the first round's
+    // twiddles are issued behind them and arrive during the barrier
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = in[j + P * i];
 #pragma unroll
     for (int i = 0; i < 16; i++) srow[swz(j + P * i)] = v[i];
+    RoundTw<S - 4> T1;
+    round_tw_load_tab<S - 4>(T1, twr, P);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 16; i++) v[i] = srow[swz(16 * j + i)];
@@ -300,14 +319,21 @@ void launch_col(int S, dim3 grid, dim3 block, const NttArgs& a, hipStream_t st) 
     default: hipLaunchKernelGGL((ntt_col_kernel<FWD, 8>), grid, block, 0, st, a); break;
   }
 }
+// The ModDown epilogue is its own instantiation so that the plain forward
+// pass keeps its smaller register footprint (and occupancy).
+template <bool FWD, bool EPI>
+void launch_row_t(int S, dim3 grid, dim3 block, const NttArgs& a, hipStream_t st) {
+  switch (S) {
+    case 5: hipLaunchKernelGGL((ntt_row_kernel<FWD, 5, EPI>), grid, block, 0, st, a); break;
+    case 6: hipLaunchKernelGGL((ntt_row_kernel<FWD, 6, EPI>), grid, block, 0, st, a); break;
+    case 7: hipLaunchKernelGGL((ntt_row_kernel<FWD, 7, EPI>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((ntt_row_kernel<FWD, 8, EPI>), grid, block, 0, st, a); break;
+  }
+}
 template <bool FWD>
 void launch_row(int S, dim3 grid, dim3 block, const NttArgs& a, hipStream_t st) {
-  switch (S) {
-    case 5: hipLaunchKernelGGL((ntt_row_kernel<FWD, 5>), grid, block, 0, st, a); break;
-    case 6: hipLaunchKernelGGL((ntt_row_kernel<FWD, 6>), grid, block, 0, st, a); break;
-    case 7: hipLaunchKernelGGL((ntt_row_kernel<FWD, 7>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((ntt_row_kernel<FWD, 8>), grid, block, 0, st, a); break;
-  }
+  if (FWD && a.epi) launch_row_t<true, true>(S, grid, block, a, st);
+  else launch_row_t<FWD, false>(S, grid, block, a, st);
 }
 
 }  // namespace
