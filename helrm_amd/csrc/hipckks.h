@@ -146,8 +146,8 @@ __device__ __forceinline__ void acc_value(const Acc128& A, u64& lo, u64& hi) {
 // Montgomery reduction of T = hi*2^64 + lo < q*2^64: returns T * 2^-64 mod q.
 __device__ __forceinline__ u64 redc(u64 lo, u64 hi, u64 q, u64 qinv) {
   u64 m = lo * qinv;
-  u64 t = hi + __umul64hi(m, q) + (lo != 0 ? 1 : 0);
-  return t >= q ? t - q : t;
+  u64 t = hi + mulhi64(m, q) + (lo != 0 ? 1 : 0);
+  return csub_b(t, q);
 }
 __device__ __forceinline__ u64 mont_mul(u64 a, u64 bR, u64 q, u64 qinv) {
   return redc(a * bR, __umul64hi(a, bR), q, qinv);

@@ -100,7 +100,22 @@ void launch_mont_mul(u64* out, size_t obstride, const u64* a, size_t abstride, c
 void launch_mont_convert(u64* data, size_t bstride, int batch, RowMap rm, const ModC* mods, int N, bool to, hipStream_t st);
 void launch_permute(u64* out, const u64* in, size_t bstride, int batch, int rows, const uint32_t* perm, int N, hipStream_t st);
 // Basis extension of the ns source rows of `in` into the target rows rm of `out`.
-void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable& tab, u64* out, size_t out_bstride, int batch, const RowMap& rm, const ModC* mods, int N, bool force_v0, hipStream_t st);
+// One source group of a batched basis extension (e.g. one digit of a
+// decomposition): its table (device copy), source rows, destination rows.
+struct BConvJob {
+  const BConvTable* tab;
+  int src_row, ns, force_v0, pad;
+  RowMap rm;
+  size_t out_off;  // word offset of the group's output inside a batch entry
+};
+#define HCK_MAXJOBS 16
+struct BConvJobs { BConvJob j[HCK_MAXJOBS]; int n, rows_per_block; };
+// Basis extension of every job for every batch entry, in one launch.
+void launch_bconv(const u64* in, size_t in_bstride, BConvJobs jobs, u64* out, size_t out_bstride, int batch,
+                  const ModC* mods, int N, hipStream_t st);
+// Single source group: the sources are rows [0, ns) of in.
+void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable* dtab, u64* out, size_t out_bstride, int batch,
+                  const RowMap& rm, const ModC* mods, int N, bool force_v0, hipStream_t st);
 void launch_moddown_combine(u64* out, size_t o_bstride, const u64* x, size_t x_bstride, const u64* ext, size_t e_bstride, const u64* add, size_t a_bstride, int add_batches, const uint32_t* perm, const u64* pinv, const u64* pinvp, int qrows, int batch, const ModC* mods, int N, hipStream_t st);
 void launch_keymac(const KeyMacArgs& a, int batch, hipStream_t st);
 void launch_giant_acc(const GiantAccArgs& a, hipStream_t st);

@@ -5,6 +5,7 @@
 // wrappers at the bottom of this file.
 #include "hipckks.h"
 #include "kernels.h"
+#include <algorithm>
 
 // High word of a 128-bit sum of products of words < q < 2^62: after at most
 // 16 products (plus one earlier fold) it is below 5q; bring it below q.
@@ -118,35 +119,48 @@ void launch_copy(u64* dst, size_t dstride, const u64* src, size_t sstride, size_
 // exact in 128 bits (folded below 4t after every 16 products), then one
 // Montgomery REDC removes the 2^64 the (S/s_i mod t) table carries.
 // ---------------------------------------------------------------------------
-// NS > 0: exactly NS sources (the constants of a destination row are one
-// scalar load); NS == 0: ns sources at run time, at most MAXS.
-template <int MAXS, int NS>
-__global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, size_t in_bstride, int ns_rt,
-                                                    BConvTable tab, u64* __restrict__ out, size_t out_bstride,
-                                                    RowMap rm, const ModC* __restrict__ mods, int N, int force_v0) {
-  const int ns = NS > 0 ? NS : ns_rt;
+// At most MAXS sources.  With MAXS == 8 every row takes 8 products: the
+// sources past ns are zero and the table holds 8 spare words at its end, so
+// a job of 7 sources runs the same straight-line code as one of 8.
+// blockIdx.z selects (batch entry, job): all digits of a decomposition go
+// in one launch.
+template <int MAXS>
+__global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, size_t in_bstride, BConvJobs jobs,
+                                                    u64* __restrict__ out, size_t out_bstride,
+                                                    const ModC* __restrict__ mods, int N) {
+  const int b = blockIdx.z / jobs.n, d = blockIdx.z - b * jobs.n;
+  const BConvJob& J = jobs.j[d];
+  const BConvTable* __restrict__ tab = J.tab;
+  const int ns = J.ns;
   const int x = blockIdx.x * blockDim.x + threadIdx.x;
-  const u64* inb = in + (size_t)blockIdx.z * in_bstride;
-  u64* outb = out + (size_t)blockIdx.z * out_bstride;
+  const u64* inb = in + (size_t)b * in_bstride + (size_t)J.src_row * N;
+  u64* outb = out + (size_t)b * out_bstride + J.out_off;
   u64 y[MAXS];
   double vf = 0.0;
+  // every source word in flight at once (rows past ns re-read row 0, unused)
+#pragma unroll
+  for (int i = 0; i < MAXS; i++) y[i] = inb[(size_t)(i < ns ? i : 0) * N + x];
 #pragma unroll
   for (int i = 0; i < MAXS; i++) {
-    y[i] = 0;
     if (i < ns) {
-      const BConvSrc s = tab.src[i];
-      y[i] = shoup_mul(inb[(size_t)i * N + x], s.hinv, s.hinvp, s.q);
+      const BConvSrc s = tab->src[i];
+      y[i] = shoup_mul(y[i], s.hinv, s.hinvp, s.q);
       vf += (double)y[i] / s.qd;
+    } else {
+      y[i] = 0;
     }
   }
-  const int v = force_v0 ? 0 : (int)(u64)vf;
-  const int r0 = blockIdx.y * tab.rows_per_block;
-  const int r1 = min(r0 + tab.rows_per_block, rm.nact());
+  const int v = J.force_v0 ? 0 : (int)(u64)vf;
+  const RowMap rm = J.rm;
+  const int r0 = blockIdx.y * jobs.rows_per_block;
+  const int r1 = min(r0 + jobs.rows_per_block, rm.nact());
+  const u64* __restrict__ hat = tab->hat;
+  const u64* __restrict__ vS = tab->vS;
   for (int r = r0; r < r1; r++) {
     const int row = rm.row(r);
     const int m = rm.mod(row);
     const ModC mc = mods[m];
-    const u64* __restrict__ h = tab.hat + (size_t)m * ns;
+    const u64* __restrict__ h = hat + (size_t)m * ns;
     // exact column sums of 16 products (words < 2^62), folded below q
     u64 res;
     if (MAXS <= 8) {
@@ -155,8 +169,7 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
       Acc128 A;
       acc_zero(A);
 #pragma unroll
-      for (int i = 0; i < MAXS; i++)
-        if (i < ns) acc_mac_s(A, y[i], h[i]);
+      for (int i = 0; i < MAXS; i++) acc_mac_s(A, y[i], h[i]);  // y[i] = 0 past ns
       u64 lo, hi;
       acc_value(A, lo, hi);
       res = redc(lo, csub64(hi, mc.q), mc.q, mc.qinv);
@@ -175,31 +188,39 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
       }
       res = redc((u64)acc, fold_hi4((u64)(acc >> 64), mc.q), mc.q, mc.qinv);
     }
-    res = sub_mod(res, tab.vS[(size_t)m * (ns + 1) + v], mc.q);
+    res = sub_mod(res, vS[(size_t)m * (ns + 1) + v], mc.q);
     outb[(size_t)row * N + x] = res;
   }
 }
-void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable& tab, u64* out, size_t out_bstride, int batch,
-                  const RowMap& rm, const ModC* mods, int N, bool force_v0, hipStream_t st) {
-  const int nrows = rm.nact();
-  if (nrows <= 0 || batch <= 0) return;
-  BConvTable t = tab;
+void launch_bconv(const u64* in, size_t in_bstride, BConvJobs jobs, u64* out, size_t out_bstride, int batch,
+                  const ModC* mods, int N, hipStream_t st) {
+  if (jobs.n <= 0 || batch <= 0) return;
+  int nrows = 0, nsmax = 0;
+  for (int d = 0; d < jobs.n; d++) {
+    nrows = std::max(nrows, jobs.j[d].rm.nact());
+    nsmax = std::max(nsmax, jobs.j[d].ns);
+  }
+  if (nrows <= 0) return;
   // all destination rows in one thread unless that leaves too few workgroups
   const int cols = N / 256;
   int ny = 1;
-  while (ny < nrows && (long)cols * batch * ny < 2048) ny *= 2;
-  t.rows_per_block = (nrows + ny - 1) / ny;
-  ny = (nrows + t.rows_per_block - 1) / t.rows_per_block;
-  dim3 grid(cols, ny, batch);
-  const int fv = force_v0 ? 1 : 0;
-  if (ns == 8)
-    hipLaunchKernelGGL((bconv_kernel<8, 8>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rm, mods, N, fv);
-  else if (ns < 8)
-    hipLaunchKernelGGL((bconv_kernel<8, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rm, mods, N, fv);
-  else if (ns <= 16)
-    hipLaunchKernelGGL((bconv_kernel<16, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rm, mods, N, fv);
+  while (ny < nrows && (long)cols * batch * jobs.n * ny < 2048) ny *= 2;
+  jobs.rows_per_block = (nrows + ny - 1) / ny;
+  ny = (nrows + jobs.rows_per_block - 1) / jobs.rows_per_block;
+  dim3 grid(cols, ny, batch * jobs.n);
+  if (nsmax <= 8)
+    hipLaunchKernelGGL((bconv_kernel<8>), grid, dim3(256), 0, st, in, in_bstride, jobs, out, out_bstride, mods, N);
+  else if (nsmax <= 16)
+    hipLaunchKernelGGL((bconv_kernel<16>), grid, dim3(256), 0, st, in, in_bstride, jobs, out, out_bstride, mods, N);
   else
-    hipLaunchKernelGGL((bconv_kernel<HCK_MAXSRC, 0>), grid, dim3(256), 0, st, in, in_bstride, ns, t, out, out_bstride, rm, mods, N, fv);
+    hipLaunchKernelGGL((bconv_kernel<HCK_MAXSRC>), grid, dim3(256), 0, st, in, in_bstride, jobs, out, out_bstride, mods, N);
+}
+void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable* dtab, u64* out, size_t out_bstride, int batch,
+                  const RowMap& rm, const ModC* mods, int N, bool force_v0, hipStream_t st) {
+  BConvJobs jobs{};
+  jobs.n = 1;
+  jobs.j[0] = BConvJob{dtab, 0, ns, force_v0 ? 1 : 0, 0, rm, 0};
+  launch_bconv(in, in_bstride, jobs, out, out_bstride, batch, mods, N, st);
 }
 
 // ModDown combine: out = (x - ext) * P^-1 (+ add) [gathered through perm]

@@ -60,7 +60,7 @@ __device__ __forceinline__ void round_tw_load_tab(RoundTw<NST>& T, const uint4* 
 // NST butterfly stages on v[16] with the preloaded twiddles.
 template <bool FWD, int NST>
 __device__ __forceinline__ void ntt_round(u64 (&v)[16], const RoundTw<NST>& T, u64 q) {
-  const u64 q2 = q + q, nq = 0 - q;
+  const u64 q2 = q + q, q4 = q2 + q2, nq = 0 - q;
   int sl = 0;
 #pragma unroll
   for (int s = 0; s < NST; s++) {
@@ -76,7 +76,12 @@ __device__ __forceinline__ void ntt_round(u64 (&v)[16], const RoundTw<NST>& T, u
         const int i = (k << sh) + r;
         u64 X = v[i], Y = v[i + rd];
         if (FWD) {
-          const u64 x = csub(X, q2);
+          // Harvey butterflies with the reduction of X on every other stage
+          // (q < 2^61): a reducing stage takes X < 8q to x < 4q and leaves
+          // outputs < 6q, the next one skips it and leaves outputs < 8q; the
+          // last stage of every round reduces, so rounds start below 6q.
+          const bool reduce = ((NST - 1 - s) & 1) == 0;
+          const u64 x = reduce ? csub(X, q4) : X;
           const u64 t = shoup_lazy(Y, w, wp, nq);
           v[i] = x + t;
           v[i + rd] = x + q2 - t;
@@ -243,7 +248,7 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
     ntt_round<true, S - 4>(v, T2, q);
     const u64 q2 = q + q;
 #pragma unroll
-    for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = csub(csub(v[i], q2), q);
+    for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = csub(csub(csub(v[i], q2 + q2), q2), q);
     __syncthreads();
     if (EPI) {
       // ModDown epilogue: limb (batch b, Q row) of the extension

@@ -238,7 +238,7 @@ struct LinTrans {
   bool ptrs_ready = false;
 };
 
-struct BConvHost { int ns; BConvTable tab; DU64 hat, vS; };
+struct BConvHost { int ns; BConvTable tab; DU64 hat, vS; DevArray<BConvTable> dtab; };
 
 struct Timing { bool on = false; std::map<std::string, std::vector<std::pair<hipEvent_t, hipEvent_t>>> ev; std::map<std::string, std::pair<long, double>> acc; };
 
@@ -358,9 +358,11 @@ BConvHost& bconv_table(int s0, int s1) {
       hat[(size_t)m * ns + i] = mulmod(pr, R, t);
     }
   }
+  hat.resize(hat.size() + 8, 0);  // spare words: the 8-source kernel reads h[ns..7] (times zero) past the last row
   b->hat = DU64(hat.size()); upload(b->hat.p, hat.data(), hat.size());
   b->vS = DU64(vS.size()); upload(b->vS.p, vS.data(), vS.size());
   b->tab.hat = b->hat.p; b->tab.vS = b->vS.p; b->tab.rows_per_block = 8;
+  b->dtab = DevArray<BConvTable>(1); upload(b->dtab.p, &b->tab, 1);
   auto& ref = *b;
   s.bconv[key] = std::move(b);
   return ref;
@@ -441,15 +443,22 @@ void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* di
   const size_t dstride = (size_t)dn * nqp * N;
   DU64 coef((size_t)batch * (l + 1) * N);
   ntt_oop(c1, c1_bstride, coef.p, (size_t)(l + 1) * N, batch, rows_q(l), false);
+  // every digit's extension in one launch: targets are every QP row except the digit's own [st0, en)
+  REQUIRE(dn <= HCK_MAXJOBS, "too many decomposition digits");
+  BConvJobs jobs{};
+  jobs.n = dn;
   for (int d = 0; d < dn; d++) {
-    int st0 = d * K, en = std::min(st0 + K, l + 1), ns = en - st0;
-    BConvHost& bt = bconv_table(st0, en);
-    // targets: every QP row except the digit's own [st0, en)
-    RowMap trm{nqp, l + 1, 0, s.L, st0, en};
-    u64* D = digits + (size_t)d * nqp * N;
-    launch_bconv(coef.p + (size_t)st0 * N, (size_t)(l + 1) * N, ns, bt.tab, D, dstride, batch, trm, s.d_mods.p, N, ns == 1, s.st);
-    if (copy_own) copy_rows(D + (size_t)st0 * N, dstride, c1 + (size_t)st0 * N, c1_bstride, (size_t)ns * N, batch);
+    const int st0 = d * K, en = std::min(st0 + K, l + 1), ns = en - st0;
+    jobs.j[d] = BConvJob{bconv_table(st0, en).dtab.p, st0, ns, ns == 1 ? 1 : 0, 0, RowMap{nqp, l + 1, 0, s.L, st0, en},
+                         (size_t)d * nqp * N};
   }
+  launch_bconv(coef.p, (size_t)(l + 1) * N, jobs, digits, dstride, batch, s.d_mods.p, N, s.st);
+  if (copy_own)
+    for (int d = 0; d < dn; d++) {
+      const int st0 = d * K, ns = std::min(st0 + K, l + 1) - st0;
+      u64* D = digits + (size_t)d * nqp * N;
+      copy_rows(D + (size_t)st0 * N, dstride, c1 + (size_t)st0 * N, c1_bstride, (size_t)ns * N, batch);
+    }
   // one forward transform over the extended rows of every digit of every batch entry
   const DigitRows& dr = digit_rows(l, batch, dstride);
   launch_ntt_list(digits, dr.list.p, dr.n, s.logN, true, s.tw, s.st);
@@ -464,7 +473,7 @@ void mod_down(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t
   // P rows of x (rows l+1.. of each batch entry) -> coefficient domain in pc
   ntt_oop(x + (size_t)(l + 1) * N, x_bstride, pc.p, (size_t)K * N, batch, rows_p(), false);
   BConvHost& bt = bconv_table(s.L, s.L + K);
-  launch_bconv(pc.p, (size_t)K * N, K, bt.tab, ext.p, (size_t)(l + 1) * N, batch, rows_q(l), s.d_mods.p, N, false, s.st);
+  launch_bconv(pc.p, (size_t)K * N, K, bt.dtab.p, ext.p, (size_t)(l + 1) * N, batch, rows_q(l), s.d_mods.p, N, false, s.st);
   // forward transform of the extension fused with (x - ext) * P^-1 (+ add), gathered through perm
   launch_ntt_moddown(ext.p, (size_t)(l + 1) * N, batch, l, s.logN, x, x_bstride, out, o_bstride, add, a_bstride,
                      add_batches, perm_inv, s.pinv_w.p, s.pinv_wp.p, s.tw, s.st);
@@ -726,7 +735,7 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
   REQUIRE(s.K <= HCK_MAXSRC, "too many special primes");
   s.mod = q; s.mod.insert(s.mod.end(), p.begin(), p.end());
   for (u64 m : s.mod) {
-    REQUIRE(m < (1ULL << 62) && m > 2, "moduli must be < 2^62");
+    REQUIRE(m < (1ULL << 61) && m > 2, "moduli must be < 2^61");
     REQUIRE((m - 1) % (2 * (u64)s.N) == 0, "moduli must be 1 mod 2N");
     REQUIRE(is_prime(m), "moduli must be prime");
   }
@@ -1170,7 +1179,7 @@ std::unique_ptr<Cipher> encrypt_pt(const Plain& pt) {
   // ModDown from Q + {p_0} in the coefficient domain
   DU64 ext((size_t)2 * (l + 1) * N);
   BConvHost& bt = bconv_table(s.L, s.L + 1);
-  launch_bconv(tt.p + (size_t)(l + 1) * N, (size_t)nr * N, 1, bt.tab, ext.p, (size_t)(l + 1) * N, 2, rows_q(l), s.d_mods.p, N, false, s.st);
+  launch_bconv(tt.p + (size_t)(l + 1) * N, (size_t)nr * N, 1, bt.dtab.p, ext.p, (size_t)(l + 1) * N, 2, rows_q(l), s.d_mods.p, N, false, s.st);
   auto out = new_ct(l, pt.scale); out->logslots = pt.logslots;
   launch_moddown_combine(out->d.p, (size_t)(l + 1) * N, tt.p, (size_t)nr * N, ext.p, (size_t)(l + 1) * N, nullptr, 0, 0, nullptr,
                          s.p0inv_w.p, s.p0inv_wp.p, l + 1, 2, s.d_mods.p, N, s.st);
