@@ -104,8 +104,12 @@ def describe(cfg):
     if cfg["kind"] == "pcmm":
         if cfg.get("sizes"):
             return f"{len(cfg['sizes'])}-table embedding PCMM, tables of {cfg['sizes']} rows x {cfg['dim']}"
-        return (f"{cfg['fields']}-table embedding PCMM, tables {cfg['rows']}x{cfg['dim']} as base-{cfg['base']} "
-                f"digit sub-tables")
+        d = (f"{cfg['fields']}-table embedding PCMM, tables {cfg['rows']}x{cfg['dim']} as base-{cfg['base']} "
+             f"digit sub-tables")
+        if cfg.get("repack"):
+            w, start = cfg["repack"]
+            d += f" + sparse_to_top repack Linear copy_into({cfg['fields'] * cfg['dim']}, {w}, {start})"
+        return d
     return f"encrypted dense layer {cfg['out_features']}x{cfg['in_features']}"
 
 

@@ -899,6 +899,11 @@ void add_inplace(Cipher& a, const Cipher& b, bool sub) {
   int l = std::min(a.level, b.level);
   ct_drop_to(a, l);
   const size_t bs_b = (size_t)(b.level + 1) * s.N;
+  if (b.level == l) {
+    // both parts in one launch (same row stride in a and b)
+    launch_add(a.d.p, a.d.p, b.d.p, bs_b, 2, rows_q(l), s.d_mods.p, s.N, sub, s.st);
+    return;
+  }
   for (int p = 0; p < 2; p++)
     launch_add(a.d.p + (size_t)p * (l + 1) * s.N, a.d.p + (size_t)p * (l + 1) * s.N, b.d.p + (size_t)p * bs_b, 0, 1, rows_q(l), s.d_mods.p, s.N, sub, s.st);
 }

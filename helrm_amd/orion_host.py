@@ -122,6 +122,16 @@ def block_diag_matrix(field_tables):
     return M
 
 
+def copy_into(width, output_width, start):
+    """Weight of the repacking Linear of examples/criteo/dlrm.py:174-178
+    (bias=False): output_width x width, identity block at rows
+    [start, start + width) -- HELRM.sparse_to_top moves the 416 embedding
+    outputs behind the 16 bottom-MLP features of the top MLP input."""
+    w = np.zeros((output_width, width), dtype=np.float32)
+    w[start:start + width, :width] = np.eye(width, dtype=np.float32)
+    return w
+
+
 # --------------------------------------------------------------------------
 # hybrid diagonal extraction (orion/core/packing.py:626-865, uniform path)
 # --------------------------------------------------------------------------

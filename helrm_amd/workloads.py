@@ -11,6 +11,11 @@
                 rows, the ones at or below the compression threshold (16) as
                 plain one-hots (FullTable), the others digit-decomposed
                 (RadixTable), so the block-diagonal matrix has ragged blocks
+  pcmm26_top    pcmm26 followed by HELRM.sparse_to_top (dlrm.py:194-198,
+                228): the repacking Linear copy_into(416, 432, 16) at the
+                next level, on the same kernels (64 diagonals, 6 fold
+                rotations); output slots [16, 432) hold the embeddings
+  pcmm26_top_n13  the same two layers at N=2^13
   dense_lt      encrypted dense layer, W 512 outputs x 256 inputs
                 U[-1/sqrt(512), 1/sqrt(512)], input 512 values U[-1, 1];
                 N=2^16, 16 Q limbs, P=[61x6] (dnum 3): 512 diagonals,
@@ -36,6 +41,10 @@ CONFIGS = {
     "pcmm_ragged_n13": dict(kind="pcmm", logn=13, logq=[60] + [50] * 6, logp=[61] * 3, logscale=50, h=192,
                             sizes=[3, 7, 16, 17, 100, 255, 256, 1000, 4096, 65536], threshold=16,
                             dim=16, base=16, init="uniform_bound"),
+    "pcmm26_top": dict(kind="pcmm", logn=16, logq=[60] + [50] * 23, logp=[61] * 8, logscale=50, h=192,
+                       fields=26, rows=4096, dim=16, base=16, init="normal", init_arg=0.05, repack=(432, 16)),
+    "pcmm26_top_n13": dict(kind="pcmm", logn=13, logq=[60] + [50] * 8, logp=[61] * 3, logscale=50, h=192,
+                           fields=26, rows=4096, dim=16, base=16, init="normal", init_arg=0.05, repack=(432, 16)),
     "dense_lt": dict(kind="dense", logn=16, logq=[60] + [50] * 15, logp=[61] * 6, logscale=50, h=192,
                      out_features=512, in_features=256, inputs=512),
     "dense_lt_n13": dict(kind="dense", logn=13, logq=[60] + [50] * 15, logp=[61] * 6, logscale=50, h=192,
@@ -121,6 +130,44 @@ class PCMMWorkload(LinearWorkload):
             for t, i, s in zip(self.tables, self.indices, sizes)])
 
 
+class SparseToTopWorkload(PCMMWorkload):
+    """HELRM.sparse then HELRM.sparse_to_top (dlrm.py:226-230): the embedding
+    PCMM and the repacking Linear copy_into(416, 432, 16), compiled one level
+    below it, evaluated back to back on the same kernels."""
+
+    def __init__(self, backend, name="pcmm26_top", seed=0, key_seed=1):
+        super().__init__(backend, name, seed=seed, key_seed=key_seed)
+        out_width, start = self.cfg["repack"]
+        width = self.matrix.shape[0]
+        self.repack_matrix = oh.copy_into(width, out_width, start)
+        self.lookup = self.expected
+        self.expected = np.zeros(out_width, dtype=np.float64)
+        self.expected[start:start + width] = self.lookup
+        self.repack = None
+
+    def setup(self):
+        super().setup()
+        self.repack = oh.LinearLayer(self.scheme, self.repack_matrix, level=self.layer.level - 1).compile()
+        return self
+
+    def run(self):
+        emb = self.layer.forward(self.ct_in)
+        out = self.repack.forward(emb)
+        emb.free()
+        return out
+
+    def decrypt_output(self, out):
+        vals = self.scheme.decode(self.scheme.decrypt(out))
+        return vals[: self.repack_matrix.shape[0]]
+
+    def shape_info(self):
+        info = super().shape_info()
+        info["repack"] = {"diagonals": len(self.repack.diagonals[(0, 0)]),
+                          "output_rotations": self.repack.output_rotations,
+                          "matrix": list(self.repack_matrix.shape)}
+        return info
+
+
 class DenseLTWorkload(LinearWorkload):
     """Encrypted dense layer y = W x (orion.nn.Linear without bias)."""
 
@@ -135,5 +182,9 @@ class DenseLTWorkload(LinearWorkload):
 
 
 def make_workload(backend, name, seed=0, key_seed=1):
-    cls = PCMMWorkload if CONFIGS[name]["kind"] == "pcmm" else DenseLTWorkload
+    c = CONFIGS[name]
+    if c["kind"] == "pcmm":
+        cls = SparseToTopWorkload if c.get("repack") else PCMMWorkload
+    else:
+        cls = DenseLTWorkload
     return cls(backend, name, seed=seed, key_seed=key_seed)

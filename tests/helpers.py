@@ -60,3 +60,21 @@ def oracle_pcmm(orc, diagonals, output_rotations, level, selector, logscale, enc
     b = np.zeros(1, np.float32) if bias is None else bias
     out[0] = orc.add(out[0][None], orc.encode(b, l, scale)[None], l)[0]
     return out, l, sc
+
+
+def oracle_linear(orc, ct, level, scale, diagonals, output_rotations, logscale, bias=None, bsgs_ratio=2.0):
+    """One more Orion Linear (LT at `level`, rescale, hybrid fold, bias) on an
+    oracle ciphertext at `level` and `scale`.  Returns (ct, level, scale)."""
+    idx = list(diagonals.keys())
+    data = np.stack([diagonals[i] for i in idx])
+    t = orc.lt_new(idx, data, level, bsgs_ratio)
+    out, l = orc.lt_eval(t, ct, level)
+    sc = scale * orc.q[level]
+    out = orc.rescale(out, l)
+    sc /= orc.q[l]
+    l -= 1
+    for i in range(1, output_rotations + 1):
+        out = orc.add(out, orc.rotate(out, l, orc.slots // (2 ** i)), l)
+    b = np.zeros(1, np.float32) if bias is None else bias
+    out[0] = orc.add(out[0][None], orc.encode(b, l, float(1 << logscale))[None], l)[0]
+    return out, l, sc

@@ -10,9 +10,9 @@ transform -> rescale -> hybrid fold -> bias -> decrypt -> decode.
 import numpy as np
 import pytest
 
-from helpers import assert_equal_u64, oracle_pcmm
+from helpers import assert_equal_u64, oracle_linear, oracle_pcmm
 from oracle import oracle as O
-from helrm_amd.workloads import PCMMWorkload
+from helrm_amd.workloads import PCMMWorkload, SparseToTopWorkload
 
 pytestmark = pytest.mark.gpu
 
@@ -59,6 +59,53 @@ def test_pcmm26_full_size_decrypts(hip_lib):
     # the fold leaves the output periodic with period 512: slot j+512 decrypts to row j as well
     full = np.asarray(w.scheme.decode(w.scheme.decrypt(out.__class__(w.scheme, out.ids, 2 * 512))))
     assert np.abs(full[512:512 + 416] - w.expected).max() < TOL
+    hip_lib.DeleteScheme()
+
+
+def test_sparse_to_top_bitexact_vs_oracle(hip_lib):
+    """HELRM.sparse then HELRM.sparse_to_top (dlrm.py:226-230) at N=2^13:
+    both layers bit-exact with the restatement, then the 416 embeddings
+    decrypt at slots [16, 432) of the top-MLP input within 2^-20."""
+    name = "pcmm26_top_n13"
+    print(f"[pcmm] {name}: building", flush=True)
+    w = SparseToTopWorkload(hip_lib, name, seed=3, key_seed=17).setup()
+    info = w.shape_info()
+    print(f"[pcmm] {name}: {info}", flush=True)
+    assert info["repack"]["diagonals"] == 1 and info["repack"]["output_rotations"] == 3
+    out = w.run()
+    got = hip_lib.export_ciphertext(out.ids[0])
+    c = w.cfg
+    orc = O.Oracle(c["logn"], hip_lib.GetModuliChain(), hip_lib.GetAuxModuliChain(), h=c["h"], seed=17)
+    try:
+        ct1, l1, sc1 = oracle_pcmm(orc, w.layer.diagonals[(0, 0)], w.layer.output_rotations, w.layer.level,
+                                   w.selector, c["logscale"], 0)
+        assert l1 == w.repack.level
+        want, l2, sc2 = oracle_linear(orc, ct1, l1, sc1, w.repack.diagonals[(0, 0)], w.repack.output_rotations,
+                                      c["logscale"])
+        assert hip_lib.GetCiphertextLevel(out.ids[0]) == l2
+        assert hip_lib.GetCiphertextScaleDouble(out.ids[0]) == sc2
+        assert_equal_u64(got, want, f"{name} sparse_to_top output")
+    finally:
+        orc.close()
+    y = w.decrypt_output(out)
+    err = np.abs(y - w.expected).max()
+    print(f"[pcmm] {name}: max |decrypted - expected| = {err:.3e}", flush=True)
+    assert err < TOL
+    hip_lib.DeleteScheme()
+
+
+def test_sparse_to_top_full_size_decrypts(hip_lib):
+    print("[pcmm] pcmm26_top (N=2^16): building", flush=True)
+    w = SparseToTopWorkload(hip_lib, "pcmm26_top", seed=3, key_seed=17).setup()
+    info = w.shape_info()
+    print(f"[pcmm] pcmm26_top: {info}", flush=True)
+    assert info["repack"]["diagonals"] == 1 and info["repack"]["output_rotations"] == 6
+    out = w.run()
+    y = w.decrypt_output(out)
+    err = np.abs(y - w.expected).max()
+    print(f"[pcmm] pcmm26_top: max |decrypted - expected| = {err:.3e}", flush=True)
+    assert err < TOL
+    assert np.abs(y[:16]).max() < TOL
     hip_lib.DeleteScheme()
 
 

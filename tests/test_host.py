@@ -52,6 +52,36 @@ def test_pcmm26_shapes():
     np.testing.assert_allclose(w.matrix @ w.selector, w.expected, atol=1e-6)
 
 
+@pytest.mark.parametrize("S", [4096, 32768])
+def test_sparse_to_top_repack(S):
+    """HELRM.sparse_to_top = copy_into(416, 432, 16) (dlrm.py:174-178, 194-198):
+    the hybrid packing keeps diagonals i < 512 only, so the shift by 16 is the
+    single diagonal 512 - 16, nonzero in the last 512-slot block alone (the
+    fold adds the blocks); log2(S/512) fold rotations; on the periodic PCMM
+    output layout (slot j holds row j mod 512, rows >= 416 zero) the LT + fold
+    puts the 416 embeddings at slots [16, 432)."""
+    W = oh.copy_into(416, 432, 16)
+    assert W.shape == (432, 416) and W[16:, :].trace() == 416 and W.sum() == 416
+    d, rots = oh.diagonalize(W, S, "hybrid", False)
+    assert rots == int(math.log2(S // 512))
+    assert list(d[(0, 0)]) == [496]
+    nz = np.nonzero(d[(0, 0)][496])[0]
+    assert nz.min() == S - 512 + 16 and nz.max() == S - 512 + 431 and len(nz) == 416
+    rng = np.random.default_rng(S)
+    emb = rng.standard_normal(416)
+    x = np.zeros(S)
+    for k in range(S // 512):
+        x[512 * k:512 * k + 416] = emb
+    y = np.zeros(S)
+    for i, v in d[(0, 0)].items():
+        y += v.astype(np.float64) * np.roll(x, -i)
+    for i in range(1, rots + 1):
+        y = y + np.roll(y, -(S // 2 ** i))
+    want = np.zeros(432)
+    want[16:] = emb
+    np.testing.assert_allclose(y[:432], want, atol=1e-12)
+
+
 def test_digits_and_selector():
     """examples/criteo/dlrm.py:66-82, 202-221."""
     assert oh.digits(201, 16, 2).tolist() == [9, 12]
