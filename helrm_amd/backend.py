@@ -155,6 +155,19 @@ _SIGNATURES = {
     "AddCiphertextNew": ([_I, _I], _I),
     "SubCiphertext": ([_I, _I], _I),
     "SubCiphertextNew": ([_I, _I], _I),
+    "Negate": ([_I], _I),
+    "AddScalar": ([_I, _c.c_float], _I),
+    "AddScalarNew": ([_I, _c.c_float], _I),
+    "SubScalar": ([_I, _c.c_float], _I),
+    "SubScalarNew": ([_I, _c.c_float], _I),
+    "MulScalarInt": ([_I, _I], _I),
+    "MulScalarIntNew": ([_I, _I], _I),
+    "MulScalarFloat": ([_I, _c.c_float], _I),
+    "MulScalarFloatNew": ([_I, _c.c_float], _I),
+    "MulPlaintext": ([_I, _I], _I),
+    "MulPlaintextNew": ([_I, _I], _I),
+    "MulRelinCiphertext": ([_I, _I], _I),
+    "MulRelinCiphertextNew": ([_I, _I], _I),
     # linear transforms
     "NewLinearTransformEvaluator": ([], _I),
     "GenerateLinearTransform": ([_PI, _I, _PF, _I, _I, _c.c_float, _c.c_char_p], _I),

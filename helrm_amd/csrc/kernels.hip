@@ -60,6 +60,21 @@ void launch_mont_mul(u64* out, size_t obstride, const u64* a, size_t abstride, c
   hipLaunchKernelGGL(mont_mul_kernel, dim3(N / 256, rm.nact(), batch), dim3(256), 0, st, out, a, abstride, bR, bbstride, obstride, rm, mods, N, acc ? 1 : 0);
 }
 
+// out[row] = in[row] +- c[modulus of row] (a constant in every NTT slot)
+__global__ void add_scalar_kernel(u64* __restrict__ out, const u64* __restrict__ in, RowMap rm, const u64* __restrict__ c,
+                                  const ModC* __restrict__ mods, int N, int sub) {
+  int x = blockIdx.x * blockDim.x + threadIdx.x;
+  int row = rm.row(blockIdx.y);
+  int m = rm.mod(row);
+  u64 q = mods[m].q;
+  size_t o = (size_t)row * N + x;
+  out[o] = sub ? sub_mod(in[o], c[m], q) : add_mod(in[o], c[m], q);
+}
+void launch_add_scalar(u64* out, const u64* in, RowMap rm, const u64* c, const ModC* mods, int N, bool sub, hipStream_t st) {
+  if (rm.nact() <= 0) return;
+  hipLaunchKernelGGL(add_scalar_kernel, dim3(N / 256, rm.nact(), 1), dim3(256), 0, st, out, in, rm, c, mods, N, sub ? 1 : 0);
+}
+
 // v -> v*R mod q (to Montgomery form) or v*R^-1 (from), in place
 __global__ void mont_convert_kernel(u64* __restrict__ data, size_t bstride, RowMap rm, const ModC* __restrict__ mods, int N, int to) {
   int x = blockIdx.x * blockDim.x + threadIdx.x;

@@ -145,6 +145,8 @@ inline u64 ST_GK_E(u64 g, u64 d) { return (5ULL << 56) | (g << 8) | d; }
 inline u64 ST_ENC_U(u64 e) { return (6ULL << 56) | e; }
 inline u64 ST_ENC_E0(u64 e) { return (7ULL << 56) | e; }
 inline u64 ST_ENC_E1(u64 e) { return (8ULL << 56) | e; }
+inline u64 ST_RLK_A(u64 d) { return (9ULL << 56) | d; }
+inline u64 ST_RLK_E(u64 d) { return (10ULL << 56) | d; }
 // ternary vector with exactly h entries +-1 (partial Fisher-Yates)
 std::vector<int8_t> ternary_hw(u64 seed, u64 stream, int N, int h) {
   std::vector<int> idx(N);
@@ -263,6 +265,7 @@ struct Scheme {
   std::vector<int8_t> s;
   DU64 sR, pkR;
   std::map<u64, std::unique_ptr<DU64>> gkeys;
+  std::unique_ptr<DU64> rlk;  // relinearization key s^2 -> s
   std::set<u64> rot_keys, lt_keys;
   u64 enc_counter = 0;
   // registries
@@ -518,13 +521,33 @@ void gen_public() {
   sync();
   s.has_pk = true;
 }
+// Evaluation key from s_in to s_out (NTT, Montgomery form, all QP rows):
+// dnum digits of (b_d, a_d), b_d = -a_d s_out + e_d + [P s_in on the rows of digit d].
+template <class FA, class FE>
+std::unique_ptr<DU64> gen_eval_key(const u64* s_inR, const u64* s_outR, FA st_a, FE st_e) {
+  Scheme& s = sch();
+  const int N = s.N, nm = s.L + s.K, K = s.K;
+  auto key = std::make_unique<DU64>((size_t)s.dnum * 2 * nm * N);
+  for (int d = 0; d < s.dnum; d++) {
+    u64* b = key->p + (size_t)d * 2 * nm * N;
+    u64* a = b + (size_t)nm * N;
+    launch_sample_uniform(a, rows_all(), s.seed, st_a(d), s.d_mods.p, N, s.st);
+    ntt(a, 0, 1, rows_all(), true);
+    launch_sample_cbd(b, rows_all(), s.seed, st_e(d), s.d_mods.p, N, false, s.st);
+    ntt(b, 0, 1, rows_all(), true);
+    launch_gk_combine(b, a, s_outR, s_inR, d * K, std::min((d + 1) * K, s.L), s.pmod_plain.p, nm, s.d_mods.p, N, s.st);
+  }
+  launch_mont_convert(key->p, (size_t)nm * N, 2 * s.dnum, rows_all(), s.d_mods.p, N, true, s.st);
+  sync();
+  return key;
+}
 void ensure_galois_key(u64 galel) {
   Scheme& s = sch();
   if (s.gkeys.count(galel)) return;
   REQUIRE(s.has_sk, "secret key not generated");
   // the key-product kernels sum at most 16 digit products per accumulator
   REQUIRE(s.dnum <= 16, "key switching needs at most 16 decomposition digits (len(Q) <= 16 * len(P))");
-  const int N = s.N, nm = s.L + s.K, K = s.K;
+  const int N = s.N, nm = s.L + s.K;
   u64 M = 2 * (u64)N, ginv = invmod_odd(galel, M);
   std::vector<int8_t> so(N, 0);
   for (int i = 0; i < N; i++) { u64 t = ((u64)i * ginv) % M; if (t < (u64)N) so[t] = (int8_t)(so[t] + s.s[i]); else so[t - N] = (int8_t)(so[t - N] - s.s[i]); }
@@ -533,19 +556,20 @@ void ensure_galois_key(u64 galel) {
   launch_signed_rows(soR.p, rows_all(), dso.p, s.d_mods.p, N, s.st);
   ntt(soR.p, 0, 1, rows_all(), true);
   launch_mont_convert(soR.p, 0, 1, rows_all(), s.d_mods.p, N, true, s.st);
-  auto key = std::make_unique<DU64>((size_t)s.dnum * 2 * nm * N);
-  for (int d = 0; d < s.dnum; d++) {
-    u64* b = key->p + (size_t)d * 2 * nm * N;
-    u64* a = b + (size_t)nm * N;
-    launch_sample_uniform(a, rows_all(), s.seed, ST_GK_A(galel, d), s.d_mods.p, N, s.st);
-    ntt(a, 0, 1, rows_all(), true);
-    launch_sample_cbd(b, rows_all(), s.seed, ST_GK_E(galel, d), s.d_mods.p, N, false, s.st);
-    ntt(b, 0, 1, rows_all(), true);
-    launch_gk_combine(b, a, soR.p, s.sR.p, d * K, std::min((d + 1) * K, s.L), s.pmod_plain.p, nm, s.d_mods.p, N, s.st);
-  }
-  launch_mont_convert(key->p, (size_t)nm * N, 2 * s.dnum, rows_all(), s.d_mods.p, N, true, s.st);
-  sync();
-  s.gkeys[galel] = std::move(key);
+  s.gkeys[galel] = gen_eval_key(s.sR.p, soR.p, [galel](int d) { return ST_GK_A(galel, (u64)d); },
+                                 [galel](int d) { return ST_GK_E(galel, (u64)d); });
+}
+// Relinearization key: s^2 -> s (Lattigo GenRelinearizationKey), same
+// generator as the oracle's, random streams ST_RLK_A/E(d).
+void ensure_relin_key() {
+  Scheme& s = sch();
+  if (s.rlk) return;
+  REQUIRE(s.has_sk, "secret key not generated");
+  REQUIRE(s.dnum <= 16, "key switching needs at most 16 decomposition digits (len(Q) <= 16 * len(P))");
+  const int N = s.N, nm = s.L + s.K;
+  DU64 s2R((size_t)nm * N);  // s^2 in Montgomery form: mont_mul(sR, sR) = s^2 R
+  launch_mont_mul(s2R.p, 0, s.sR.p, 0, s.sR.p, 0, 1, rows_all(), s.d_mods.p, N, false, s.st);
+  s.rlk = gen_eval_key(s2R.p, s.sR.p, [](int d) { return ST_RLK_A((u64)d); }, [](int d) { return ST_RLK_E((u64)d); });
 }
 
 // ============================================================================
@@ -867,6 +891,102 @@ std::unique_ptr<Cipher> automorphism(const Cipher& ct, u64 galel, bool lt_keyset
   launch_keymac(a, 1, s.st);
   auto out = new_ct(l, ct.scale); out->logslots = ct.logslots;
   mod_down(l, dd.p, (size_t)nqp * N, 2, out->d.p, (size_t)(l + 1) * N, ct.d.p, 0, 1, perm_inv_for(galel));
+  return out;
+}
+// ---- plaintext, scalar and ciphertext products (Lattigo ckks Evaluator
+// Mul / Add with a constant / MulRelin, restated for the GPU) ----
+
+// Lattigo's scaled real constant (float64 encoding precision): v * scale
+// rounded to double, then +-0.5 in double, truncated toward zero.
+int64_t scaled_constant(double v, double scale) {
+  double t = v * scale;
+  REQUIRE(t < 4611686018427387904.0 && t > -4611686018427387904.0, "scaled constant exceeds 2^62");
+  if (t > 0) t = t + 0.5; else if (t < 0) t = t - 0.5;
+  return (int64_t)t;
+}
+u64 residue_i64(int64_t k, u64 q) {
+  if (k >= 0) return (u64)k % q;
+  u64 m = (u64)(-(k + 1)) % q;
+  m = (m + 1) % q;
+  return m ? q - m : 0;
+}
+// both parts of c (level l) times the integer k, in place
+void mul_int_inplace(Cipher& c, int64_t k) {
+  Scheme& s = sch();
+  const int l = c.level, nm = s.L + s.K;
+  std::vector<u64> w(nm, 0), wp(nm, 0);
+  for (int i = 0; i <= l; i++) { w[i] = residue_i64(k, s.mod[i]); wp[i] = shoup(w[i], s.mod[i]); }
+  DU64 dw(nm), dwp(nm);
+  upload(dw.p, w.data(), nm); upload(dwp.p, wp.data(), nm);
+  launch_mul_const(c.d.p, c.d.p, (size_t)(l + 1) * s.N, 2, rows_q(l), dw.p, dwp.p, s.d_mods.p, s.N, s.st);
+  sync();  // the constant tables are freed on return
+}
+// Mul(ct, float64): integer-valued constants multiply as integers (scale
+// unchanged); others are scaled by q_l and rounded, and the scale grows by q_l
+void mul_float_inplace(Cipher& c, double v) {
+  Scheme& s = sch();
+  if (v < 4611686018427387904.0 && v > -4611686018427387904.0 && v == (double)(int64_t)v) {
+    mul_int_inplace(c, (int64_t)v);
+    return;
+  }
+  const int64_t k = scaled_constant(v, (double)s.mod[c.level]);
+  mul_int_inplace(c, k);
+  c.scale *= (double)s.mod[c.level];
+}
+// Add(ct, float64): round(v * scale) added to (subtracted from) every NTT slot of part 0
+void add_const_inplace(Cipher& c, double v, bool sub) {
+  Scheme& s = sch();
+  const int l = c.level, nm = s.L + s.K;
+  const int64_t k = scaled_constant(v, c.scale);
+  std::vector<u64> kq(nm, 0);
+  for (int i = 0; i <= l; i++) kq[i] = residue_i64(k, s.mod[i]);
+  DU64 dk(nm);
+  upload(dk.p, kq.data(), nm);
+  launch_add_scalar(c.d.p, c.d.p, rows_q(l), dk.p, s.d_mods.p, s.N, sub, s.st);
+  sync();
+}
+// Mul(ct, pt): both parts times the plaintext at level min(ct, pt); scales multiply
+std::unique_ptr<Cipher> mul_plain_ct(const Cipher& ct, const Plain& pt) {
+  Scheme& s = sch();
+  const int l = std::min(ct.level, pt.level), N = s.N;
+  DU64 pR((size_t)(l + 1) * N);
+  d2d(pR.p, pt.d.p, (size_t)(l + 1) * N * 8);
+  launch_mont_convert(pR.p, 0, 1, rows_q(l), s.d_mods.p, N, true, s.st);
+  auto out = new_ct(l, ct.scale * pt.scale); out->logslots = ct.logslots;
+  launch_mont_mul(out->d.p, (size_t)(l + 1) * N, ct.d.p, (size_t)(ct.level + 1) * N, pR.p, 0, 2, rows_q(l), s.d_mods.p, N,
+                  false, s.st);
+  return out;
+}
+// MulRelin(a, b): tensor (a0 b0, a0 b1 + a1 b0, a1 b1) at level min, then the
+// third part key switched with the relinearization key and added
+std::unique_ptr<Cipher> mul_relin_ct(const Cipher& a, const Cipher& b) {
+  Scheme& s = sch();
+  REQUIRE(s.rlk, "relinearization key not generated");
+  const int l = std::min(a.level, b.level), N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
+  const size_t ps = (size_t)(l + 1) * N;
+  const u64 *a0 = a.d.p, *a1 = a.d.p + (size_t)(a.level + 1) * N;
+  const u64 *b0 = b.d.p, *b1 = b.d.p + (size_t)(b.level + 1) * N;
+  DU64 bR(2 * ps), d2(ps);
+  copy_rows(bR.p, ps, b.d.p, (size_t)(b.level + 1) * N, ps, 2);
+  launch_mont_convert(bR.p, ps, 2, rows_q(l), s.d_mods.p, N, true, s.st);
+  auto out = new_ct(l, a.scale * b.scale); out->logslots = a.logslots;
+  u64 *o0 = out->d.p, *o1 = out->d.p + ps;
+  launch_mont_mul(o0, 0, a0, 0, bR.p, 0, 1, rows_q(l), s.d_mods.p, N, false, s.st);
+  launch_mont_mul(o1, 0, a0, 0, bR.p + ps, 0, 1, rows_q(l), s.d_mods.p, N, false, s.st);
+  launch_mont_mul(o1, 0, a1, 0, bR.p, 0, 1, rows_q(l), s.d_mods.p, N, true, s.st);
+  launch_mont_mul(d2.p, 0, a1, 0, bR.p + ps, 0, 1, rows_q(l), s.d_mods.p, N, false, s.st);
+  (void)b0; (void)b1;
+  DU64 digits((size_t)dn * nqp * N), dd((size_t)2 * nqp * N);
+  decompose_modup(l, d2.p, 0, 1, digits.p, false);
+  KeyMacArgs k{};
+  k.digits = digits.p; k.dig_bstride = 0; k.digits_per_batch = 0; k.key = nullptr; k.perm = nullptr;
+  k.key1 = s.rlk->p; k.perm1 = nullptr; k.add0 = nullptr;
+  k.own = d2.p; k.own_bstride = 0;
+  k.out0 = dd.p; k.out1 = dd.p + (size_t)nqp * N; k.out_bstride = 0; k.mods = s.d_mods.p;
+  k.N = N; k.l = l; k.L = s.L; k.K = K; k.nqp = nqp; k.dn = dn;
+  launch_keymac(k, 1, s.st);
+  // out = ModDown(dd) + (d0, d1): the epilogue reads and writes each word in one thread
+  mod_down(l, dd.p, (size_t)nqp * N, 2, out->d.p, ps, out->d.p, ps, 2, nullptr);
   return out;
 }
 std::unique_ptr<Cipher> rescale_ct(const Cipher& ct) {
@@ -1287,7 +1407,7 @@ int GeneratePrimes(int logN, const int* logQ, int lenQ, const int* logP, int len
 int NewKeyGenerator(void) { return guard([&] { sch(); return 0; }); }
 int GenerateSecretKey(void) { return guard([&] { gen_secret(); return 0; }); }
 int GeneratePublicKey(void) { return guard([&] { gen_public(); return 0; }); }
-int GenerateRelinearizationKey(void) { return guard([&] { sch(); return 0; }); }
+int GenerateRelinearizationKey(void) { return guard([&] { ensure_relin_key(); return 0; }); }
 int GenerateEvaluationKeys(void) { return guard([&] { sch(); return 0; }); }
 
 // ---- encoder ----
@@ -1374,6 +1494,29 @@ int SubCiphertext(int a, int b) { return guard([&] { add_inplace(get_ct(a), get_
 int SubCiphertextNew(int a, int b) { return guard([&] { auto c = copy_ct(get_ct(a)); add_inplace(*c, get_ct(b), true); return push_ct(std::move(c)); }); }
 int AddPlaintext(int ct, int pt) { return guard([&] { add_plain_inplace(get_ct(ct), get_pt(pt), false); return ct; }); }
 int AddPlaintextNew(int ct, int pt) { return guard([&] { auto c = copy_ct(get_ct(ct)); add_plain_inplace(*c, get_pt(pt), false); return push_ct(std::move(c)); }); }
+int MulPlaintext(int ct, int pt) {
+  return guard([&] { Cipher& c = get_ct(ct); auto r = mul_plain_ct(c, get_pt(pt)); c = std::move(*r); return ct; });
+}
+int MulPlaintextNew(int ct, int pt) { return guard([&] { return push_ct(mul_plain_ct(get_ct(ct), get_pt(pt))); }); }
+int MulScalarInt(int ct, int k) { return guard([&] { mul_int_inplace(get_ct(ct), k); return ct; }); }
+int MulScalarIntNew(int ct, int k) { return guard([&] { auto c = copy_ct(get_ct(ct)); mul_int_inplace(*c, k); return push_ct(std::move(c)); }); }
+int MulScalarFloat(int ct, float v) { return guard([&] { mul_float_inplace(get_ct(ct), (double)v); return ct; }); }
+int MulScalarFloatNew(int ct, float v) {
+  return guard([&] { auto c = copy_ct(get_ct(ct)); mul_float_inplace(*c, (double)v); return push_ct(std::move(c)); });
+}
+int AddScalar(int ct, float v) { return guard([&] { add_const_inplace(get_ct(ct), (double)v, false); return ct; }); }
+int AddScalarNew(int ct, float v) {
+  return guard([&] { auto c = copy_ct(get_ct(ct)); add_const_inplace(*c, (double)v, false); return push_ct(std::move(c)); });
+}
+int SubScalar(int ct, float v) { return guard([&] { add_const_inplace(get_ct(ct), (double)v, true); return ct; }); }
+int SubScalarNew(int ct, float v) {
+  return guard([&] { auto c = copy_ct(get_ct(ct)); add_const_inplace(*c, (double)v, true); return push_ct(std::move(c)); });
+}
+int Negate(int ct) { return guard([&] { auto c = copy_ct(get_ct(ct)); mul_float_inplace(*c, -1.0); return push_ct(std::move(c)); }); }
+int MulRelinCiphertext(int a, int b) {
+  return guard([&] { Cipher& c = get_ct(a); auto r = mul_relin_ct(c, get_ct(b)); c = std::move(*r); return a; });
+}
+int MulRelinCiphertextNew(int a, int b) { return guard([&] { return push_ct(mul_relin_ct(get_ct(a), get_ct(b))); }); }
 int SubPlaintext(int ct, int pt) { return guard([&] { add_plain_inplace(get_ct(ct), get_pt(pt), true); return ct; }); }
 int SubPlaintextNew(int ct, int pt) { return guard([&] { auto c = copy_ct(get_ct(ct)); add_plain_inplace(*c, get_pt(pt), true); return push_ct(std::move(c)); }); }
 

@@ -53,7 +53,7 @@ const char* GetLastError(void);
 int NewKeyGenerator(void);            /* keygenerator.go:12 */
 int GenerateSecretKey(void);          /* keygenerator.go:17 */
 int GeneratePublicKey(void);          /* keygenerator.go:22 */
-int GenerateRelinearizationKey(void); /* keygenerator.go:27 (no relinearization on this path: no-op) */
+int GenerateRelinearizationKey(void); /* keygenerator.go:27-30 (evaluation key s^2 -> s) */
 int GenerateEvaluationKeys(void);     /* keygenerator.go:32 */
 
 /* ---- encoder ------------------------------------------------------------------ */
@@ -86,6 +86,19 @@ int AddCiphertext(int ctID0, int ctID1);                 /* evaluator.go:297-304
 int AddCiphertextNew(int ctID0, int ctID1);              /* evaluator.go:306-318 */
 int SubCiphertext(int ctID0, int ctID1);                 /* evaluator.go:320-327 */
 int SubCiphertextNew(int ctID0, int ctID1);              /* evaluator.go:329-341 */
+int Negate(int ciphertextID);                            /* evaluator.go:68-78 (Mul by -1.0: a new ciphertext) */
+int AddScalar(int ciphertextID, float scalar);           /* evaluator.go:148-154 (round(scalar * scale) into part 0) */
+int AddScalarNew(int ciphertextID, float scalar);        /* evaluator.go:156-166 */
+int SubScalar(int ciphertextID, float scalar);           /* evaluator.go:168-174 */
+int SubScalarNew(int ciphertextID, float scalar);        /* evaluator.go:176-186 */
+int MulScalarInt(int ciphertextID, int scalar);          /* evaluator.go:188-194 (scale unchanged) */
+int MulScalarIntNew(int ciphertextID, int scalar);       /* evaluator.go:196-206 */
+int MulScalarFloat(int ciphertextID, float scalar);      /* evaluator.go:208-214 (non-integer: round(scalar * q_l), scale x q_l) */
+int MulScalarFloatNew(int ciphertextID, float scalar);   /* evaluator.go:216-226 */
+int MulPlaintext(int ciphertextID, int plaintextID);     /* evaluator.go:274-281 (level min, scales multiply, no rescale) */
+int MulPlaintextNew(int ciphertextID, int plaintextID);  /* evaluator.go:283-295 */
+int MulRelinCiphertext(int ctID0, int ctID1);            /* evaluator.go:343-350 (tensor + relinearize, no rescale) */
+int MulRelinCiphertextNew(int ctID0, int ctID1);         /* evaluator.go:352-364 */
 
 /* ---- linear transforms -------------------------------------------------------- */
 int NewLinearTransformEvaluator(void);   /* lineartransform.go:30-34 */

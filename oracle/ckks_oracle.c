@@ -208,6 +208,8 @@ uint64_t orc_rand64(uint64_t seed, uint64_t stream, uint64_t ctr) {
 #define ST_ENC_U(e) ((6ULL << 56) | (u64)(e))
 #define ST_ENC_E0(e) ((7ULL << 56) | (u64)(e))
 #define ST_ENC_E1(e) ((8ULL << 56) | (u64)(e))
+#define ST_RLK_A(d) ((9ULL << 56) | (u64)(d))
+#define ST_RLK_E(d) ((10ULL << 56) | (u64)(d))
 
 static inline u64 uniform_mod(u64 r, u64 q) { return (u64)(((u128)r * q) >> 64); }
 /* centred binomial, eta = 21 per side: sigma = sqrt(21/2) ~ 3.24 */
@@ -244,6 +246,7 @@ struct orc_ctx {
     u64* s_ntt;      /* [L+K][N] */
     u64* pk;         /* [2][L+K][N] */
     struct gk_entry* gk; int ngk, capgk;
+    u64* rlk;        /* relinearization key [dnum][2][L+K][N], or NULL */
     /* encoder */
     double *rre, *rim; /* roots of unity exp(2 pi i k / M), k = 0..M */
     int* rotgroup;   /* 5^j mod M */
@@ -719,33 +722,59 @@ void orc_public_key(const orc_ctx* c, uint64_t* out) { memcpy(out, c->pk, 8 * (s
 /* Galois key for galel: dnum digits of (b_d, a_d) over QP, b_d = -a_d*s' + e_d
  * + [P*s on the limbs of digit d], s' = sigma_{galel^-1}(s)
  * (Lattigo KeyGenerator.GenGaloisKey: encrypts s under pi_{k^-1}(s)). */
-static u64* gen_galois_key(orc_ctx* c, u64 galel) {
+/* Evaluation key from s_in to s_out (both NTT over QP): dnum digits of
+ * (b_d, a_d), b_d = -a_d*s_out + e_d + [P*s_in on the limbs of digit d]
+ * (Lattigo KeyGenerator.GenEvaluationKey). */
+static u64* gen_eval_key(orc_ctx* c, const u64* s_in_ntt, const u64* s_out_ntt, u64 (*st_a)(u64, u64),
+                         u64 (*st_e)(u64, u64), u64 tag) {
     int N = c->N, nm = c->L + c->K, K = c->K; int mi[MAXMOD]; full_qp_list(c, mi);
-    u64 M = 2 * (u64)N; u64 ginv = invmod_generic(galel, M);
-    i64* so = (i64*)xcalloc(sizeof(i64) * N);
-    for (int i = 0; i < N; i++) { u64 t = ((u64)i * ginv) % M; if (t < (u64)N) so[t] += c->s[i]; else so[t - N] -= c->s[i]; }
-    u64* so_ntt = (u64*)xmalloc(8 * (size_t)nm * N);
-    poly_from_signed(c, so, mi, nm, so_ntt); ntt_limbs(c, so_ntt, mi, nm);
     u64* key = (u64*)xmalloc(8 * (size_t)c->dnum * 2 * nm * N);
     i64* e = (i64*)xmalloc(sizeof(i64) * N);
     for (int d = 0; d < c->dnum; d++) {
         u64* b = key + (size_t)d * 2 * nm * N; u64* a = b + (size_t)nm * N;
-        sample_uniform_qp(c, ST_GK_A(galel, d), mi, nm, a); ntt_limbs(c, a, mi, nm);
-        sample_cbd(c->seed, ST_GK_E(galel, d), N, e);
+        sample_uniform_qp(c, st_a(tag, (u64)d), mi, nm, a); ntt_limbs(c, a, mi, nm);
+        sample_cbd(c->seed, st_e(tag, (u64)d), N, e);
         poly_from_signed(c, e, mi, nm, b); ntt_limbs(c, b, mi, nm);
         for (int j = 0; j < nm; j++) {
             u64 q = c->mod[j]; u64 Pq = 0; int own = (j < c->L) && (j >= d * K) && (j < (d + 1) * K);
             if (own) { Pq = 1; for (int k = 0; k < K; k++) Pq = orc_mulmod(Pq, c->mod[c->L + k] % q, q); }
             for (int x = 0; x < N; x++) {
                 size_t o = (size_t)j * N + x;
-                u64 v = submod(b[o], mulmod_b(&c->bar[j], a[o], so_ntt[o]), q);
-                if (own) v = addmod(v, mulmod_b(&c->bar[j], Pq, c->s_ntt[o]), q);
+                u64 v = submod(b[o], mulmod_b(&c->bar[j], a[o], s_out_ntt[o]), q);
+                if (own) v = addmod(v, mulmod_b(&c->bar[j], Pq, s_in_ntt[o]), q);
                 b[o] = v;
             }
         }
     }
-    free(e); free(so); free(so_ntt);
+    free(e);
     return key;
+}
+static u64 st_gk_a(u64 g, u64 d) { return ST_GK_A(g, d); }
+static u64 st_gk_e(u64 g, u64 d) { return ST_GK_E(g, d); }
+static u64 st_rlk_a(u64 g, u64 d) { (void)g; return ST_RLK_A(d); }
+static u64 st_rlk_e(u64 g, u64 d) { (void)g; return ST_RLK_E(d); }
+static u64* gen_galois_key(orc_ctx* c, u64 galel) {
+    int N = c->N, nm = c->L + c->K; int mi[MAXMOD]; full_qp_list(c, mi);
+    u64 M = 2 * (u64)N; u64 ginv = invmod_generic(galel, M);
+    i64* so = (i64*)xcalloc(sizeof(i64) * N);
+    for (int i = 0; i < N; i++) { u64 t = ((u64)i * ginv) % M; if (t < (u64)N) so[t] += c->s[i]; else so[t - N] -= c->s[i]; }
+    u64* so_ntt = (u64*)xmalloc(8 * (size_t)nm * N);
+    poly_from_signed(c, so, mi, nm, so_ntt); ntt_limbs(c, so_ntt, mi, nm);
+    u64* key = gen_eval_key(c, c->s_ntt, so_ntt, st_gk_a, st_gk_e, galel);
+    free(so); free(so_ntt);
+    return key;
+}
+/* Relinearization key: s^2 -> s (Lattigo KeyGenerator.GenRelinearizationKey). */
+const uint64_t* orc_relin_key(orc_ctx* c) {
+    if (c->rlk) return c->rlk;
+    int N = c->N, nm = c->L + c->K;
+    u64* s2 = (u64*)xmalloc(8 * (size_t)nm * N);
+    for (int j = 0; j < nm; j++) for (int x = 0; x < N; x++) {
+        size_t o = (size_t)j * N + x; s2[o] = mulmod_b(&c->bar[j], c->s_ntt[o], c->s_ntt[o]);
+    }
+    c->rlk = gen_eval_key(c, s2, c->s_ntt, st_rlk_a, st_rlk_e, 0);
+    free(s2);
+    return c->rlk;
 }
 const uint64_t* orc_galois_key(orc_ctx* c, uint64_t galel) {
     for (int i = 0; i < c->ngk; i++) if (c->gk[i].galel == galel) return c->gk[i].key;
@@ -770,7 +799,7 @@ void orc_free(orc_ctx* c) {
     if (!c) return;
     free(c->psi); free(c->psip); free(c->ipsi); free(c->ipsip); free(c->s); free(c->s_ntt); free(c->pk);
     for (int i = 0; i < c->ngk; i++) free(c->gk[i].key);
-    free(c->gk); free(c->rre); free(c->rim); free(c->rotgroup); free(c);
+    free(c->gk); free(c->rlk); free(c->rre); free(c->rim); free(c->rotgroup); free(c);
 }
 
 /* =====================================================================
@@ -871,6 +900,98 @@ void orc_automorphism_ct(orc_ctx* c, const uint64_t* ct, int l, uint64_t galel, 
     free(idx); free(t); free(d0); free(d1); free(digits);
 }
 void orc_rotate(orc_ctx* c, const uint64_t* ct, int l, int k, uint64_t* out) { orc_automorphism_ct(c, ct, l, orc_galois_element(c, k), out); }
+
+/* Lattigo ckks Evaluator.Mul(ct, pt) (MulPlaintext, evaluator.go:274-295):
+ * per-limb product of both parts with the plaintext at level min(lc, lp);
+ * the output scale is the product of the scales (not rescaled). */
+void orc_mul_plain(const orc_ctx* c, const uint64_t* ct, int lc, const uint64_t* pt, int lp, uint64_t* out) {
+    int N = c->N, l = lc < lp ? lc : lp;
+    for (int p = 0; p < 2; p++) for (int i = 0; i <= l; i++) for (int x = 0; x < N; x++) {
+        size_t oc = ((size_t)p * (lc + 1) + i) * N + x, oo = ((size_t)p * (l + 1) + i) * N + x;
+        out[oo] = mulmod_b(&c->bar[i], ct[oc], pt[(size_t)i * N + x]);
+    }
+}
+/* Residues of an integer constant k (two's complement int64) mod each q_i. */
+static u64 residue_i64(int64_t k, u64 q) {
+    if (k >= 0) return (u64)k % q;
+    u64 m = (u64)(-(k + 1)) % q;  /* |k| - 1 without overflow */
+    return negmod((m + 1) % q, q);
+}
+/* Lattigo's scaled real constant (bigComplexToRNSScalar at float64 encoding
+ * precision): t = v * scale rounded to double, then +-0.5 (in double) and
+ * truncated toward zero.  Returns 0 and sets *out when |t| < 2^62. */
+int orc_scaled_constant(double v, double scale, int64_t* out) {
+    double t = v * scale;
+    if (!(t < 4611686018427387904.0 && t > -4611686018427387904.0)) return -1;
+    if (t > 0) t = t + 0.5; else if (t < 0) t = t - 0.5;
+    *out = (int64_t)t;
+    return 0;
+}
+/* Evaluator.Mul(ct, int) (MulScalarInt, evaluator.go:188-205): every limb of
+ * both parts times k mod q_i; the scale is unchanged. */
+void orc_mul_int(const orc_ctx* c, const uint64_t* ct, int l, int64_t k, uint64_t* out) {
+    int N = c->N;
+    for (int i = 0; i <= l; i++) {
+        u64 kq = residue_i64(k, c->mod[i]);
+        for (int p = 0; p < 2; p++) for (int x = 0; x < N; x++) {
+            size_t o = ((size_t)p * (l + 1) + i) * N + x; out[o] = mulmod_b(&c->bar[i], ct[o], kq);
+        }
+    }
+}
+/* Evaluator.Mul(ct, float64) (MulScalarFloat, evaluator.go:208-225): an
+ * integer-valued constant multiplies as an integer (scale unchanged);
+ * otherwise the constant is scaled by q_l, rounded as above, and the output
+ * scale is multiplied by q_l (the caller rescales).  Returns 1 when the
+ * scale was multiplied by q_l, 0 when not, -1 when the constant is too large. */
+int orc_mul_float(const orc_ctx* c, const uint64_t* ct, int l, double v, uint64_t* out) {
+    int64_t k;
+    if (v < 4611686018427387904.0 && v > -4611686018427387904.0 && v == (double)(int64_t)v) {
+        orc_mul_int(c, ct, l, (int64_t)v, out);
+        return 0;
+    }
+    if (orc_scaled_constant(v, (double)c->mod[l], &k) != 0) return -1;
+    orc_mul_int(c, ct, l, k, out);
+    return 1;
+}
+/* Evaluator.Add(ct, float64) (AddScalar / SubScalar, evaluator.go:148-185):
+ * the constant scaled by the ciphertext scale and rounded is added to (or
+ * subtracted from) every NTT slot of part 0 in every limb. */
+int orc_add_const(const orc_ctx* c, const uint64_t* ct, int l, double v, double scale, int sub, uint64_t* out) {
+    int N = c->N; int64_t k;
+    if (orc_scaled_constant(v, scale, &k) != 0) return -1;
+    memcpy(out, ct, 8 * (size_t)2 * (l + 1) * N);
+    for (int i = 0; i <= l; i++) {
+        u64 q = c->mod[i], kq = residue_i64(k, q);
+        for (int x = 0; x < N; x++) {
+            size_t o = (size_t)i * N + x; out[o] = sub ? submod(ct[o], kq, q) : addmod(ct[o], kq, q);
+        }
+    }
+    return 0;
+}
+/* Evaluator.MulRelin (MulRelinCiphertext, evaluator.go:343-362): tensor
+ * (d0, d1, d2) = (a0 b0, a0 b1 + a1 b0, a1 b1) at level l, then d2 is key
+ * switched with the relinearization key (decompose, key product, ModDown of
+ * both parts) and added to (d0, d1).  The output scale is the product. */
+void orc_mul_relin(orc_ctx* c, const uint64_t* a, const uint64_t* b, int l, uint64_t* out) {
+    int N = c->N, K = c->K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
+    size_t ps = (size_t)(l + 1) * N;
+    u64* d2 = (u64*)xmalloc(8 * ps);
+    for (int i = 0; i <= l; i++) for (int x = 0; x < N; x++) {
+        size_t o = (size_t)i * N + x; const barrett_t* B = &c->bar[i]; u64 q = c->mod[i];
+        out[o] = mulmod_b(B, a[o], b[o]);
+        out[ps + o] = addmod(mulmod_b(B, a[o], b[ps + o]), mulmod_b(B, a[ps + o], b[o]), q);
+        d2[o] = mulmod_b(B, a[ps + o], b[ps + o]);
+    }
+    const u64* rlk = orc_relin_key(c);
+    u64* digits = (u64*)xmalloc(8 * (size_t)dn * nqp * N);
+    orc_decompose_modup(c, l, d2, digits);
+    u64* e0 = (u64*)xmalloc(8 * (size_t)nqp * N); u64* e1 = (u64*)xmalloc(8 * (size_t)nqp * N);
+    gadget_mac(c, l, digits, rlk, e0, e1);
+    u64* t = (u64*)xmalloc(8 * 2 * ps);
+    orc_mod_down(c, l, e0, t); orc_mod_down(c, l, e1, t + ps);
+    orc_add(c, out, t, l, 2, out);
+    free(d2); free(digits); free(e0); free(e1); free(t);
+}
 
 /* Lattigo ring.DivRoundByLastModulusNTT (ckks Rescale, evaluator.go:131-146):
  * u = (iNTT(x_l) + q_l>>1) mod q_l; out_i = (x_i - NTT_i(u - q_l>>1)) * q_l^-1. */

@@ -63,6 +63,8 @@ void orc_secret_key(const orc_ctx* c, int64_t* s_coeffs);
 /* Galois key [dnum][2][L+K][N] in the NTT domain (cached in the context). */
 const uint64_t* orc_galois_key(orc_ctx* c, uint64_t galel);
 void orc_public_key(const orc_ctx* c, uint64_t* out); /* [2][L+K][N] */
+/* Relinearization key (s^2 -> s) [dnum][2][L+K][N], NTT (cached). */
+const uint64_t* orc_relin_key(orc_ctx* c);
 
 /* ---- encoder ----------------------------------------------------------- */
 void orc_encode(const orc_ctx* c, const float* v, int n, int level,
@@ -78,6 +80,14 @@ void orc_decode_f64(const orc_ctx* c, const uint64_t* pt, int level,
 void orc_encrypt(const orc_ctx* c, const uint64_t* pt, int level,
                  uint64_t enc_index, uint64_t* ct);
 void orc_decrypt(const orc_ctx* c, const uint64_t* ct, int level, uint64_t* pt);
+
+/* ---- plaintext / scalar / ciphertext products ----------------------------- */
+void orc_mul_plain(const orc_ctx* c, const uint64_t* ct, int lc, const uint64_t* pt, int lp, uint64_t* out);
+int  orc_scaled_constant(double v, double scale, int64_t* out);
+void orc_mul_int(const orc_ctx* c, const uint64_t* ct, int l, int64_t k, uint64_t* out);
+int  orc_mul_float(const orc_ctx* c, const uint64_t* ct, int l, double v, uint64_t* out);
+int  orc_add_const(const orc_ctx* c, const uint64_t* ct, int l, double v, double scale, int sub, uint64_t* out);
+void orc_mul_relin(orc_ctx* c, const uint64_t* a, const uint64_t* b, int l, uint64_t* out);
 
 /* ---- evaluator --------------------------------------------------------- */
 void orc_add(const orc_ctx* c, const uint64_t* a, const uint64_t* b, int level,

@@ -81,6 +81,13 @@ def lib():
             "orc_lt_eval_partial": ([vp, vp, u64p, ctypes.c_int, ctypes.c_int, ctypes.c_int, u64p], None),
             "orc_lt_num_giant": ([vp], ctypes.c_int),
             "orc_set_threads": ([ctypes.c_int], None),
+            "orc_relin_key": ([vp], u64p),
+            "orc_mul_plain": ([vp, u64p, ctypes.c_int, u64p, ctypes.c_int, u64p], None),
+            "orc_scaled_constant": ([ctypes.c_double, ctypes.c_double, i64p], ctypes.c_int),
+            "orc_mul_int": ([vp, u64p, ctypes.c_int, ctypes.c_int64, u64p], None),
+            "orc_mul_float": ([vp, u64p, ctypes.c_int, ctypes.c_double, u64p], ctypes.c_int),
+            "orc_add_const": ([vp, u64p, ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_int, u64p], ctypes.c_int),
+            "orc_mul_relin": ([vp, u64p, u64p, ctypes.c_int, u64p], None),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -246,6 +253,56 @@ class Oracle:
         npoly = a.size // ((level + 1) * self.N)
         out = np.zeros_like(a)
         lib().orc_add(self.ctx, _p(a), _p(b), level, npoly, _p(out))
+        return out
+
+    def relin_key(self):
+        ptr = lib().orc_relin_key(self.ctx)
+        n = self.dnum * 2 * (self.L + self.K) * self.N
+        return np.ctypeslib.as_array(ptr, shape=(n,)).reshape(self.dnum, 2, self.L + self.K, self.N).copy()
+
+    def mul_plain(self, ct, lc, pt, lp):
+        """MulPlaintext: (ciphertext at level lc) x (plaintext at level lp), level min(lc, lp)."""
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        pt = np.ascontiguousarray(pt, dtype=np.uint64)
+        l = min(lc, lp)
+        out = np.zeros((2, l + 1, self.N), dtype=np.uint64)
+        lib().orc_mul_plain(self.ctx, _p(ct), lc, _p(pt), lp, _p(out))
+        return out
+
+    @staticmethod
+    def scaled_constant(v, scale):
+        k = ctypes.c_int64(0)
+        if lib().orc_scaled_constant(float(v), float(scale), ctypes.byref(k)) != 0:
+            raise ValueError("scaled constant out of range")
+        return k.value
+
+    def mul_int(self, ct, level, k):
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        out = np.zeros_like(ct)
+        lib().orc_mul_int(self.ctx, _p(ct), level, int(k), _p(out))
+        return out
+
+    def mul_float(self, ct, level, v):
+        """MulScalarFloat; returns (out, scale_multiplied_by_q_level)."""
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        out = np.zeros_like(ct)
+        r = lib().orc_mul_float(self.ctx, _p(ct), level, float(v), _p(out))
+        if r < 0:
+            raise ValueError("scaled constant out of range")
+        return out, bool(r)
+
+    def add_const(self, ct, level, v, scale, sub=False):
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        out = np.zeros_like(ct)
+        if lib().orc_add_const(self.ctx, _p(ct), level, float(v), float(scale), int(sub), _p(out)) != 0:
+            raise ValueError("scaled constant out of range")
+        return out
+
+    def mul_relin(self, a, b, level):
+        a = np.ascontiguousarray(a, dtype=np.uint64)
+        b = np.ascontiguousarray(b, dtype=np.uint64)
+        out = np.zeros((2, level + 1, self.N), dtype=np.uint64)
+        lib().orc_mul_relin(self.ctx, _p(a), _p(b), level, _p(out))
         return out
 
     def rescale(self, ct, level):

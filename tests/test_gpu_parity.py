@@ -179,3 +179,103 @@ def test_linear_transform(ctx, case):
     if case in ("identity", "shift", "wrap"):
         np.testing.assert_allclose(dec, np.roll(vals.astype(np.float64), -idx[0]), atol=1e-3)
     ctx.lib.DeleteLinearTransform(tid)
+
+
+# ---------------------------------------------------------------- products and constants
+# (evaluator.go:68-78, 148-226, 274-295, 343-364; orion/backend/python/evaluator.py:12-94)
+
+
+def _ct_scale(ctx, ct_id):
+    return ctx.lib.GetCiphertextScaleDouble(ct_id)
+
+
+def test_mul_plaintext(ctx):
+    top = ctx.L - 1
+    ct, ref, a = ctx.fresh_ct(top, 50)
+    b = ctx.rng.uniform(-1, 1, ctx.slots).astype(np.float32)
+    scale = 1 << ctx.logscale
+    pt = ctx.lib.Encode(b.tolist(), top - 1, scale)
+    pt_ref = ctx.orc.encode(b, top - 1, float(scale))
+    out = ctx.lib.MulPlaintextNew(ct, pt)
+    assert ctx.lib.GetCiphertextLevel(out) == top - 1
+    assert _ct_scale(ctx, out) == float(scale) * float(scale)
+    want = ctx.orc.mul_plain(ref, top, pt_ref, top - 1)
+    assert_equal_u64(ctx.lib.export_ciphertext(out), want, "MulPlaintextNew")
+    # in place, then Orion's rescale (evaluator.py:59-65)
+    assert ctx.lib.MulPlaintext(ct, pt) == ct
+    assert_equal_u64(ctx.lib.export_ciphertext(ct), want, "MulPlaintext")
+    r = ctx.lib.RescaleNew(ct)
+    dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(r)))
+    np.testing.assert_allclose(dec, a.astype(np.float64) * b, atol=1e-3)
+
+
+@pytest.mark.parametrize("k", [3, -5, 1, 0])
+def test_mul_scalar_int(ctx, k):
+    top = ctx.L - 1
+    ct, ref, _ = ctx.fresh_ct(top, 51)
+    out = ctx.lib.MulScalarIntNew(ct, k)
+    assert _ct_scale(ctx, out) == float(1 << ctx.logscale)
+    assert_equal_u64(ctx.lib.export_ciphertext(out), ctx.orc.mul_int(ref, top, k), f"MulScalarIntNew {k}")
+    assert ctx.lib.MulScalarInt(ct, k) == ct
+    assert_equal_u64(ctx.lib.export_ciphertext(ct), ctx.orc.mul_int(ref, top, k), f"MulScalarInt {k}")
+
+
+@pytest.mark.parametrize("v", [0.75, -1.3, -2.0])
+def test_mul_scalar_float(ctx, v):
+    top = ctx.L - 1
+    ct, ref, vals = ctx.fresh_ct(top, 52)
+    v32 = float(np.float32(v))
+    want, scaled = ctx.orc.mul_float(ref, top, v32)
+    out = ctx.lib.MulScalarFloatNew(ct, v32)
+    sc = float(1 << ctx.logscale) * (float(ctx.q[top]) if scaled else 1.0)
+    assert _ct_scale(ctx, out) == sc
+    assert_equal_u64(ctx.lib.export_ciphertext(out), want, f"MulScalarFloatNew {v}")
+    assert ctx.lib.MulScalarFloat(ct, v32) == ct
+    assert_equal_u64(ctx.lib.export_ciphertext(ct), want, f"MulScalarFloat {v}")
+    if scaled:  # Orion rescales after a non-integer constant (evaluator.py:35-48)
+        out = ctx.lib.RescaleNew(out)
+    dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(out)))
+    np.testing.assert_allclose(dec, v32 * vals.astype(np.float64), atol=1e-3)
+
+
+def test_negate_and_scalar_add(ctx):
+    top = ctx.L - 1
+    ct, ref, vals = ctx.fresh_ct(top, 53)
+    neg = ctx.lib.Negate(ct)
+    assert neg != ct
+    assert_equal_u64(ctx.lib.export_ciphertext(neg), ctx.orc.mul_int(ref, top, -1), "Negate")
+    scale = float(1 << ctx.logscale)
+    c = float(np.float32(0.375))
+    for sub in (False, True):
+        want = ctx.orc.add_const(ref, top, c, scale, sub)
+        f_new = ctx.lib.SubScalarNew if sub else ctx.lib.AddScalarNew
+        out = f_new(ct, c)
+        assert_equal_u64(ctx.lib.export_ciphertext(out), want, f"{'Sub' if sub else 'Add'}ScalarNew")
+        dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(out)))
+        np.testing.assert_allclose(dec, vals + (-c if sub else c), atol=1e-4)
+    ct2, ref2, _ = ctx.fresh_ct(top, 54)
+    assert ctx.lib.AddScalar(ct2, c) == ct2
+    assert ctx.lib.SubScalar(ct2, c) == ct2
+    assert_equal_u64(ctx.lib.export_ciphertext(ct2), ctx.orc.add_const(ctx.orc.add_const(ref2, top, c, scale), top, c, scale, True),
+                     "AddScalar then SubScalar")
+
+
+def test_mul_relin(ctx):
+    ctx.lib.GenerateRelinearizationKey()
+    top = ctx.L - 1
+    a, ra, va = ctx.fresh_ct(top, 55)
+    b, rb, vb = ctx.fresh_ct(top - 1, 56)
+    out = ctx.lib.MulRelinCiphertextNew(a, b)
+    l = top - 1
+    assert ctx.lib.GetCiphertextLevel(out) == l
+    assert _ct_scale(ctx, out) == float(1 << ctx.logscale) ** 2
+    ra_l = ra[:, : l + 1]
+    want = ctx.orc.mul_relin(ra_l, rb, l)
+    assert_equal_u64(ctx.lib.export_ciphertext(out), want, "MulRelinCiphertextNew")
+    # squaring in place (the tensor of a ciphertext with itself)
+    sq_want = ctx.orc.mul_relin(ra, ra, top)
+    assert ctx.lib.MulRelinCiphertext(a, a) == a
+    assert_equal_u64(ctx.lib.export_ciphertext(a), sq_want, "MulRelinCiphertext (square)")
+    r = ctx.lib.RescaleNew(out)
+    dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(r)))
+    np.testing.assert_allclose(dec, va.astype(np.float64) * vb, atol=1e-3)

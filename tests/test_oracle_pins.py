@@ -390,3 +390,133 @@ def test_bsgs_split(mid, diags, slots, ratio, n1):
         assert o.lt_n1(t) == n1
     finally:
         o.close()
+
+
+# ---------------------------------------------------------------- products and constants
+
+
+def _negacyclic(a, b, N):
+    prod = [0] * N
+    for x in range(N):
+        if a[x] == 0:
+            continue
+        for y in range(N):
+            if b[y] == 0:
+                continue
+            k = x + y
+            if k < N:
+                prod[k] += a[x] * b[y]
+            else:
+                prod[k - N] -= a[x] * b[y]
+    return prod
+
+
+def test_relin_key_relation(small):
+    """b_d + a_d * s = e_d + P * s^2 on the digit's limbs (key from s^2 to s)."""
+    key = small.relin_key()
+    s = [int(v) for v in small.secret_key()]
+    N, mods = small.N, small.q + small.p
+    s2 = _negacyclic(s, s, N)
+    P = math.prod(small.p)
+    for d in range(small.dnum):
+        for i, m in enumerate(mods):
+            b = small.intt(key[d][0][i], i)
+            a = small.intt(key[d][1][i], i)
+            prod = _negacyclic([int(v) for v in a], s, N)
+            own = i < small.L and d * small.K <= i < (d + 1) * small.K
+            e = [(int(b[x]) + prod[x] - (P * s2[x] if own else 0)) % m for x in range(N)]
+            e = [v - m if v > m // 2 else v for v in e]
+            assert max(abs(v) for v in e) <= 21
+
+
+def test_mul_plain_is_decrypt_times_plaintext(mid):
+    """Dec(ct x pt) == Dec(ct) * pt slot-wise (exact), and it decodes to the product."""
+    level = mid.L - 1
+    rng = np.random.default_rng(31)
+    a = rng.uniform(-1, 1, mid.slots).astype(np.float32)
+    b = rng.uniform(-1, 1, mid.slots).astype(np.float32)
+    ct = _enc(mid, a, level, 35, 2)
+    pt = mid.encode(b, level - 1, 2.0 ** 35)
+    out = mid.mul_plain(ct, level, pt, level - 1)
+    assert out.shape == (2, level, mid.N)
+    dec = mid.decrypt(out, level - 1)
+    base = mid.decrypt(ct, level)[:level]
+    for i in range(level):
+        q = mid.q[i]
+        np.testing.assert_array_equal(dec[i], (base[i].astype(object) * pt[i].astype(object)) % q)
+    got = mid.decode_f64(dec, level - 1, 2.0 ** 70)
+    np.testing.assert_allclose(got, a.astype(np.float64) * b, atol=1e-4)
+
+
+@pytest.mark.parametrize("k", [3, -5, 0, 1, -1])
+def test_mul_int_scales_the_plaintext(mid, k):
+    level = mid.L - 1
+    vals = np.linspace(-1, 1, mid.slots).astype(np.float32)
+    ct = _enc(mid, vals, level, 35, 3)
+    out = mid.mul_int(ct, level, k)
+    dec, base = mid.decrypt(out, level), mid.decrypt(ct, level)
+    for i in range(level + 1):
+        q = mid.q[i]
+        np.testing.assert_array_equal(dec[i], (base[i].astype(object) * (k % q)) % q)
+
+
+def test_scaled_constant_rounds_half_away_from_zero():
+    from fractions import Fraction
+    rng = np.random.default_rng(5)
+    for v in list(rng.uniform(-3, 3, 200).astype(np.float32)) + [0.5, -0.5, 2.5, -2.5, 0.0]:
+        for scale in (2.0 ** 35, 2.0 ** 40 + 12345, 1073741827.0):
+            exact = Fraction(float(v)) * Fraction(scale)
+            if abs(exact) >= 2 ** 52:
+                continue
+            want = int(exact + Fraction(1, 2)) if exact > 0 else -int(-exact + Fraction(1, 2))
+            assert O.Oracle.scaled_constant(float(v), scale) == want
+
+
+def test_mul_float_and_add_const(mid):
+    level = mid.L - 1
+    vals = np.linspace(-1, 1, mid.slots).astype(np.float32)
+    ct = _enc(mid, vals, level, 35, 4)
+    base = mid.decrypt(ct, level)
+    # non-integer constant: times round(v * q_level), scale grows by q_level
+    out, scaled = mid.mul_float(ct, level, 0.75)
+    assert scaled
+    k = O.Oracle.scaled_constant(0.75, float(mid.q[level]))
+    dec = mid.decrypt(out, level)
+    for i in range(level + 1):
+        np.testing.assert_array_equal(dec[i], (base[i].astype(object) * (k % mid.q[i])) % mid.q[i])
+    got = mid.decode_f64(dec, level, 2.0 ** 35 * mid.q[level])
+    np.testing.assert_allclose(got, 0.75 * vals.astype(np.float64), atol=1e-5)
+    # integer-valued constant: plain integer product, scale unchanged
+    out2, scaled2 = mid.mul_float(ct, level, -2.0)
+    assert not scaled2
+    np.testing.assert_array_equal(out2, mid.mul_int(ct, level, -2))
+    # constants: every NTT slot of part 0 moves by round(v * scale), part 1 untouched
+    for sub in (False, True):
+        out3 = mid.add_const(ct, level, 0.375, 2.0 ** 35, sub)
+        np.testing.assert_array_equal(out3[1], ct[1])
+        kk = O.Oracle.scaled_constant(0.375, 2.0 ** 35)
+        for i in range(level + 1):
+            q = mid.q[i]
+            delta = (out3[0][i].astype(object) - ct[0][i].astype(object)) % q
+            assert set(delta.tolist()) == {(-kk if sub else kk) % q}
+        got = mid.decode_f64(mid.decrypt(out3, level), level, 2.0 ** 35)
+        np.testing.assert_allclose(got, vals + (-0.375 if sub else 0.375), atol=1e-6)
+
+
+def test_mul_relin_decrypts_to_product(mid):
+    level = mid.L - 1
+    rng = np.random.default_rng(41)
+    a = rng.uniform(-1, 1, mid.slots).astype(np.float32)
+    b = rng.uniform(-1, 1, mid.slots).astype(np.float32)
+    ca, cb = _enc(mid, a, level, 35, 5), _enc(mid, b, level, 35, 6)
+    out = mid.mul_relin(ca, cb, level)
+    got = mid.decode_f64(mid.decrypt(out, level), level, 2.0 ** 70)
+    np.testing.assert_allclose(got, a.astype(np.float64) * b, atol=1e-6)
+    # squaring: the same ciphertext twice
+    sq = mid.mul_relin(ca, ca, level)
+    got = mid.decode_f64(mid.decrypt(sq, level), level, 2.0 ** 70)
+    np.testing.assert_allclose(got, a.astype(np.float64) ** 2, atol=1e-6)
+    # rescaled once: back to scale 2^70 / q_level
+    r = mid.rescale(out, level)
+    got = mid.decode_f64(mid.decrypt(r, level - 1), level - 1, 2.0 ** 70 / mid.q[level])
+    np.testing.assert_allclose(got, a.astype(np.float64) * b, atol=1e-6)
