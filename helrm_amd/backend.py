@@ -168,6 +168,11 @@ _SIGNATURES = {
     "MulPlaintextNew": ([_I, _I], _I),
     "MulRelinCiphertext": ([_I, _I], _I),
     "MulRelinCiphertextNew": ([_I, _I], _I),
+    # polynomial evaluator
+    "NewPolynomialEvaluator": ([], _I),
+    "GenerateMonomial": ([_PF, _I], _I),
+    "GenerateChebyshev": ([_PF, _I], _I),
+    "EvaluatePolynomial": ([_I, _I, _c.c_ulong], _I),
     # linear transforms
     "NewLinearTransformEvaluator": ([], _I),
     "GenerateLinearTransform": ([_PI, _I, _PF, _I, _I, _c.c_float, _c.c_char_p], _I),

@@ -269,7 +269,8 @@ struct Scheme {
   std::set<u64> rot_keys, lt_keys;
   u64 enc_counter = 0;
   // registries
-  IdHeap pt_ids, ct_ids, lt_ids;
+  IdHeap pt_ids, ct_ids, lt_ids, poly_ids;
+  std::map<int, std::vector<double>> polys;  // monomial coefficients, lowest degree first
   std::map<int, std::unique_ptr<Plain>> pts;
   std::map<int, std::unique_ptr<Cipher>> cts;
   std::map<int, std::unique_ptr<LinTrans>> lts;
@@ -898,20 +899,22 @@ std::unique_ptr<Cipher> automorphism(const Cipher& ct, u64 galel, bool lt_keyset
 
 // Lattigo's scaled real constant (float64 encoding precision): v * scale
 // rounded to double, then +-0.5 in double, truncated toward zero.
-int64_t scaled_constant(double v, double scale) {
+typedef __int128 i128;
+i128 scaled_constant(double v, double scale) {
   double t = v * scale;
-  REQUIRE(t < 4611686018427387904.0 && t > -4611686018427387904.0, "scaled constant exceeds 2^62");
+  REQUIRE(t < 42535295865117307932921825928971026432.0 && t > -42535295865117307932921825928971026432.0,
+          "scaled constant exceeds 2^125");
   if (t > 0) t = t + 0.5; else if (t < 0) t = t - 0.5;
-  return (int64_t)t;
+  return (i128)t;
 }
-u64 residue_i64(int64_t k, u64 q) {
-  if (k >= 0) return (u64)k % q;
-  u64 m = (u64)(-(k + 1)) % q;
+u64 residue_i64(i128 k, u64 q) {
+  if (k >= 0) return (u64)((u128)k % q);
+  u64 m = (u64)((u128)(-(k + 1)) % q);
   m = (m + 1) % q;
   return m ? q - m : 0;
 }
 // both parts of c (level l) times the integer k, in place
-void mul_int_inplace(Cipher& c, int64_t k) {
+void mul_int_inplace(Cipher& c, i128 k) {
   Scheme& s = sch();
   const int l = c.level, nm = s.L + s.K;
   std::vector<u64> w(nm, 0), wp(nm, 0);
@@ -926,10 +929,10 @@ void mul_int_inplace(Cipher& c, int64_t k) {
 void mul_float_inplace(Cipher& c, double v) {
   Scheme& s = sch();
   if (v < 4611686018427387904.0 && v > -4611686018427387904.0 && v == (double)(int64_t)v) {
-    mul_int_inplace(c, (int64_t)v);
+    mul_int_inplace(c, (i128)(int64_t)v);
     return;
   }
-  const int64_t k = scaled_constant(v, (double)s.mod[c.level]);
+  const i128 k = scaled_constant(v, (double)s.mod[c.level]);
   mul_int_inplace(c, k);
   c.scale *= (double)s.mod[c.level];
 }
@@ -937,7 +940,7 @@ void mul_float_inplace(Cipher& c, double v) {
 void add_const_inplace(Cipher& c, double v, bool sub) {
   Scheme& s = sch();
   const int l = c.level, nm = s.L + s.K;
-  const int64_t k = scaled_constant(v, c.scale);
+  const i128 k = scaled_constant(v, c.scale);
   std::vector<u64> kq(nm, 0);
   for (int i = 0; i <= l; i++) kq[i] = residue_i64(k, s.mod[i]);
   DU64 dk(nm);
@@ -987,6 +990,62 @@ std::unique_ptr<Cipher> mul_relin_ct(const Cipher& a, const Cipher& b) {
   launch_keymac(k, 1, s.st);
   // out = ModDown(dd) + (d0, d1): the epilogue reads and writes each word in one thread
   mod_down(l, dd.p, (size_t)nqp * N, 2, out->d.p, ps, out->d.p, ps, 2, nullptr);
+  return out;
+}
+std::unique_ptr<Cipher> rescale_ct(const Cipher& ct);
+void add_inplace(Cipher& a, const Cipher& b, bool sub);
+// keep rows 0..nl of both parts (Lattigo DropLevel: the scale is unchanged)
+std::unique_ptr<Cipher> dropped_copy(const Cipher& c, int nl) {
+  Scheme& s = sch();
+  auto out = new_ct(nl, c.scale); out->logslots = c.logslots;
+  copy_rows(out->d.p, (size_t)(nl + 1) * s.N, c.d.p, (size_t)(c.level + 1) * s.N, (size_t)(nl + 1) * s.N, 2);
+  return out;
+}
+// Monomial polynomial of degree <= 3 at depth ceil(log2(d + 1)), output scale
+// `so` (the same composition as the restatement's orc_eval_poly):
+//   d = 1: Rescale(X * K1) + c0, K1 = round(c1 * so * q_l / s)
+//   d = 2, 3: X2 = Rescale(MulRelin(X, X)); B = Rescale(X * K3) + c2 at
+//     scale sB = so * q_{l-1} / scale(X2), K3 = round(c3 * sB * q_l / s);
+//     out = Rescale(MulRelin(X2, B)) + (Rescale(X * K1) dropped one level + c0)
+std::unique_ptr<Cipher> eval_poly_ct(const Cipher& x, std::vector<double> coef, double so) {
+  Scheme& s = sch();
+  int d = (int)coef.size() - 1;
+  while (d > 0 && coef[d] == 0.0) d--;
+  REQUIRE(d >= 0 && d <= 3, "the hip backend evaluates polynomials of degree <= 3");
+  const int l = x.level;
+  if (d == 0) {
+    auto out = copy_ct(x);
+    mul_int_inplace(*out, 0);
+    out->scale = so;
+    add_const_inplace(*out, coef[0], false);
+    return out;
+  }
+  REQUIRE(l >= (d == 1 ? 1 : 2), "not enough levels left for the polynomial");
+  const double ql = (double)s.mod[l];
+  auto t = copy_ct(x);
+  mul_int_inplace(*t, scaled_constant(coef[1], so * ql / x.scale));
+  auto A = rescale_ct(*t);
+  A->scale = so;
+  if (d == 1) {
+    add_const_inplace(*A, coef[0], false);
+    return A;
+  }
+  const double s2 = x.scale * x.scale / ql;
+  const double sB = so * (double)s.mod[l - 1] / s2;
+  auto sq = mul_relin_ct(x, x);
+  auto X2 = rescale_ct(*sq);
+  X2->scale = s2;
+  auto tb = copy_ct(x);
+  mul_int_inplace(*tb, scaled_constant(d == 3 ? coef[3] : 0.0, sB * ql / x.scale));
+  auto B = rescale_ct(*tb);
+  B->scale = sB;
+  add_const_inplace(*B, coef[2], false);
+  auto PB = mul_relin_ct(*X2, *B);
+  auto out = rescale_ct(*PB);
+  out->scale = so;
+  auto A2 = dropped_copy(*A, l - 2);
+  add_const_inplace(*A2, coef[0], false);
+  add_inplace(*out, *A2, false);
   return out;
 }
 std::unique_ptr<Cipher> rescale_ct(const Cipher& ct) {
@@ -1517,6 +1576,42 @@ int MulRelinCiphertext(int a, int b) {
   return guard([&] { Cipher& c = get_ct(a); auto r = mul_relin_ct(c, get_ct(b)); c = std::move(*r); return a; });
 }
 int MulRelinCiphertextNew(int a, int b) { return guard([&] { return push_ct(mul_relin_ct(get_ct(a), get_ct(b))); }); }
+
+// ---- polynomial evaluator ----
+int NewPolynomialEvaluator(void) { return guard([&] { sch(); return 0; }); }
+int GenerateMonomial(const float* coeffs, int lenCoeffs) {
+  return guard([&] {
+    REQUIRE(coeffs && lenCoeffs >= 1, "empty polynomial");
+    Scheme& s = sch();
+    int id = s.poly_ids.take();
+    s.polys[id] = std::vector<double>(coeffs, coeffs + lenCoeffs);
+    return id;
+  });
+}
+// Chebyshev basis on [-1, 1] (T0 = 1, T1 = x, T2 = 2x^2 - 1, T3 = 4x^3 - 3x),
+// kept as its monomial form (degree <= 3)
+int GenerateChebyshev(const float* coeffs, int lenCoeffs) {
+  return guard([&] {
+    REQUIRE(coeffs && lenCoeffs >= 1, "empty polynomial");
+    REQUIRE(lenCoeffs <= 4, "the hip backend evaluates polynomials of degree <= 3");
+    double c[4] = {0, 0, 0, 0};
+    for (int i = 0; i < lenCoeffs; i++) c[i] = coeffs[i];
+    std::vector<double> m = {c[0] - c[2], c[1] - 3.0 * c[3], 2.0 * c[2], 4.0 * c[3]};
+    m.resize(lenCoeffs);
+    Scheme& s = sch();
+    int id = s.poly_ids.take();
+    s.polys[id] = m;
+    return id;
+  });
+}
+int EvaluatePolynomial(int ctInID, int polyID, unsigned long outScale) {
+  return guard([&] {
+    Scheme& s = sch();
+    auto it = s.polys.find(polyID);
+    REQUIRE(it != s.polys.end(), "polynomial not found: " + std::to_string(polyID));
+    return push_ct(eval_poly_ct(get_ct(ctInID), it->second, (double)outScale));
+  });
+}
 int SubPlaintext(int ct, int pt) { return guard([&] { add_plain_inplace(get_ct(ct), get_pt(pt), true); return ct; }); }
 int SubPlaintextNew(int ct, int pt) { return guard([&] { auto c = copy_ct(get_ct(ct)); add_plain_inplace(*c, get_pt(pt), true); return push_ct(std::move(c)); }); }
 

@@ -100,6 +100,14 @@ int MulPlaintextNew(int ciphertextID, int plaintextID);  /* evaluator.go:283-295
 int MulRelinCiphertext(int ctID0, int ctID1);            /* evaluator.go:343-350 (tensor + relinearize, no rescale) */
 int MulRelinCiphertextNew(int ctID0, int ctID1);         /* evaluator.go:352-364 */
 
+/* ---- polynomial evaluator (polyeval.go) ------------------------------------------ */
+int NewPolynomialEvaluator(void);                                   /* polyeval.go:32-35 */
+int GenerateMonomial(const float* coeffs, int lenCoeffs);           /* polyeval.go:37-47 (lowest degree first) */
+int GenerateChebyshev(const float* coeffs, int lenCoeffs);          /* polyeval.go:49-60 (degree <= 3, on [-1, 1]) */
+/* polyeval.go:62-84: a new ciphertext at scale outScale; degree <= 3 at depth
+ * ceil(log2(degree + 1)) (orion/nn/activation.py:22-28). */
+int EvaluatePolynomial(int ctInID, int polyID, unsigned long outScale);
+
 /* ---- linear transforms -------------------------------------------------------- */
 int NewLinearTransformEvaluator(void);   /* lineartransform.go:30-34 */
 /* lineartransform.go:36-93 (diagonals as C floats, LevelQ = level,

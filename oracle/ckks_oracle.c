@@ -911,57 +911,65 @@ void orc_mul_plain(const orc_ctx* c, const uint64_t* ct, int lc, const uint64_t*
         out[oo] = mulmod_b(&c->bar[i], ct[oc], pt[(size_t)i * N + x]);
     }
 }
-/* Residues of an integer constant k (two's complement int64) mod each q_i. */
-static u64 residue_i64(int64_t k, u64 q) {
-    if (k >= 0) return (u64)k % q;
-    u64 m = (u64)(-(k + 1)) % q;  /* |k| - 1 without overflow */
+typedef __int128 i128;
+/* Residues of an integer constant k mod q. */
+static u64 residue_i128(i128 k, u64 q) {
+    if (k >= 0) return (u64)((u128)k % q);
+    u64 m = (u64)((u128)(-(k + 1)) % q);  /* |k| - 1 without overflow */
     return negmod((m + 1) % q, q);
 }
 /* Lattigo's scaled real constant (bigComplexToRNSScalar at float64 encoding
  * precision): t = v * scale rounded to double, then +-0.5 (in double) and
- * truncated toward zero.  Returns 0 and sets *out when |t| < 2^62. */
-int orc_scaled_constant(double v, double scale, int64_t* out) {
+ * truncated toward zero.  Returns 0 and sets *out when |t| < 2^125. */
+static int scaled_constant128(double v, double scale, i128* out) {
     double t = v * scale;
-    if (!(t < 4611686018427387904.0 && t > -4611686018427387904.0)) return -1;
+    if (!(t < 42535295865117307932921825928971026432.0 && t > -42535295865117307932921825928971026432.0)) return -1;
     if (t > 0) t = t + 0.5; else if (t < 0) t = t - 0.5;
-    *out = (int64_t)t;
+    *out = (i128)t;
     return 0;
 }
-/* Evaluator.Mul(ct, int) (MulScalarInt, evaluator.go:188-205): every limb of
- * both parts times k mod q_i; the scale is unchanged. */
-void orc_mul_int(const orc_ctx* c, const uint64_t* ct, int l, int64_t k, uint64_t* out) {
+int orc_scaled_constant(double v, double scale, int64_t* out) {
+    i128 k;
+    if (scaled_constant128(v, scale, &k) != 0 || k >= ((i128)1 << 62) || k <= -((i128)1 << 62)) return -1;
+    *out = (int64_t)k;
+    return 0;
+}
+static void mul_const128(const orc_ctx* c, const uint64_t* ct, int l, i128 k, uint64_t* out) {
     int N = c->N;
     for (int i = 0; i <= l; i++) {
-        u64 kq = residue_i64(k, c->mod[i]);
+        u64 kq = residue_i128(k, c->mod[i]);
         for (int p = 0; p < 2; p++) for (int x = 0; x < N; x++) {
             size_t o = ((size_t)p * (l + 1) + i) * N + x; out[o] = mulmod_b(&c->bar[i], ct[o], kq);
         }
     }
 }
+/* Evaluator.Mul(ct, int) (MulScalarInt, evaluator.go:188-205): every limb of
+ * both parts times k mod q_i; the scale is unchanged. */
+void orc_mul_int(const orc_ctx* c, const uint64_t* ct, int l, int64_t k, uint64_t* out) { mul_const128(c, ct, l, (i128)k, out); }
 /* Evaluator.Mul(ct, float64) (MulScalarFloat, evaluator.go:208-225): an
  * integer-valued constant multiplies as an integer (scale unchanged);
  * otherwise the constant is scaled by q_l, rounded as above, and the output
  * scale is multiplied by q_l (the caller rescales).  Returns 1 when the
  * scale was multiplied by q_l, 0 when not, -1 when the constant is too large. */
 int orc_mul_float(const orc_ctx* c, const uint64_t* ct, int l, double v, uint64_t* out) {
-    int64_t k;
+    i128 k;
     if (v < 4611686018427387904.0 && v > -4611686018427387904.0 && v == (double)(int64_t)v) {
         orc_mul_int(c, ct, l, (int64_t)v, out);
         return 0;
     }
-    if (orc_scaled_constant(v, (double)c->mod[l], &k) != 0) return -1;
-    orc_mul_int(c, ct, l, k, out);
+    if (scaled_constant128(v, (double)c->mod[l], &k) != 0) return -1;
+    mul_const128(c, ct, l, k, out);
     return 1;
 }
 /* Evaluator.Add(ct, float64) (AddScalar / SubScalar, evaluator.go:148-185):
  * the constant scaled by the ciphertext scale and rounded is added to (or
  * subtracted from) every NTT slot of part 0 in every limb. */
 int orc_add_const(const orc_ctx* c, const uint64_t* ct, int l, double v, double scale, int sub, uint64_t* out) {
-    int N = c->N; int64_t k;
-    if (orc_scaled_constant(v, scale, &k) != 0) return -1;
-    memcpy(out, ct, 8 * (size_t)2 * (l + 1) * N);
+    int N = c->N; i128 k;
+    if (scaled_constant128(v, scale, &k) != 0) return -1;
+    if (out != ct) memcpy(out, ct, 8 * (size_t)2 * (l + 1) * N);
     for (int i = 0; i <= l; i++) {
-        u64 q = c->mod[i], kq = residue_i64(k, q);
+        u64 q = c->mod[i], kq = residue_i128(k, q);
         for (int x = 0; x < N; x++) {
             size_t o = (size_t)i * N + x; out[o] = sub ? submod(ct[o], kq, q) : addmod(ct[o], kq, q);
         }
@@ -992,6 +1000,74 @@ void orc_mul_relin(orc_ctx* c, const uint64_t* a, const uint64_t* b, int l, uint
     orc_add(c, out, t, l, 2, out);
     free(d2); free(digits); free(e0); free(e1); free(t);
 }
+
+/* Polynomial evaluation (EvaluatePolynomial, polyeval.go:62-84, monomial
+ * basis of GenerateMonomial, polyeval.go:37-47), degree <= 3 at depth
+ * ceil(log2(degree + 1)) (orion/nn/activation.py:22-28), the output scale
+ * set to out_scale as Lattigo sets its target scale:
+ *   d = 0: X*0 + c0                                       (level l)
+ *   d = 1: Rescale(X * K1) + c0, K1 = round(c1 * So q_l / s)    (l-1)
+ *   d = 2, 3: with X2 = Rescale(MulRelin(X, X)) (scale s^2 / q_l),
+ *     B = Rescale(X * K3) + c2 at scale sB = So q_{l-1} / scale(X2),
+ *         K3 = round(c3 * sB q_l / s);
+ *     P = Rescale(MulRelin(X2, B))                              (l-2, So)
+ *     A = Rescale(X * K1) dropped to l-2, + c0                  (l-2, So)
+ *     out = P + A.
+ * Constants are added as round(c * scale) (orc_add_const).  Returns the
+ * output level, or -1 on an unsupported degree or too few levels. */
+static void drop_to(const orc_ctx* c, const u64* ct, int l, int nl, u64* out) {
+    size_t N = (size_t)c->N;
+    for (int p = 0; p < 2; p++) memcpy(out + (size_t)p * (nl + 1) * N, ct + (size_t)p * (l + 1) * N, 8 * (size_t)(nl + 1) * N);
+}
+int orc_eval_poly(orc_ctx* c, const uint64_t* x, int l, double s, const double* coef, int d, double so, uint64_t* out) {
+    int N = c->N;
+    size_t ps = (size_t)N;
+    while (d > 0 && coef[d] == 0.0) d--;
+    if (d > 3 || d < 0) return -1;
+    if (d == 0) {
+        u64* z = (u64*)xmalloc(8 * 2 * (l + 1) * ps);
+        orc_mul_int(c, x, l, 0, z);
+        int r = orc_add_const(c, z, l, coef[0], so, 0, out);
+        free(z);
+        return r == 0 ? l : -1;
+    }
+    if (l < (d == 1 ? 1 : 2)) return -1;
+    i128 k1;
+    /* A = Rescale(X * K1) (+ c0 when d == 1) */
+    if (scaled_constant128(coef[1], so * (double)c->mod[l] / s, &k1) != 0) return -1;
+    u64* t = (u64*)xmalloc(8 * 2 * (l + 1) * ps);
+    u64* A = (u64*)xmalloc(8 * 2 * l * ps);
+    mul_const128(c, x, l, k1, t);
+    orc_rescale(c, t, l, A);
+    if (d == 1) {
+        int r = orc_add_const(c, A, l - 1, coef[0], so, 0, out);
+        free(t); free(A);
+        return r == 0 ? l - 1 : -1;
+    }
+    double s2 = s * s / (double)c->mod[l];
+    double sB = so * (double)c->mod[l - 1] / s2;
+    double c3 = d == 3 ? coef[3] : 0.0;
+    i128 k3;
+    if (scaled_constant128(c3, sB * (double)c->mod[l] / s, &k3) != 0) { free(t); free(A); return -1; }
+    u64* sq = (u64*)xmalloc(8 * 2 * (l + 1) * ps);
+    u64* X2 = (u64*)xmalloc(8 * 2 * l * ps);
+    orc_mul_relin(c, x, x, l, sq);
+    orc_rescale(c, sq, l, X2);
+    u64* B = (u64*)xmalloc(8 * 2 * l * ps);
+    mul_const128(c, x, l, k3, t);
+    orc_rescale(c, t, l, B);
+    if (orc_add_const(c, B, l - 1, coef[2], sB, 0, B) != 0) { free(t); free(A); free(sq); free(X2); free(B); return -1; }
+    u64* PB = (u64*)xmalloc(8 * 2 * l * ps);
+    orc_mul_relin(c, X2, B, l - 1, PB);
+    orc_rescale(c, PB, l - 1, out);
+    u64* A2 = (u64*)xmalloc(8 * 2 * (l - 1) * ps);
+    drop_to(c, A, l - 1, l - 2, A2);
+    int r = orc_add_const(c, A2, l - 2, coef[0], so, 0, A2);
+    orc_add(c, out, A2, l - 2, 2, out);
+    free(t); free(A); free(sq); free(X2); free(B); free(PB); free(A2);
+    return r == 0 ? l - 2 : -1;
+}
+
 
 /* Lattigo ring.DivRoundByLastModulusNTT (ckks Rescale, evaluator.go:131-146):
  * u = (iNTT(x_l) + q_l>>1) mod q_l; out_i = (x_i - NTT_i(u - q_l>>1)) * q_l^-1. */

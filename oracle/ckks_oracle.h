@@ -88,6 +88,9 @@ void orc_mul_int(const orc_ctx* c, const uint64_t* ct, int l, int64_t k, uint64_
 int  orc_mul_float(const orc_ctx* c, const uint64_t* ct, int l, double v, uint64_t* out);
 int  orc_add_const(const orc_ctx* c, const uint64_t* ct, int l, double v, double scale, int sub, uint64_t* out);
 void orc_mul_relin(orc_ctx* c, const uint64_t* a, const uint64_t* b, int l, uint64_t* out);
+/* Monomial polynomial of degree <= 3 on a ciphertext at level l and scale s;
+ * returns the output level (output scale = so), -1 if unsupported. */
+int  orc_eval_poly(orc_ctx* c, const uint64_t* x, int l, double s, const double* coef, int d, double so, uint64_t* out);
 
 /* ---- evaluator --------------------------------------------------------- */
 void orc_add(const orc_ctx* c, const uint64_t* a, const uint64_t* b, int level,

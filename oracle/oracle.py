@@ -88,6 +88,7 @@ def lib():
             "orc_mul_float": ([vp, u64p, ctypes.c_int, ctypes.c_double, u64p], ctypes.c_int),
             "orc_add_const": ([vp, u64p, ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_int, u64p], ctypes.c_int),
             "orc_mul_relin": ([vp, u64p, u64p, ctypes.c_int, u64p], None),
+            "orc_eval_poly": ([vp, u64p, ctypes.c_int, ctypes.c_double, dp, ctypes.c_int, ctypes.c_double, u64p], ctypes.c_int),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -304,6 +305,16 @@ class Oracle:
         out = np.zeros((2, level + 1, self.N), dtype=np.uint64)
         lib().orc_mul_relin(self.ctx, _p(a), _p(b), level, _p(out))
         return out
+
+    def eval_poly(self, ct, level, scale, coeffs, out_scale):
+        """Monomial polynomial (degree <= 3) of a ciphertext; returns (ct, level)."""
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        co = np.ascontiguousarray(np.asarray(coeffs, dtype=np.float64))
+        out = np.zeros(2 * (level + 1) * self.N, dtype=np.uint64)
+        nl = lib().orc_eval_poly(self.ctx, _p(ct), level, float(scale), _p(co, dp), len(co) - 1, float(out_scale), _p(out))
+        if nl < 0:
+            raise ValueError("unsupported polynomial")
+        return out[: 2 * (nl + 1) * self.N].reshape(2, nl + 1, self.N).copy(), nl
 
     def rescale(self, ct, level):
         ct = np.ascontiguousarray(ct, dtype=np.uint64)

@@ -279,3 +279,37 @@ def test_mul_relin(ctx):
     r = ctx.lib.RescaleNew(out)
     dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(r)))
     np.testing.assert_allclose(dec, va.astype(np.float64) * vb, atol=1e-3)
+
+
+@pytest.mark.parametrize("coeffs", [[0.25], [0.1, 0.9], [0.05, 0.5, 0.25], [0.047, 0.5, 0.24, -0.003]])
+def test_evaluate_polynomial(ctx, coeffs):
+    """GenerateMonomial + EvaluatePolynomial (polyeval.go:37-84) bit-exact with
+    the restatement; decodes to the polynomial (Orion's Activation, lowest
+    coefficient first as generate_monomial passes them)."""
+    ctx.lib.GenerateRelinearizationKey()
+    ctx.lib.NewPolynomialEvaluator()
+    top = ctx.L - 1
+    ct, ref, vals = ctx.fresh_ct(top, 57)
+    c32 = np.asarray(coeffs, dtype=np.float32)
+    pid = ctx.lib.GenerateMonomial(c32.tolist())
+    scale = 1 << ctx.logscale
+    out = ctx.lib.EvaluatePolynomial(ct, pid, scale)
+    want, nl = ctx.orc.eval_poly(ref, top, float(scale), c32.astype(np.float64), float(scale))
+    assert ctx.lib.GetCiphertextLevel(out) == nl
+    assert ctx.lib.GetCiphertextScaleDouble(out) == float(scale)
+    assert_equal_u64(ctx.lib.export_ciphertext(out), want, f"EvaluatePolynomial {coeffs}")
+    dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(out)))
+    np.testing.assert_allclose(dec, np.polyval(c32[::-1].astype(np.float64), vals.astype(np.float64)), atol=1e-3)
+
+
+def test_chebyshev_polynomial(ctx):
+    ctx.lib.GenerateRelinearizationKey()
+    top = ctx.L - 1
+    ct, _, vals = ctx.fresh_ct(top, 58)
+    c = np.asarray([0.1, 0.3, -0.2, 0.05], dtype=np.float32)
+    pid = ctx.lib.GenerateChebyshev(c.tolist())
+    out = ctx.lib.EvaluatePolynomial(ct, pid, 1 << ctx.logscale)
+    x = vals.astype(np.float64)
+    want = c[0] + c[1] * x + c[2] * (2 * x * x - 1) + c[3] * (4 * x ** 3 - 3 * x)
+    dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(out)))
+    np.testing.assert_allclose(dec, want, atol=1e-3)

@@ -520,3 +520,19 @@ def test_mul_relin_decrypts_to_product(mid):
     r = mid.rescale(out, level)
     got = mid.decode_f64(mid.decrypt(r, level - 1), level - 1, 2.0 ** 70 / mid.q[level])
     np.testing.assert_allclose(got, a.astype(np.float64) * b, atol=1e-6)
+
+
+@pytest.mark.parametrize("coeffs", [[0.25], [0.1, 0.9], [0.05, 0.5, 0.25], [0.047, 0.5, 0.24, -0.003], [0.0, 1.0, 0.0, 0.0]])
+def test_eval_poly_decrypts_to_polynomial(mid, coeffs):
+    """Degree <= 3 at depth ceil(log2(d + 1)), output at the requested scale."""
+    level = mid.L - 1
+    vals = np.linspace(-1, 1, mid.slots).astype(np.float32)
+    ct = _enc(mid, vals, level, 35, 7)
+    out, nl = mid.eval_poly(ct, level, 2.0 ** 35, coeffs, 2.0 ** 35)
+    d = len(coeffs) - 1
+    while d > 0 and coeffs[d] == 0:
+        d -= 1
+    assert nl == level - (0 if d == 0 else 1 if d == 1 else 2)
+    got = mid.decode_f64(mid.decrypt(out, nl), nl, 2.0 ** 35)
+    want = np.polyval(np.asarray(coeffs[::-1], dtype=np.float64), vals.astype(np.float64))
+    np.testing.assert_allclose(got, want, atol=1e-5)
