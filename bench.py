@@ -100,7 +100,86 @@ def cpu_baseline(q, p, h, key_seed, diagonals, selector, level, logscale, thread
         orc.close()
 
 
+def cpu_baseline_dlrm(q, p, w, threads):
+    """The whole encrypted DLRM forward (both inputs encrypted at the input
+    level, every Linear and activation) on the CPU restatement (oracle/);
+    key generation and diagonal encoding happen before the timed region.
+    Returns (inferences/s, seconds per forward, sample description)."""
+    from oracle import oracle as O
+    O.set_threads(threads)
+    c = w.cfg
+    orc = O.Oracle(c["logn"], q, p, h=c["h"], seed=1)
+    try:
+        scale = float(1 << c["logscale"])
+        slots = orc.slots
+        lts = {}
+        for name, m in w.modules.items():
+            if not hasattr(m, "diagonals"):
+                continue
+            d = m.diagonals[(0, 0)]
+            idx = list(d.keys())
+            t = orc.lt_new(idx, np.stack([d[i] for i in idx]), w.levels[name], 2.0)
+            for r in orc.lt_rotations(t):
+                if r:
+                    orc.galois_key(orc.galois_element(r))
+            for i in range(1, m.output_rotations + 1):
+                orc.galois_key(orc.galois_element(slots >> i))
+            lts[name] = (t, m)
+        orc.relin_key()
+        L = w.input_level
+        xd = orc.encrypt(orc.encode(w.dense, L, scale), L, 0)
+        xs = orc.encrypt(orc.encode(w.emb.selector, L, scale), L, 1)
+
+        def step(name, x):
+            ct, lv, sc = x
+            if name in lts:
+                t, m = lts[name]
+                out, l = orc.lt_eval(t, ct, lv)
+                sc2 = sc * orc.q[w.levels[name]]
+                out = orc.rescale(out, l)
+                sc2 /= orc.q[l]
+                l -= 1
+                for i in range(1, m.output_rotations + 1):
+                    out = orc.add(out, orc.rotate(out, l, slots >> i), l)
+                out[0] = orc.add(out[0][None], orc.encode(m.bias, l, scale)[None], l)[0]
+                return out, l, sc2
+            m = w.modules[name]
+            out, nl = orc.eval_poly(ct, lv, sc, list(m.coeffs[::-1]), scale)
+            return out, nl, scale
+        t0 = time.perf_counter()
+        x = (xd, L, scale)
+        for _, name in w.bottom_names:
+            x = step(name, x)
+        e = step("sparse_to_top", step("sparse", (xs, L, scale)))
+        z = (orc.add(x[0], e[0], x[1]), x[1], x[2])
+        for _, name in w.top_names:
+            z = step(name, z)
+        t_fwd = time.perf_counter() - t0
+        logit = orc.decode_f64(orc.decrypt(z[0], z[1]), z[1], z[2])[0]
+        sample = (f"CPU restatement (oracle/), {threads} threads: one whole encrypted forward "
+                  f"({len(lts)} Linears, {len(w.activations())} activations; keys and diagonals prepared "
+                  f"beforehand), {t_fwd:.2f} s, logit {logit:.6f}")
+        return 1.0 / t_fwd, t_fwd, sample
+    finally:
+        orc.close()
+
+
+def lt_roofline_bytes(lib, layer, N, K, w=8):
+    """(whole-layer, diagonal-MAC) algorithmic bytes of one compiled Linear
+    at its level: algorithmic_bytes with L = level + 1 active Q limbs and the
+    transform's own baby / giant counts and fold rotations."""
+    tid = list(layer.transform_ids.values())[0]
+    lti = lib.lt_info(tid)
+    Lq = layer.level + 1
+    return algorithmic_bytes(N=N, L=Lq, K=K, D=lti["plaintexts"], n1=lti["baby"], n2=lti["giant"],
+                             f=layer.output_rotations, dnum=(Lq + K - 1) // K, w=w), lti
+
+
 def describe(cfg):
+    if cfg["kind"] == "dlrm":
+        return ("encrypted HE-LRM forward at batch 1: bottom MLP 13-512-256-64-16, 26-table embedding PCMM "
+                f"(tables {cfg['rows']}x{cfg['dim']}, base-{cfg['base']} digits), repacking Linears, Add, "
+                "top MLP 432-512-256-1, degree-3 activations, no bootstrapping")
     if cfg["kind"] == "pcmm":
         if cfg.get("sizes"):
             return f"{len(cfg['sizes'])}-table embedding PCMM, tables of {cfg['sizes']} rows x {cfg['dim']}"
@@ -228,13 +307,20 @@ def main():
     lib.Synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1000.0 / args.steps
-    # one step = one query: one lookup per table for the embedding PCMM, one forward of the dense layer
+    # one step = one query: one lookup per table for the embedding PCMM, one forward of the dense layer or DLRM
     per_step = len(cfg.get("sizes") or [0] * cfg.get("fields", 1)) if cfg["kind"] == "pcmm" else 1
     lookups = per_step / (ms / 1000.0)
     if cfg["kind"] == "pcmm":
         metric, unit = (METRIC if args.workload == "pcmm26" else f"encrypted embedding lookups/sec ({args.workload})"), "lookups/s"
+    elif cfg["kind"] == "dlrm":
+        metric, unit = f"encrypted DLRM inferences/sec (HE-LRM forward, batch 1, {args.workload})", "inferences/s"
     else:
         metric, unit = f"encrypted dense-layer forwards/sec ({args.workload})", "forwards/s"
+    stages = None
+    if cfg["kind"] == "dlrm":
+        o, st = w.run_staged(lib.Synchronize, time.perf_counter)
+        o.free()
+        stages = {k: v * 1000.0 for k, v in st.items()}
 
     # per-kernel HIP-event timings (separate, untimed passes)
     lib.KernelTimingEnable(1)
@@ -251,19 +337,39 @@ def main():
 
     L, K = len(cfg["logq"]), len(cfg["logp"])
     N = 1 << cfg["logn"]
-    lti = lib.lt_info(list(w.layer.transform_ids.values())[0])
-    # the giant groups are split over this many diagonal-MAC launches per PCMM
-    chunks = max(1, round(kt["diag_mac"]["launches"] / nprof)) if kt["diag_mac"]["launches"] else 1
-    pcmm_bytes, mac_bytes = algorithmic_bytes(N=N, L=L, K=K, D=info["diagonals"], n1=lti["baby"], n2=lti["giant"],
-                                              f=info["output_rotations"], dnum=(L + K - 1) // K, chunks=chunks)
+    # diagonal-MAC launches per step (one per 32 baby steps of every Linear)
+    launches = max(1, round(kt["diag_mac"]["launches"] / nprof)) if kt["diag_mac"]["launches"] else 1
+    layers = w.linear_layers()
+    step_bytes, mac_bytes, lt_shapes = 0, 0, []
+    for layer in layers:
+        (b_layer, b_mac), lti = lt_roofline_bytes(lib, layer, N, K)
+        step_bytes += b_layer
+        mac_bytes += b_mac
+        lt_shapes.append({"level": layer.level, "diagonals": lti["plaintexts"], "baby": lti["baby"],
+                          "giant": lti["giant"], "fold": layer.output_rotations})
+    if cfg["kind"] == "dlrm":
+        # each degree-3 activation reads the relinearisation key twice at its level
+        for name, _ in w.activations():
+            lq = w.levels[name] + 1
+            step_bytes += 2 * ((lq + K - 1) // K) * 2 * (lq + K) * N * 8
+    # average algorithmic bytes per diagonal-MAC launch over one step
+    mac_per_launch = mac_bytes / launches
     mac_ms = kt["diag_mac"]["avg_ms"]
-    achieved = mac_bytes / (mac_ms / 1000.0) / 1e9 if mac_ms else None
+    achieved = mac_per_launch / (mac_ms / 1000.0) / 1e9 if mac_ms else None
     roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": (achieved / HBM_PEAK_GBS) if achieved else None, "traffic": read_traffic("diag_mac"),
-                "kernel": "diag_mac_kernel", "algorithmic_bytes_per_launch": mac_bytes, "launches_per_pcmm": chunks}
+                "frac": (achieved / HBM_PEAK_GBS) if achieved else None,
+                "traffic": read_traffic("diag_mac") if args.workload == "pcmm26" else None,
+                "kernel": "diag_mac_kernel", "algorithmic_bytes_per_launch": mac_per_launch,
+                "launches_per_step": launches}
+    lti = lib.lt_info(list(layers[0].transform_ids.values())[0])
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and cfg["kind"] == "dlrm":
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        v, t_cpu, sample = cpu_baseline_dlrm(lib.GetModuliChain(), lib.GetAuxModuliChain(), w, threads)
+        cpu = {"value": v, "unit": unit, "cores": threads, "kind": "port", "sample": sample,
+               "seconds_per_forward": t_cpu}
+    elif not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         d = w.layer.diagonals[(0, 0)]
         v, t_cpu, sample, tm = cpu_baseline(lib.GetModuliChain(), lib.GetAuxModuliChain(), cfg["h"], 1, d,
@@ -287,20 +393,25 @@ def main():
         "dtype": "u64",
         "data": "synthetic (seeded tables / weights and inputs, seeded keys and encryption randomness)",
         "config": {"workload": f"{args.workload}: {describe(cfg)}, N=2^{cfg['logn']}, "
-                               f"L={L} (60+50x{L - 1} bit), K={K} (61 bit), dnum={(L + K - 1) // K}, scale 2^{cfg['logscale']}",
-                   "diagonals": info["diagonals"], "baby_steps": lti["baby"], "giant_steps": lti["giant"],
-                   "fold_rotations": info["output_rotations"], "matrix": info["matrix"]},
-        "pcmm_ms": ms,
-        "end_to_end_hbm": {"algorithmic_bytes": pcmm_bytes,
-                           "achieved_GBs": pcmm_bytes / (ms / 1000.0) / 1e9,
-                           "frac": pcmm_bytes / (ms / 1000.0) / 1e9 / HBM_PEAK_GBS},
+                               f"L={L} (60+50x{L - 1} bit), K={K} (61 bit), dnum={(L + K - 1) // K}, scale 2^{cfg['logscale']}"},
+        "end_to_end_hbm": {"algorithmic_bytes": step_bytes,
+                           "achieved_GBs": step_bytes / (ms / 1000.0) / 1e9,
+                           "frac": step_bytes / (ms / 1000.0) / 1e9 / HBM_PEAK_GBS},
         "kernels": kt,
+        "linear_transforms": lt_shapes,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "max_abs_err_vs_plaintext": err,
         "ntt_microbench": ntt,
         "setup_s": t_setup,
     }
+    if cfg["kind"] == "dlrm":
+        line["stage_ms"] = stages
+        line["levels"] = {"input": w.input_level, "add": w.add_level, "output": 0}
+    else:
+        line["config"].update({"diagonals": info["diagonals"], "baby_steps": lti["baby"], "giant_steps": lti["giant"],
+                               "fold_rotations": info["output_rotations"], "matrix": info["matrix"]})
+        line["pcmm_ms"] = ms
     print(json.dumps(line), flush=True)
 
 

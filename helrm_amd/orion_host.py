@@ -196,6 +196,7 @@ class Scheme:
         backend.NewDecryptor()
         backend.NewEvaluator()
         backend.NewLinearTransformEvaluator()
+        backend.NewPolynomialEvaluator()
         self.saved_rotation_keys = set()
 
     # orion/backend/python/encoder.py:14-88 (real values, default path)
@@ -355,6 +356,38 @@ class LinearLayer:
         for t in self.transform_ids.values():
             self.scheme.backend.DeleteLinearTransform(int(t))
         self.transform_ids = {}
+
+
+class Activation:
+    """orion.nn.Activation (orion/nn/activation.py:12-48): a polynomial given
+    highest-degree coefficient first (the Horner order of its cleartext
+    forward), compiled through PolynomialEvaluator.generate_monomial, which
+    hands the backend the coefficients lowest degree first
+    (orion/backend/python/poly_evaluator.py:15-18), and evaluated on every
+    ciphertext of the tensor at `output_scale` (the default scale when unset,
+    poly_evaluator.py:25-35).  Consumes ceil(log2(len(coeffs))) levels."""
+
+    def __init__(self, scheme, coeffs):
+        self.scheme = scheme
+        self.coeffs = [float(c) for c in coeffs]
+        self.depth = int(math.ceil(math.log2(len(self.coeffs)))) if len(self.coeffs) > 1 else 0
+        self.output_scale = None
+        self.poly = None
+
+    def compile(self):
+        self.poly = self.scheme.backend.GenerateMonomial(self.coeffs[::-1])
+        return self
+
+    def clear(self, x):
+        out = 0.0
+        for c in self.coeffs:
+            out = c + x * out
+        return out
+
+    def forward(self, x):
+        b = self.scheme.backend
+        scale = self.output_scale or self.scheme.params.get_default_scale()
+        return CipherTensor(self.scheme, [b.EvaluatePolynomial(c, self.poly, int(scale)) for c in x.ids], x.n)
 
 
 def embedding_pcmm(scheme, layer, selector):

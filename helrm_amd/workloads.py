@@ -21,6 +21,14 @@
                 N=2^16, 16 Q limbs, P=[61x6] (dnum 3): 512 diagonals,
                 16 baby x 32 giant steps, 6 fold rotations
   dense_lt_n13  the dense_lt structure at N=2^13
+  dlrm          encrypted HE-LRM forward at batch 1 (dlrm.py:181-231): bottom
+                MLP 13-512-256-64-16, the pcmm26 embedding PCMM, both
+                repacking Linears, Add, top MLP 432-512-256-1, degree-3
+                activations after every Linear but the last; weights and
+                biases N(0, 0.05), 13 dense features log-normal(0, 1);
+                N=2^16, Q=[60,50x29] (30 limbs), P=[61x8], scale 2^50, no
+                bootstrapping
+  dlrm_n13      the dlrm network at N=2^13 on the same 30-limb chain
 
 The embedding selector is the digit one-hot of examples/criteo/dlrm.py:202-221,
 the plaintext matrix block_diag(W_0..W_25)^T of dlrm.py:241-247 and the
@@ -45,6 +53,10 @@ CONFIGS = {
                        fields=26, rows=4096, dim=16, base=16, init="normal", init_arg=0.05, repack=(432, 16)),
     "pcmm26_top_n13": dict(kind="pcmm", logn=13, logq=[60] + [50] * 8, logp=[61] * 3, logscale=50, h=192,
                            fields=26, rows=4096, dim=16, base=16, init="normal", init_arg=0.05, repack=(432, 16)),
+    "dlrm": dict(kind="dlrm", logn=16, logq=[60] + [50] * 29, logp=[61] * 8, logscale=50, h=192,
+                 fields=26, rows=4096, dim=16, base=16, init="normal", init_arg=0.05, weight_std=0.05),
+    "dlrm_n13": dict(kind="dlrm", logn=13, logq=[60] + [50] * 29, logp=[61] * 8, logscale=50, h=192,
+                     fields=26, rows=4096, dim=16, base=16, init="normal", init_arg=0.05, weight_std=0.05),
     "dense_lt": dict(kind="dense", logn=16, logq=[60] + [50] * 15, logp=[61] * 6, logscale=50, h=192,
                      out_features=512, in_features=256, inputs=512),
     "dense_lt_n13": dict(kind="dense", logn=13, logq=[60] + [50] * 15, logp=[61] * 6, logscale=50, h=192,
@@ -84,6 +96,9 @@ class LinearWorkload:
     def decrypt_output(self, out):
         vals = self.scheme.decode(self.scheme.decrypt(out))
         return vals[: self.matrix.shape[0]]
+
+    def linear_layers(self):
+        return [self.layer]
 
     def shape_info(self):
         d = self.layer.diagonals[(0, 0)]
@@ -160,6 +175,9 @@ class SparseToTopWorkload(PCMMWorkload):
         vals = self.scheme.decode(self.scheme.decrypt(out))
         return vals[: self.repack_matrix.shape[0]]
 
+    def linear_layers(self):
+        return [self.layer, self.repack]
+
     def shape_info(self):
         info = super().shape_info()
         info["repack"] = {"diagonals": len(self.repack.diagonals[(0, 0)]),
@@ -181,8 +199,238 @@ class DenseLTWorkload(LinearWorkload):
         self.expected = self.matrix.astype(np.float64) @ self.input[: c["in_features"]].astype(np.float64)
 
 
+# Degree-3 activation, highest-degree coefficient first (orion.nn.Activation
+# order): the least-squares cubic fit of ReLU on [-2, 4], rounded to four
+# places.  It stands in for HE-LRM's on.ReLU (dlrm.py:133-139), whose
+# minimax sign composite needs bootstrapping.
+ACTIVATION3 = (-0.0320, 0.2195, 0.5706, 0.2048)
+BOTTOM_WIDTHS = (13, 512, 256, 64, 16)   # dlrm.py:19
+TOP_WIDTHS = (432, 512, 256, 1)          # dlrm.py:20
+
+
+def plan_levels(bottom_layers, top_layers, sparse_depth, linear_depth=1, act_depth=2):
+    """Levels Orion's bootstrap solver (orion/core/auto_bootstrap.py:114-158)
+    gives HE-LRM when the chain is long enough to need no bootstrap: a linear
+    layer's cost grows with its level (level_dag.py:167-197) and activations
+    cost nothing, so every layer sits at the lowest level its successors
+    allow and the network ends at level 0.  Layers are ('L', name) or ('A',
+    name) in forward order; returns ({name: level}, add_level, input_level)."""
+    levels, lvl = {}, 0
+    for kind, name in reversed(top_layers):
+        lvl += linear_depth if kind == "L" else act_depth
+        levels[name] = lvl
+    add_level = lvl
+    for kind, name in reversed(bottom_layers):
+        lvl += linear_depth if kind == "L" else act_depth
+        levels[name] = lvl
+    input_level = lvl
+    levels["sparse_to_top"] = add_level + linear_depth
+    levels["sparse"] = add_level + linear_depth + sparse_depth
+    return levels, add_level, input_level
+
+
+class DLRMWorkload:
+    """HELRM.forward (dlrm.py:224-231) under encryption:
+        top(add(bottom_to_top(bottom(dense)), sparse_to_top(sparse(selector))))
+    with every on.Linear a LinearLayer (hybrid packing; the network's last
+    Linear square-packed, orion/core/orion.py:255-285), every activation an
+    Activation of ACTIVATION3, and both inputs encrypted at the input level
+    (bench_sweep.py:346-349, 395-399).  The embedding part is the
+    PCMMWorkload of the same config and seed."""
+
+    def __init__(self, backend, name="dlrm", seed=0, key_seed=1):
+        c = CONFIGS[name]
+        self.name, self.cfg = name, c
+        self.backend = backend
+        self.params = oh.Params(c["logn"], c["logq"], c["logp"], c["logscale"], c["h"], seed=key_seed)
+        self.emb = PCMMWorkload(None, name, seed=seed, key_seed=key_seed)
+        rng = np.random.default_rng([seed, 5])
+        std = c["weight_std"]
+
+        def linear(i, o):
+            return (rng.normal(0.0, std, (o, i)).astype(np.float32), rng.normal(0.0, std, o).astype(np.float32))
+        self.bottom_w = [linear(i, o) for i, o in zip(BOTTOM_WIDTHS, BOTTOM_WIDTHS[1:])]
+        self.top_w = [linear(i, o) for i, o in zip(TOP_WIDTHS, TOP_WIDTHS[1:])]
+        self.dense = rng.lognormal(0.0, 1.0, BOTTOM_WIDTHS[0]).astype(np.float32)
+        # coefficients cross the backend ABI as fp32 (polyeval.go GenerateMonomial)
+        self.coeffs = tuple(float(np.float32(cf)) for cf in ACTIVATION3)
+        dim = c["dim"]
+        width = self.emb.matrix.shape[0]
+        self.bottom_to_top_w = oh.copy_into(dim, TOP_WIDTHS[0], 0)        # dlrm.py:194
+        self.sparse_to_top_w = oh.copy_into(width, TOP_WIDTHS[0], dim)    # dlrm.py:198
+        self.bottom_names = []
+        for k in range(len(self.bottom_w)):
+            self.bottom_names += [("L", f"bottom.{2 * k}"), ("A", f"bottom.{2 * k + 1}")]
+        self.bottom_names.append(("L", "bottom_to_top"))
+        self.top_names = []
+        for k in range(len(self.top_w)):
+            self.top_names.append(("L", f"top.{2 * k}"))
+            if k < len(self.top_w) - 1:
+                self.top_names.append(("A", f"top.{2 * k + 1}"))
+        self.levels, self.add_level, self.input_level = plan_levels(self.bottom_names, self.top_names, 1)
+        self.expected = self.clear_forward()
+        self.scheme = None
+        self.modules = {}
+        self.ct_dense = self.ct_sparse = None
+
+    # ---- cleartext model (float64 on the fp32 weights) ----
+    def act(self, x):
+        out = np.zeros_like(x)
+        for cf in self.coeffs:
+            out = cf + x * out
+        return out
+
+    def clear_trace(self):
+        """Every layer's cleartext output, keyed by layer name."""
+        tr = {}
+        x = self.dense.astype(np.float64)
+        for k, (w, b) in enumerate(self.bottom_w):
+            x = w.astype(np.float64) @ x + b
+            tr[f"bottom.{2 * k}"] = x
+            x = self.act(x)
+            tr[f"bottom.{2 * k + 1}"] = x
+        dense = self.bottom_to_top_w.astype(np.float64) @ x
+        tr["bottom_to_top"] = dense
+        emb = self.emb.matrix.astype(np.float64) @ self.emb.selector
+        tr["sparse"] = emb
+        sparse = self.sparse_to_top_w.astype(np.float64) @ emb
+        tr["sparse_to_top"] = sparse
+        z = dense + sparse
+        tr["add"] = z
+        for k, (w, b) in enumerate(self.top_w):
+            z = w.astype(np.float64) @ z + b
+            tr[f"top.{2 * k}"] = z
+            if k < len(self.top_w) - 1:
+                z = self.act(z)
+                tr[f"top.{2 * k + 1}"] = z
+        return tr
+
+    def clear_forward(self):
+        return self.clear_trace()[self.top_names[-1][1]]
+
+    # ---- encrypted model ----
+    def setup(self):
+        s = self.scheme = oh.Scheme(self.params, self.backend)
+        L = self.levels
+        mods = {}
+        for k, (w, b) in enumerate(self.bottom_w):
+            mods[f"bottom.{2 * k}"] = oh.LinearLayer(s, w, b, level=L[f"bottom.{2 * k}"])
+            mods[f"bottom.{2 * k + 1}"] = oh.Activation(s, self.coeffs)
+        mods["bottom_to_top"] = oh.LinearLayer(s, self.bottom_to_top_w, level=L["bottom_to_top"])
+        mods["sparse"] = oh.LinearLayer(s, self.emb.matrix, level=L["sparse"])
+        mods["sparse_to_top"] = oh.LinearLayer(s, self.sparse_to_top_w, level=L["sparse_to_top"])
+        for k, (w, b) in enumerate(self.top_w):
+            last = k == len(self.top_w) - 1
+            mods[f"top.{2 * k}"] = oh.LinearLayer(s, w, b, level=L[f"top.{2 * k}"], last=last)
+            if not last:
+                mods[f"top.{2 * k + 1}"] = oh.Activation(s, self.coeffs)
+        for m in mods.values():
+            m.compile()
+        self.modules = mods
+        pd = s.encode(self.dense, self.input_level)
+        self.ct_dense = s.encrypt(pd)
+        ps = s.encode(self.emb.selector, self.input_level)
+        self.ct_sparse = s.encrypt(ps)
+        for i in pd.ids + ps.ids:
+            self.backend.DeletePlaintext(i)
+        return self
+
+    def run_stages(self, keep=False):
+        """One encrypted forward; with keep=True also returns every layer's
+        output ciphertext tensor (the caller frees them)."""
+        m = self.modules
+        kept = {}
+
+        def step(name, x, free_in):
+            y = m[name].forward(x)
+            if keep:
+                kept[name] = y
+            elif free_in:
+                x.free()
+            return y
+        x = self.ct_dense
+        for i, (_, name) in enumerate(self.bottom_names):
+            x = step(name, x, i > 0)
+        e = step("sparse", self.ct_sparse, False)
+        e = step("sparse_to_top", e, True)
+        z = x.add(e)
+        if keep:
+            kept["add"] = z
+        else:
+            x.free()
+            e.free()
+        for i, (_, name) in enumerate(self.top_names):
+            z = step(name, z, True)
+        return z, kept
+
+    def run(self):
+        return self.run_stages(False)[0]
+
+    # stage split of bench_sweep.py:186-192 (HELRM_STAGES)
+    STAGES = {"bottom_mlp": ("bottom", "bottom_to_top"), "lookup": ("sparse",), "sparse_to_top": ("sparse_to_top",),
+              "add": ("add",), "top_mlp": ("top",)}
+
+    def stage_of(self, name):
+        for stage, prefixes in self.STAGES.items():
+            if any(name == p or name.startswith(p + ".") for p in prefixes):
+                return stage
+        raise KeyError(name)
+
+    def run_staged(self, sync, clock):
+        """One forward with `sync()` before each timestamp around every
+        layer (the stage hooks of bench_sweep.py:195-219); returns (output,
+        {stage: seconds})."""
+        times = {}
+        m = self.modules
+
+        def step(name, x, free_in):
+            sync()
+            t0 = clock()
+            y = m[name].forward(x) if name != "add" else x[0].add(x[1])
+            sync()
+            st = self.stage_of(name)
+            times[st] = times.get(st, 0.0) + clock() - t0
+            if free_in:
+                for c in (x if isinstance(x, tuple) else (x,)):
+                    c.free()
+            return y
+        x = self.ct_dense
+        for i, (_, name) in enumerate(self.bottom_names):
+            x = step(name, x, i > 0)
+        e = step("sparse", self.ct_sparse, False)
+        e = step("sparse_to_top", e, True)
+        z = step("add", (x, e), True)
+        for _, name in self.top_names:
+            z = step(name, z, True)
+        return z, times
+
+    def linear_layers(self):
+        return [m for m in self.modules.values() if isinstance(m, oh.LinearLayer)]
+
+    def activations(self):
+        return [(n, m) for n, m in self.modules.items() if isinstance(m, oh.Activation)]
+
+    def decrypt_output(self, out):
+        return self.scheme.decode(self.scheme.decrypt(out))[: TOP_WIDTHS[-1]]
+
+    def shape_info(self):
+        info = {}
+        for kind, name in self.bottom_names + [("L", "sparse"), ("L", "sparse_to_top")] + self.top_names:
+            m = self.modules.get(name)
+            if kind == "L":
+                d = m.diagonals[(0, 0)] if m is not None else None
+                info[name] = {"level": self.levels[name], "diagonals": None if d is None else len(d),
+                              "output_rotations": None if m is None else m.output_rotations}
+            else:
+                info[name] = {"level": self.levels[name]}
+        info["input_level"], info["add_level"] = self.input_level, self.add_level
+        return info
+
+
 def make_workload(backend, name, seed=0, key_seed=1):
     c = CONFIGS[name]
+    if c["kind"] == "dlrm":
+        return DLRMWorkload(backend, name, seed=seed, key_seed=key_seed)
     if c["kind"] == "pcmm":
         cls = SparseToTopWorkload if c.get("repack") else PCMMWorkload
     else:

@@ -62,14 +62,17 @@ def oracle_pcmm(orc, diagonals, output_rotations, level, selector, logscale, enc
     return out, l, sc
 
 
-def oracle_linear(orc, ct, level, scale, diagonals, output_rotations, logscale, bias=None, bsgs_ratio=2.0):
-    """One more Orion Linear (LT at `level`, rescale, hybrid fold, bias) on an
-    oracle ciphertext at `level` and `scale`.  Returns (ct, level, scale)."""
+def oracle_linear(orc, ct, level, scale, diagonals, output_rotations, logscale, bias=None, bsgs_ratio=2.0,
+                  lt_level=None):
+    """One more Orion Linear (LT compiled at `lt_level`, default `level`;
+    rescale, hybrid fold, bias) on an oracle ciphertext at `level` and
+    `scale`.  Returns (ct, level, scale)."""
     idx = list(diagonals.keys())
     data = np.stack([diagonals[i] for i in idx])
-    t = orc.lt_new(idx, data, level, bsgs_ratio)
+    lt_level = level if lt_level is None else lt_level
+    t = orc.lt_new(idx, data, lt_level, bsgs_ratio)
     out, l = orc.lt_eval(t, ct, level)
-    sc = scale * orc.q[level]
+    sc = scale * orc.q[lt_level]
     out = orc.rescale(out, l)
     sc /= orc.q[l]
     l -= 1
@@ -78,3 +81,43 @@ def oracle_linear(orc, ct, level, scale, diagonals, output_rotations, logscale, 
     b = np.zeros(1, np.float32) if bias is None else bias
     out[0] = orc.add(out[0][None], orc.encode(b, l, float(1 << logscale))[None], l)[0]
     return out, l, sc
+
+
+def oracle_dlrm(orc, w, dense_index=0, sparse_index=1, keep=False):
+    """DLRMWorkload.run_stages on the CPU restatement: both inputs encrypted
+    at the input level with encryption indices `dense_index` and
+    `sparse_index`, then every Linear (oracle_linear) and activation
+    (monomial eval_poly at the default scale) in forward order.  Returns
+    ((ct, level, scale), {layer name: (ct, level, scale)} when keep)."""
+    logscale = w.cfg["logscale"]
+    scale = float(1 << logscale)
+    L = w.input_level
+    trace = {}
+
+    def enc(values, index):
+        return orc.encrypt(orc.encode(np.asarray(values, np.float32), L, scale), L, index), L, scale
+
+    def step(name, x):
+        ct, l, sc = x
+        m = w.modules[name]
+        if hasattr(m, "diagonals"):
+            y = oracle_linear(orc, ct, l, sc, m.diagonals[(0, 0)], m.output_rotations, logscale, bias=m.bias,
+                              lt_level=w.levels[name])
+        else:
+            out, nl = orc.eval_poly(ct, l, sc, list(m.coeffs[::-1]), scale)
+            y = (out, nl, scale)
+        if keep:
+            trace[name] = y
+        return y
+    x = enc(w.dense, dense_index)
+    for _, name in w.bottom_names:
+        x = step(name, x)
+    e = step("sparse", enc(w.emb.selector, sparse_index))
+    e = step("sparse_to_top", e)
+    assert x[1] == e[1] and x[2] == e[2]
+    z = (orc.add(x[0], e[0], x[1]), x[1], x[2])
+    if keep:
+        trace["add"] = z
+    for _, name in w.top_names:
+        z = step(name, z)
+    return z, trace

@@ -1,0 +1,72 @@
+"""Encrypted HE-LRM forward (examples/criteo/dlrm.py:181-231) on the GPU:
+bottom MLP, embedding PCMM, both repacking Linears, Add and top MLP with
+degree-3 activations, on a 30-limb chain without bootstrapping.
+
+* dlrm_n13: every layer's output ciphertext is bit-exact with the same flow
+  on the CPU restatement (oracle/), which itself decrypts to the cleartext
+  model.
+* dlrm (N=2^16): the decrypted logit is within 2^-20 of the float64 cleartext
+  forward on the same fp32 weights.
+"""
+import numpy as np
+import pytest
+
+from helpers import assert_equal_u64, oracle_dlrm
+from oracle import oracle as O
+from helrm_amd.workloads import DLRMWorkload
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2.0 ** -20
+
+
+def test_dlrm_n13_bitexact_vs_oracle(hip_lib):
+    name = "dlrm_n13"
+    print(f"[dlrm] {name}: building", flush=True)
+    w = DLRMWorkload(hip_lib, name, seed=3, key_seed=17).setup()
+    print(f"[dlrm] {name}: {w.shape_info()}", flush=True)
+    out, kept = w.run_stages(keep=True)
+    got = {n: (hip_lib.export_ciphertext(t.ids[0]), hip_lib.GetCiphertextLevel(t.ids[0]),
+               hip_lib.GetCiphertextScaleDouble(t.ids[0])) for n, t in kept.items()}
+    y = w.decrypt_output(out)
+    c = w.cfg
+    print(f"[dlrm] {name}: running the restatement", flush=True)
+    orc = O.Oracle(c["logn"], hip_lib.GetModuliChain(), hip_lib.GetAuxModuliChain(), h=c["h"], seed=17)
+    try:
+        (want, l, sc), trace = oracle_dlrm(orc, w, keep=True)
+        clear = w.clear_trace()
+        for n, (ct, lv, s) in trace.items():
+            g, glv, gs = got[n]
+            assert glv == lv and gs == s, f"{n}: level/scale {glv}/{gs} vs {lv}/{s}"
+            assert_equal_u64(g, ct, f"{name} {n} output")
+            ref = clear[n]
+            dec = orc.decode_f64(orc.decrypt(ct, lv), lv, s)[: len(ref)]
+            assert np.abs(dec - ref).max() < TOL, n
+        print(f"[dlrm] {name}: {len(trace)} layer outputs bit-exact", flush=True)
+    finally:
+        orc.close()
+    err = np.abs(y - w.expected).max()
+    print(f"[dlrm] {name}: logit {y[0]:.9f} vs {w.expected[0]:.9f} (|err| {err:.3e})", flush=True)
+    assert err < TOL
+    for t in kept.values():
+        t.free()
+    hip_lib.DeleteScheme()
+
+
+def test_dlrm_full_size_decrypts(hip_lib):
+    print("[dlrm] dlrm (N=2^16): building", flush=True)
+    w = DLRMWorkload(hip_lib, "dlrm", seed=3, key_seed=17).setup()
+    info = w.shape_info()
+    print(f"[dlrm] dlrm: {info}", flush=True)
+    assert info["bottom.0"]["diagonals"] == 512 and info["sparse"]["diagonals"] == 512
+    assert info["top.4"]["output_rotations"] == 0
+    out = w.run()
+    assert hip_lib.GetCiphertextLevel(out.ids[0]) == 0
+    y = w.decrypt_output(out)
+    err = np.abs(y - w.expected).max()
+    print(f"[dlrm] dlrm: logit {y[0]:.9f} vs {w.expected[0]:.9f} (|err| {err:.3e})", flush=True)
+    assert err < TOL
+    # the square-packed last layer leaves no partial sums in the other slots
+    full = np.asarray(w.scheme.decode(w.scheme.decrypt(out.__class__(w.scheme, out.ids, 4096))))
+    assert np.abs(full[1:]).max() < TOL
+    hip_lib.DeleteScheme()

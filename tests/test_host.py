@@ -133,3 +133,62 @@ def test_ragged_selector_and_matrix():
     np.testing.assert_allclose(w.matrix.astype(np.float64) @ w.selector, w.expected, atol=1e-6)
     d, r = oh.diagonalize(w.matrix, 4096)
     assert r == 4  # block height 256 for 160 outputs
+
+
+def test_dlrm_levels_follow_orion_solver():
+    """Lowest-cost level plan of orion/core/auto_bootstrap.py for HE-LRM with
+    no bootstrap: linear layers cost level x diagonals (level_dag.py:167-197),
+    activations nothing, so the chain is tight and ends at level 0; the
+    degree-3 activations take 2 levels (activation.py:23-25)."""
+    from helrm_amd.workloads import DLRMWorkload
+    w = DLRMWorkload(None, "dlrm", seed=0)
+    assert w.levels == {"bottom.0": 20, "bottom.1": 19, "bottom.2": 17, "bottom.3": 16, "bottom.4": 14,
+                        "bottom.5": 13, "bottom.6": 11, "bottom.7": 10, "bottom_to_top": 8,
+                        "sparse": 9, "sparse_to_top": 8,
+                        "top.0": 7, "top.1": 6, "top.2": 4, "top.3": 3, "top.4": 1}
+    assert w.input_level == 20 and w.add_level == 7
+    assert w.input_level < len(w.cfg["logq"])
+
+
+@pytest.mark.parametrize("name", ["dlrm_n13", "dlrm"])
+def test_dlrm_slot_algebra_matches_cleartext(name):
+    """The encrypted forward's slot algebra in float64 -- hybrid diagonals and
+    fold (periodic copies without bias), bias in the first rows only, the
+    activation on every slot, square packing for the last Linear
+    (orion/core/orion.py:255-285) -- gives the cleartext model on the live
+    rows of every layer, and zeros outside slot 0 at the end."""
+    from helrm_amd.workloads import DLRMWorkload
+    w = DLRMWorkload(None, name, seed=1)
+    S = 1 << (w.cfg["logn"] - 1)
+    clear = w.clear_trace()
+
+    def linear(x, W, b=None, last=False):
+        d, rots = oh.diagonalize(W, S, "hybrid", last)
+        y = np.zeros(S)
+        for i, v in d[(0, 0)].items():
+            y += v.astype(np.float64) * np.roll(x, -i)
+        for i in range(1, rots + 1):
+            y = y + np.roll(y, -(S // 2 ** i))
+        if b is not None:
+            y[:len(b)] += b
+        return y
+    x = np.zeros(S)
+    x[:13] = w.dense
+    for k, (W, b) in enumerate(w.bottom_w):
+        x = linear(x, W, b)
+        np.testing.assert_allclose(x[:W.shape[0]], clear[f"bottom.{2 * k}"], atol=1e-12)
+        x = w.act(x)
+    x = linear(x, w.bottom_to_top_w)
+    e = np.zeros(S)
+    e[:len(w.emb.selector)] = w.emb.selector
+    e = linear(linear(e, w.emb.matrix), w.sparse_to_top_w)
+    z = x + e
+    np.testing.assert_allclose(z[:432], clear["add"], atol=1e-12)
+    for k, (W, b) in enumerate(w.top_w):
+        last = k == len(w.top_w) - 1
+        z = linear(z, W, b, last)
+        np.testing.assert_allclose(z[:W.shape[0]], clear[f"top.{2 * k}"], atol=1e-12)
+        if not last:
+            z = w.act(z)
+    assert abs(z[0] - w.expected[0]) < 1e-12
+    assert np.abs(z[1:]).max() < 1e-12
