@@ -326,9 +326,13 @@ def main():
     lib.KernelTimingEnable(1)
     nprof = 3
     for _ in range(nprof):
+        # idle gaps isolate each profiled pass in a kernel trace of this run
+        lib.Synchronize()
+        time.sleep(0.05)
         o = w.run()
         o.free()
     lib.Synchronize()
+    time.sleep(0.05)
     kt = {}
     for name in ("diag_mac", "giant_acc", "keymac_baby"):
         c, tot = lib.kernel_time(name)
