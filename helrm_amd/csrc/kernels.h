@@ -129,5 +129,14 @@ void launch_sample_cbd(u64* out, RowMap rm, u64 seed, u64 stream, const ModC* mo
 void launch_signed_rows(u64* out, RowMap rm, const int8_t* v, const ModC* mods, int N, hipStream_t st);
 void launch_gk_combine(u64* b, const u64* a, const u64* soR, const u64* sR, int own0, int own1, const u64* pmod, int rows, const ModC* mods, int N, hipStream_t st);
 void launch_encode_residues(u64* out, RowMap rm, const u64* rec, const ModC* mods, int N, hipStream_t st);
+// Device encoder (encoder.hip): plaintext p of a batch takes element k from
+// data[src * slots + ((k + rot) mod slots)] (zero past nvals), runs the special
+// inverse FFT in float64 (work buffers re/im, pstride words per plaintext),
+// rounds to fixed point at `scale` and writes its residues to rows rm of
+// out + p * out_pstride (coefficient domain; the caller applies the NTT).
+struct EncodeSrc { int src, rot; };
+void launch_encode_fft(u64* out, size_t out_pstride, RowMap rm, const float* data, const EncodeSrc* src, int np, int nvals,
+                       double scale, double* re, double* im, size_t pstride, const int* rotgroup, const double* rre,
+                       const double* rim, const ModC* mods, int logN, hipStream_t st);
 // out[r][x] = sum_{p < npoly} a[p][r][x] * b[p][r][x] mod q_r, rows r < nrows of the modulus table
 void launch_mulacc(const u64* a, const u64* b, u64* out, int npoly, int nrows, const ModC* mods, int N, hipStream_t st);

@@ -277,6 +277,8 @@ struct Scheme {
   // encoder
   std::vector<double> rre, rim;
   std::vector<int> rotgroup;
+  DevArray<double> d_rre, d_rim;
+  DevArray<int> d_rotgroup;
   Timing timing;
   bool encoder = false, encryptor = false, decryptor = false, evaluator = false, lteval = false;
   ~Scheme() {
@@ -574,8 +576,9 @@ void ensure_relin_key() {
 }
 
 // ============================================================================
-// encoder: float64 special FFT on the host (Lattigo ckks.Encoder algorithm),
-// fixed-point rounding to per-coefficient records, residues + NTT on the GPU
+// encoder: root and rotation-group tables (Lattigo ckks.Encoder); the special
+// inverse FFT, fixed-point rounding and residues run on the GPU (encoder.hip),
+// the decoder's forward special FFT on the host
 // ============================================================================
 void init_encoder(Scheme& s) {
   const int M = 2 * s.N, slots = s.N / 2, quarm = M >> 2;
@@ -590,28 +593,13 @@ void init_encoder(Scheme& s) {
   s.rotgroup.resize(slots);
   u64 p = 1;
   for (int j = 0; j < slots; j++) { s.rotgroup[j] = (int)p; p = (p * 5) & (u64)(M - 1); }
+  s.d_rre = DevArray<double>(s.rre.size()); upload(s.d_rre.p, s.rre.data(), s.rre.size());
+  s.d_rim = DevArray<double>(s.rim.size()); upload(s.d_rim.p, s.rim.data(), s.rim.size());
+  s.d_rotgroup = DevArray<int>(slots); upload(s.d_rotgroup.p, s.rotgroup.data(), slots);
 }
 void bitrev(std::vector<double>& re, std::vector<double>& im, int n) {
   int logn = 0; while ((1 << logn) < n) logn++;
   for (int i = 0; i < n; i++) { int j = brv(i, logn); if (j > i) { std::swap(re[i], re[j]); std::swap(im[i], im[j]); } }
-}
-void special_ifft(const Scheme& s, std::vector<double>& re, std::vector<double>& im, int n) {
-  const int M = 2 * s.N;
-  for (int len = n; len >= 2; len >>= 1) {
-    int lenh = len >> 1, lenq = len << 2, gap = M / lenq, mask = lenq - 1;
-    for (int i = 0; i < n; i += len)
-      for (int j = 0; j < lenh; j++) {
-        int k = i + j;
-        double ur = re[k], ui = im[k], vr = re[k + lenh], vi = im[k + lenh];
-        int idx = (lenq - (s.rotgroup[j] & mask)) * gap;
-        double wr = s.rre[idx], wi = s.rim[idx];
-        double dr = ur - vr, di = ui - vi;
-        re[k] = ur + vr; im[k] = ui + vi;
-        re[k + lenh] = dr * wr - di * wi; im[k + lenh] = dr * wi + di * wr;
-      }
-  }
-  bitrev(re, im, n);
-  for (int i = 0; i < n; i++) { re[i] /= (double)n; im[i] /= (double)n; }
 }
 void special_fft(const Scheme& s, std::vector<double>& re, std::vector<double>& im, int n) {
   const int M = 2 * s.N;
@@ -630,36 +618,26 @@ void special_fft(const Scheme& s, std::vector<double>& re, std::vector<double>& 
       }
   }
 }
-// one coefficient -> {magnitude, neg | shift<<8}: |v|*scale, +0.5 and truncate
-// below 2^64; exact mantissa * 2^shift above (Lattigo SingleFloat64ToFixedPointCRT)
-inline void fixed_point(double value, double scale, u64* rec) {
-  if (value == 0) { rec[0] = 0; rec[1] = 0; return; }
-  u64 neg = 0;
-  if (value < 0) { neg = 1; scale *= -1; }
-  value *= scale;
-  if (value >= 1.8446744073709552e+19) {
-    int e; double m = std::frexp(value, &e);
-    rec[0] = (u64)std::ldexp(m, 53);
-    rec[1] = neg | ((u64)(e - 53) << 8);
-  } else {
-    rec[0] = (u64)(value + 0.5);
-    rec[1] = neg;
-  }
-}
-void encode_records(const Scheme& s, const double* v, int n, double scale, std::vector<u64>& rec) {
-  const int slots = s.N / 2;
-  std::vector<double> re(slots, 0.0), im(slots, 0.0);
-  for (int i = 0; i < n && i < slots; i++) re[i] = v[i];
-  special_ifft(s, re, im, slots);
-  rec.resize((size_t)2 * s.N);
-  for (int i = 0; i < slots; i++) { fixed_point(re[i], scale, &rec[2 * i]); fixed_point(im[i], scale, &rec[2 * (i + slots)]); }
-}
-// residues of records into rows rm of out, then forward NTT
-void encode_to_device(const std::vector<u64>& rec, RowMap rm, u64* out) {
+// Encode np plaintexts on the device: plaintext p reads data[src[p].src * slots
+// + ((k + src[p].rot) mod slots)] (zero past nvals), its residues go to rows
+// rm of out + p * out_pstride, then the forward NTT.  Batches of up to 64
+// plaintexts share one work buffer.
+void encode_device(const float* h_data, size_t ndata, const std::vector<EncodeSrc>& src, int nvals, double scale, RowMap rm,
+                   u64* out, size_t out_pstride) {
   Scheme& s = sch();
-  DU64 drec(rec.size()); upload(drec.p, rec.data(), rec.size());
-  launch_encode_residues(out, rm, drec.p, s.d_mods.p, s.N, s.st);
-  ntt(out, 0, 1, rm, true);
+  const int N = s.N, slots = N / 2;
+  DevArray<float> dd(std::max<size_t>(ndata, 1));
+  if (ndata) upload(dd.p, h_data, ndata);
+  const int np = (int)src.size(), chunk = std::min(np, 64);
+  DevArray<EncodeSrc> ds(np); upload(ds.p, src.data(), np);
+  DevArray<double> re((size_t)chunk * slots), im((size_t)chunk * slots);
+  for (int c0 = 0; c0 < np; c0 += chunk) {
+    const int nb = std::min(chunk, np - c0);
+    u64* o = out + (size_t)c0 * out_pstride;
+    launch_encode_fft(o, out_pstride, rm, dd.p, ds.p + c0, nb, nvals, scale, re.p, im.p, slots, s.d_rotgroup.p, s.d_rre.p,
+                      s.d_rim.p, s.d_mods.p, s.logN, s.st);
+    ntt(o, out_pstride, nb, rm, true);
+  }
   sync();
 }
 
@@ -1160,22 +1138,10 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
   t->diags = DU64((size_t)(np + 1) * nqp_lt * N);
   HCHECK(hipMemsetAsync(t->diags.p + (size_t)np * nqp_lt * N, 0, (size_t)nqp_lt * N * 8, s.st));
   RowMap rm{nqp_lt, level + 1, 0, s.L, 0, 0};
-  // host FFT in parallel, device residues + NTT + Montgomery conversion per batch
-  const int chunk = 16;
-  std::vector<std::vector<u64>> recs(chunk);
-  for (int c0 = 0; c0 < np; c0 += chunk) {
-    int c1 = std::min(np, c0 + chunk);
-    std::vector<std::thread> th;
-    for (int p = c0; p < c1; p++)
-      th.emplace_back([&, p]() {
-        std::vector<double> buf(slots);
-        int src = order[p].second, rot = rotv[p];
-        for (int k = 0; k < slots; k++) buf[k] = (double)data[(size_t)src * slots + ((k + rot) & (slots - 1))];
-        encode_records(s, buf.data(), slots, t->scale, recs[p - c0]);
-      });
-    for (auto& x : th) x.join();
-    for (int p = c0; p < c1; p++) encode_to_device(recs[p - c0], rm, t->diags.p + (size_t)p * nqp_lt * N);
-  }
+  // special FFT, fixed point, residues in QP and NTT on the device, then the Montgomery conversion
+  std::vector<EncodeSrc> src(np);
+  for (int p = 0; p < np; p++) src[p] = EncodeSrc{order[p].second, rotv[p]};
+  encode_device(data, (size_t)ndata, src, slots, t->scale, rm, t->diags.p, (size_t)nqp_lt * N);
   launch_mont_convert(t->diags.p, (size_t)nqp_lt * N, np, rm, s.d_mods.p, N, true, s.st);
   for (auto& o : order) t->plain_idx.push_back(o.first);
   if (!t->naive) {
@@ -1385,16 +1351,17 @@ std::unique_ptr<Plain> decrypt_ct(const Cipher& ct) {
   return p;
 }
 
-std::unique_ptr<Plain> encode_values(const double* v, int n, int level, double scale) {
+std::unique_ptr<Plain> encode_values(const float* v, int n, int level, double scale) {
   Scheme& s = sch();
   REQUIRE(level >= 0 && level < s.L, "invalid level");
-  REQUIRE(n <= s.N / 2, "too many values for the slot count");
+  REQUIRE(n >= 0 && n <= s.N / 2, "too many values for the slot count");
   auto p = std::make_unique<Plain>();
   p->level = level; p->scale = scale; p->logslots = s.logN - 1;
   p->d = DU64((size_t)(level + 1) * s.N);
-  std::vector<u64> rec;
-  encode_records(s, v, n, scale, rec);
-  encode_to_device(rec, rows_q(level), p->d.p);
+  // the load kernel reads a full slots-wide row: pad the values with zeros
+  std::vector<float> buf((size_t)s.N / 2, 0.0f);
+  std::copy(v, v + n, buf.begin());
+  encode_device(buf.data(), buf.size(), {EncodeSrc{0, 0}}, n, scale, rows_q(level), p->d.p, 0);
   return p;
 }
 std::vector<double> decode_pt(const Plain& p) {
@@ -1473,8 +1440,7 @@ int GenerateEvaluationKeys(void) { return guard([&] { sch(); return 0; }); }
 int NewEncoder(void) { return guard([&] { sch().encoder = true; return 0; }); }
 int Encode(const float* values, int lenValues, int level, unsigned long scale) {
   return guard([&] {
-    std::vector<double> v(values, values + lenValues);
-    return push_pt(encode_values(v.data(), lenValues, level, (double)scale));
+    return push_pt(encode_values(values, lenValues, level, (double)scale));
   });
 }
 ArrayResultFloat Decode(int plaintextID) {

@@ -86,6 +86,26 @@ def test_encode(ctx):
         ctx.lib.DeletePlaintext(pt)
 
 
+def test_encode_edge_cases(ctx):
+    """The device encoder against the restatement on the values the fixed-point
+    conversion treats specially: zeros, values below one unit of the scale,
+    magnitudes whose scaled value passes 2^64 (exact mantissa * 2^e records),
+    both signs, a partly filled slot vector, and the diagonal scale q_level."""
+    level = ctx.L - 1
+    n = ctx.slots // 2 + 3
+    vals = ctx.rng.uniform(-1, 1, n).astype(np.float32)
+    special = np.array([0.0, 1e-12, -1e-12, 1e4, -1e4, 3e6, -3e6, 65504.0, -0.0, 2.0 ** -20], dtype=np.float32)
+    vals[:len(special)] = special
+    vals[-len(special):] = special[::-1]
+    for scale in (1 << ctx.logscale, ctx.q[level]):
+        pt = ctx.lib.Encode(vals.tolist(), level, scale)
+        assert_equal_u64(ctx.lib.export_plaintext(pt), ctx.orc.encode(vals, level, float(scale)), f"encode scale {scale}")
+        ctx.lib.DeletePlaintext(pt)
+    pt = ctx.lib.Encode([], level, 1 << ctx.logscale)
+    assert not np.any(ctx.lib.export_plaintext(pt))
+    ctx.lib.DeletePlaintext(pt)
+
+
 def test_encrypt_decrypt(ctx):
     level = ctx.L - 1
     ct, ref, vals = ctx.fresh_ct(level, 3)
