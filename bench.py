@@ -269,6 +269,8 @@ def main():
     ap.add_argument("--no-ntt-microbench", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--seeded-upload", action="store_true",
+                    help="upload the selector as (b, seed) and rebuild a on the device inside every step")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (PMC counter calibration) and exit")
     args = ap.parse_args()
@@ -290,6 +292,13 @@ def main():
     t_setup = time.perf_counter() - t_setup
     info = w.shape_info()
     cfg = CONFIGS[args.workload]
+    if args.seeded_upload:
+        w.use_seeded_upload(0x5EED + args.seed)
+    sel = w.ct_sparse if cfg["kind"] == "dlrm" else w.ct_in
+    upload = {"seeded": bool(args.seeded_upload),
+              "bytes": sum((lib.GetCiphertextBxBytes(c) + 8) if args.seeded_upload else lib.GetCiphertextBytes(c)
+                           for c in sel.ids),
+              "full_ciphertext_bytes": sum(lib.GetCiphertextBytes(c) for c in sel.ids)}
 
     # correctness of the benchmarked path (outside the timed region)
     out = w.run()
@@ -403,6 +412,7 @@ def main():
                            "frac": step_bytes / (ms / 1000.0) / 1e9 / HBM_PEAK_GBS},
         "kernels": kt,
         "linear_transforms": lt_shapes,
+        "selector_upload": upload,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "max_abs_err_vs_plaintext": err,

@@ -137,6 +137,11 @@ _SIGNATURES = {
     "NewDecryptor": ([], _I),
     "Encrypt": ([_I], _I),
     "Decrypt": ([_I], _I),
+    "EncryptSeeded": ([_I, _c.c_ulonglong], _I),
+    "DropAx": ([_I], _I),
+    "ExpandSeededAx": ([_I, _c.c_ulonglong], _I),
+    "GetCiphertextBytes": ([_I], _c.c_double),
+    "GetCiphertextBxBytes": ([_I], _c.c_double),
     "SetEncryptionCounter": ([_c.c_uint64], _I),
     # evaluator
     "NewEvaluator": ([], _I),

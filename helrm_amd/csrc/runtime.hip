@@ -147,6 +147,8 @@ inline u64 ST_ENC_E0(u64 e) { return (7ULL << 56) | e; }
 inline u64 ST_ENC_E1(u64 e) { return (8ULL << 56) | e; }
 inline u64 ST_RLK_A(u64 d) { return (9ULL << 56) | d; }
 inline u64 ST_RLK_E(u64 d) { return (10ULL << 56) | d; }
+constexpr u64 ST_SEED_A = 11ULL << 56;
+inline u64 ST_SEED_E(u64 e) { return (12ULL << 56) | e; }
 // ternary vector with exactly h entries +-1 (partial Fisher-Yates)
 std::vector<int8_t> ternary_hw(u64 seed, u64 stream, int N, int h) {
   std::vector<int> idx(N);
@@ -1338,6 +1340,32 @@ std::unique_ptr<Cipher> encrypt_pt(const Plain& pt) {
   sync();
   return out;
 }
+// Seeded secret-key encryption (the compressed upload of
+// orion/backend/cheddar/ext/cheddar_pybind.cu:627-660): a is expanded from the
+// client's seed directly in the NTT domain, a[i][x] = uniform(rand64(seed,
+// ST_SEED_A, i*N + x)) mod q_i, so a server that received only (b, seed)
+// rebuilds it with expand_seeded_a; b = -a*s + e + m.
+void expand_seeded_a(Cipher& c, u64 seed) {
+  Scheme& s = sch();
+  launch_sample_uniform(c.d.p + (size_t)(c.level + 1) * s.N, rows_q(c.level), seed, ST_SEED_A, s.d_mods.p, s.N, s.st);
+}
+std::unique_ptr<Cipher> encrypt_seeded(const Plain& pt, u64 seed) {
+  Scheme& s = sch();
+  REQUIRE(s.has_sk, "secret key not generated");
+  const int l = pt.level, N = s.N;
+  const u64 enc = s.enc_counter++;
+  auto out = new_ct(l, pt.scale); out->logslots = pt.logslots;
+  u64* b = out->d.p;
+  expand_seeded_a(*out, seed);
+  launch_sample_cbd(b, rows_q(l), s.seed, ST_SEED_E(enc), s.d_mods.p, N, false, s.st);
+  ntt(b, 0, 1, rows_q(l), true);
+  DU64 as((size_t)(l + 1) * N);
+  launch_mont_mul(as.p, 0, b + (size_t)(l + 1) * N, 0, s.sR.p, 0, 1, rows_q(l), s.d_mods.p, N, false, s.st);
+  launch_add(b, b, as.p, 0, 1, rows_q(l), s.d_mods.p, N, true, s.st);
+  launch_add(b, b, pt.d.p, 0, 1, rows_q(l), s.d_mods.p, N, false, s.st);
+  sync();
+  return out;
+}
 std::unique_ptr<Plain> decrypt_ct(const Cipher& ct) {
   Scheme& s = sch();
   REQUIRE(s.has_sk, "secret key not generated");
@@ -1467,6 +1495,26 @@ int NewEncryptor(void) { return guard([&] { sch().encryptor = true; return 0; })
 int NewDecryptor(void) { return guard([&] { sch().decryptor = true; return 0; }); }
 int Encrypt(int plaintextID) { return guard([&] { return push_ct(encrypt_pt(get_pt(plaintextID))); }); }
 int Decrypt(int ciphertextID) { return guard([&] { return push_pt(decrypt_ct(get_ct(ciphertextID))); }); }
+int EncryptSeeded(int plaintextID, unsigned long long seed) {
+  return guard([&] { return push_ct(encrypt_seeded(get_pt(plaintextID), (u64)seed)); });
+}
+int DropAx(int ciphertextID) {
+  return guard([&] {
+    Scheme& s = sch(); Cipher& c = get_ct(ciphertextID);
+    HCHECK(hipMemsetAsync(c.d.p + (size_t)(c.level + 1) * s.N, 0, (size_t)(c.level + 1) * s.N * 8, s.st));
+    sync();
+    return 0;
+  });
+}
+int ExpandSeededAx(int ciphertextID, unsigned long long seed) {
+  return guard([&] { expand_seeded_a(get_ct(ciphertextID), (u64)seed); sync(); return 0; });
+}
+double GetCiphertextBytes(int ciphertextID) {
+  double v = -1; guard([&] { const Cipher& c = get_ct(ciphertextID); v = 2.0 * (c.level + 1) * sch().N * 8; return 0; }); return v;
+}
+double GetCiphertextBxBytes(int ciphertextID) {
+  double v = -1; guard([&] { const Cipher& c = get_ct(ciphertextID); v = 1.0 * (c.level + 1) * sch().N * 8; return 0; }); return v;
+}
 int SetEncryptionCounter(uint64_t v) { return guard([&] { sch().enc_counter = v; return 0; }); }
 
 // ---- evaluator ----

@@ -79,6 +79,26 @@ class LinearWorkload:
         self.matrix = None
         self.input = None
         self.expected = None
+        self.upload_seed = None
+
+    def use_seeded_upload(self, seed):
+        """Seeded selector upload (bench_sweep.py:381-403): the input is
+        encrypted with `a` expanded from `seed`, `a` is dropped (only b and the
+        seed cross the wire) and every run() rebuilds it on the device first."""
+        pt = self.scheme.encode(self.input, self.layer.level)
+        cid = self.backend.EncryptSeeded(pt.ids[0], seed)
+        self.backend.DropAx(cid)
+        for i in pt.ids:
+            self.backend.DeletePlaintext(i)
+        self.ct_in.free()
+        self.ct_in = oh.CipherTensor(self.scheme, [cid], pt.n)
+        self.upload_seed = seed
+        return self
+
+    def expand_upload(self):
+        if self.upload_seed is not None:
+            for cid in self.ct_in.ids:
+                self.backend.ExpandSeededAx(cid, self.upload_seed)
 
     def setup(self):
         self.scheme = oh.Scheme(self.params, self.backend)
@@ -91,6 +111,7 @@ class LinearWorkload:
 
     def run(self):
         """One forward of the layer. Returns the output CipherTensor."""
+        self.expand_upload()
         return self.layer.forward(self.ct_in)
 
     def decrypt_output(self, out):
@@ -166,6 +187,7 @@ class SparseToTopWorkload(PCMMWorkload):
         return self
 
     def run(self):
+        self.expand_upload()
         emb = self.layer.forward(self.ct_in)
         out = self.repack.forward(emb)
         emb.free()
@@ -272,6 +294,20 @@ class DLRMWorkload:
         self.scheme = None
         self.modules = {}
         self.ct_dense = self.ct_sparse = None
+        self.upload_seed = None
+
+    def use_seeded_upload(self, seed):
+        """The selector uploaded as (b, seed) at the input level
+        (bench_sweep.py:381-403); every forward rebuilds `a` on the device."""
+        pt = self.scheme.encode(self.emb.selector, self.input_level)
+        cid = self.backend.EncryptSeeded(pt.ids[0], seed)
+        self.backend.DropAx(cid)
+        for i in pt.ids:
+            self.backend.DeletePlaintext(i)
+        self.ct_sparse.free()
+        self.ct_sparse = oh.CipherTensor(self.scheme, [cid], pt.n)
+        self.upload_seed = seed
+        return self
 
     # ---- cleartext model (float64 on the fp32 weights) ----
     def act(self, x):
@@ -340,6 +376,9 @@ class DLRMWorkload:
         output ciphertext tensor (the caller frees them)."""
         m = self.modules
         kept = {}
+        if self.upload_seed is not None:
+            for cid in self.ct_sparse.ids:
+                self.backend.ExpandSeededAx(cid, self.upload_seed)
 
         def step(name, x, free_in):
             y = m[name].forward(x)
@@ -382,6 +421,9 @@ class DLRMWorkload:
         {stage: seconds})."""
         times = {}
         m = self.modules
+        if self.upload_seed is not None:
+            for cid in self.ct_sparse.ids:
+                self.backend.ExpandSeededAx(cid, self.upload_seed)
 
         def step(name, x, free_in):
             sync()

@@ -68,6 +68,15 @@ int NewDecryptor(void);              /* encryptor.go:14 */
 int Encrypt(int plaintextID);        /* encryptor.go:19-27 */
 int Decrypt(int ciphertextID);       /* encryptor.go:29-38 */
 int SetEncryptionCounter(uint64_t v); /* [ext] index of the next encryption's randomness */
+/* Seeded ("compressed") upload of the Cheddar bindings: secret-key encryption
+ * whose `a` is expanded from `seed` on the device (a[i][x] = uniform draw
+ * rand64(seed, i*N + x) mod q_i in the NTT domain), so only b and the seed
+ * cross the wire; DropAx zeroes a, ExpandSeededAx rebuilds it in place. */
+int EncryptSeeded(int plaintextID, unsigned long long seed);   /* cheddar_pybind.cu:638-647 */
+int DropAx(int ciphertextID);                                  /* cheddar_pybind.cu:650-655 (returns 0) */
+int ExpandSeededAx(int ciphertextID, unsigned long long seed); /* cheddar_pybind.cu:657-660 (returns 0) */
+double GetCiphertextBytes(int ciphertextID);                   /* cheddar_pybind.cu:666-673 */
+double GetCiphertextBxBytes(int ciphertextID);                 /* cheddar_pybind.cu:676-679 */
 
 /* ---- evaluator ---------------------------------------------------------------- */
 int NewEvaluator(void);                   /* evaluator.go:13-35 (+ power-of-two and conjugation keys) */

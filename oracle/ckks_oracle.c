@@ -210,6 +210,8 @@ uint64_t orc_rand64(uint64_t seed, uint64_t stream, uint64_t ctr) {
 #define ST_ENC_E1(e) ((8ULL << 56) | (u64)(e))
 #define ST_RLK_A(d) ((9ULL << 56) | (u64)(d))
 #define ST_RLK_E(d) ((10ULL << 56) | (u64)(d))
+#define ST_SEED_A (11ULL << 56)
+#define ST_SEED_E(e) ((12ULL << 56) | (u64)(e))
 
 static inline u64 uniform_mod(u64 r, u64 q) { return (u64)(((u128)r * q) >> 64); }
 /* centred binomial, eta = 21 per side: sigma = sqrt(21/2) ~ 3.24 */
@@ -836,6 +838,29 @@ void orc_encrypt(const orc_ctx* c, const uint64_t* pt, int l, uint64_t enc, uint
     ntt_limbs(c, c0, ql, l + 1); ntt_limbs(c, c1, ql, l + 1);
     for (int i = 0; i <= l; i++) for (int x = 0; x < N; x++) { size_t o = (size_t)i * N + x; c0[o] = addmod(c0[o], pt[o], c->mod[i]); }
     free(u); free(uq); free(t0); free(t1); free(e); free(ep);
+}
+/* Seeded (secret-key) encryption, the compressed upload of the Cheddar
+ * bindings (orion/backend/cheddar/ext/cheddar_pybind.cu:627-660): a is
+ * expanded from the client's seed in the NTT domain, a[i][x] =
+ * uniform(rand64(seed, ST_SEED_A, i*N + x)) mod q_i, so a server holding
+ * only (b, seed) rebuilds it; b = -a*s + e + m with e CBD from the scheme
+ * seed and encryption index. */
+void orc_expand_seeded_a(const orc_ctx* c, int l, uint64_t seed, uint64_t* a) {
+    int N = c->N;
+    for (int i = 0; i <= l; i++) for (int x = 0; x < N; x++)
+        a[(size_t)i * N + x] = uniform_mod(orc_rand64(seed, ST_SEED_A, (u64)i * N + x), c->mod[i]);
+}
+void orc_encrypt_seeded(const orc_ctx* c, const uint64_t* pt, int l, uint64_t seed, uint64_t enc, uint64_t* ct) {
+    int N = c->N; int ql[MAXMOD]; q_list(c, l, ql);
+    u64* b = ct; u64* a = ct + (size_t)(l + 1) * N;
+    orc_expand_seeded_a(c, l, seed, a);
+    i64* e = (i64*)xmalloc(sizeof(i64) * N);
+    sample_cbd(c->seed, ST_SEED_E(enc), N, e); poly_from_signed(c, e, ql, l + 1, b); ntt_limbs(c, b, ql, l + 1);
+    for (int i = 0; i <= l; i++) for (int x = 0; x < N; x++) {
+        size_t o = (size_t)i * N + x; u64 q = c->mod[i];
+        b[o] = addmod(submod(b[o], mulmod_b(&c->bar[i], a[o], c->s_ntt[o]), q), pt[o], q);
+    }
+    free(e);
 }
 void orc_decrypt(const orc_ctx* c, const uint64_t* ct, int l, uint64_t* pt) {
     int N = c->N; const u64* c0 = ct; const u64* c1 = ct + (size_t)(l + 1) * N;

@@ -79,6 +79,8 @@ void orc_decode_f64(const orc_ctx* c, const uint64_t* pt, int level,
 /* ---- encryptor --------------------------------------------------------- */
 void orc_encrypt(const orc_ctx* c, const uint64_t* pt, int level,
                  uint64_t enc_index, uint64_t* ct);
+void orc_expand_seeded_a(const orc_ctx* c, int l, uint64_t seed, uint64_t* a);
+void orc_encrypt_seeded(const orc_ctx* c, const uint64_t* pt, int l, uint64_t seed, uint64_t enc, uint64_t* ct);
 void orc_decrypt(const orc_ctx* c, const uint64_t* ct, int level, uint64_t* pt);
 
 /* ---- plaintext / scalar / ciphertext products ----------------------------- */

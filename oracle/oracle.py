@@ -61,6 +61,8 @@ def lib():
             "orc_decode_f64": ([vp, u64p, ctypes.c_int, ctypes.c_double, dp], None),
             "orc_encrypt": ([vp, u64p, ctypes.c_int, ctypes.c_uint64, u64p], None),
             "orc_decrypt": ([vp, u64p, ctypes.c_int, u64p], None),
+            "orc_expand_seeded_a": ([vp, ctypes.c_int, ctypes.c_uint64, u64p], None),
+            "orc_encrypt_seeded": ([vp, u64p, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64, u64p], None),
             "orc_add": ([vp, u64p, u64p, ctypes.c_int, ctypes.c_int, u64p], None),
             "orc_rescale": ([vp, u64p, ctypes.c_int, u64p], None),
             "orc_rotate": ([vp, u64p, ctypes.c_int, ctypes.c_int, u64p], None),
@@ -240,6 +242,18 @@ class Oracle:
         ct = np.zeros((2, level + 1, self.N), dtype=np.uint64)
         lib().orc_encrypt(self.ctx, _p(pt), level, int(enc_index), _p(ct))
         return ct
+
+    def encrypt_seeded(self, pt, level, seed, enc_index):
+        """Secret-key encryption whose `a` part is expanded from `seed`."""
+        pt = np.ascontiguousarray(pt, dtype=np.uint64)
+        ct = np.zeros((2, level + 1, self.N), dtype=np.uint64)
+        lib().orc_encrypt_seeded(self.ctx, _p(pt), level, int(seed), int(enc_index), _p(ct))
+        return ct
+
+    def expand_seeded_a(self, level, seed):
+        a = np.zeros((level + 1, self.N), dtype=np.uint64)
+        lib().orc_expand_seeded_a(self.ctx, level, int(seed), _p(a))
+        return a
 
     def decrypt(self, ct, level):
         ct = np.ascontiguousarray(ct, dtype=np.uint64)

@@ -106,6 +106,33 @@ def test_encode_edge_cases(ctx):
     ctx.lib.DeletePlaintext(pt)
 
 
+def test_encrypt_seeded(ctx):
+    """EncryptSeeded / DropAx / ExpandSeededAx (the compressed upload of
+    cheddar_pybind.cu:627-660) bit-exact with the restatement: b and the
+    seed's `a`; DropAx leaves b and zeroes a; ExpandSeededAx rebuilds a word
+    for word; the byte counts are those of the polynomials."""
+    for level in (ctx.L - 1, 1):
+        vals = ctx.rng.uniform(-1, 1, ctx.slots).astype(np.float32)
+        scale = 1 << ctx.logscale
+        pt = ctx.lib.Encode(vals.tolist(), level, scale)
+        ctx.lib.SetEncryptionCounter(7)
+        ct = ctx.lib.EncryptSeeded(pt, 0x5EED + level)
+        want = ctx.orc.encrypt_seeded(ctx.orc.encode(vals, level, float(scale)), level, 0x5EED + level, 7)
+        assert_equal_u64(ctx.lib.export_ciphertext(ct), want, f"EncryptSeeded level {level}")
+        assert ctx.lib.GetCiphertextBytes(ct) == 2 * (level + 1) * ctx.N * 8
+        assert ctx.lib.GetCiphertextBxBytes(ct) == (level + 1) * ctx.N * 8
+        assert ctx.lib.DropAx(ct) == 0
+        got = ctx.lib.export_ciphertext(ct)
+        assert_equal_u64(got[0], want[0], "b after DropAx")
+        assert not np.any(got[1])
+        assert ctx.lib.ExpandSeededAx(ct, 0x5EED + level) == 0
+        assert_equal_u64(ctx.lib.export_ciphertext(ct), want, "ExpandSeededAx")
+        dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(ct)))
+        assert np.abs(dec - vals).max() < 1e-3
+        ctx.lib.DeleteCiphertext(ct)
+        ctx.lib.DeletePlaintext(pt)
+
+
 def test_encrypt_decrypt(ctx):
     level = ctx.L - 1
     ct, ref, vals = ctx.fresh_ct(level, 3)

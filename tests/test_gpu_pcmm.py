@@ -44,6 +44,37 @@ def test_pcmm_bitexact_vs_oracle(hip_lib, name):
     hip_lib.DeleteScheme()
 
 
+def test_pcmm_seeded_upload(hip_lib):
+    """bench_sweep.py:381-399 seeded upload: the selector is encrypted with a
+    seeded `a`, `a` is dropped (only b crossed the wire) and rebuilt on the
+    device before the PCMM; the output is bit-exact with the restatement's
+    PCMM of the restatement's seeded ciphertext."""
+    name = "pcmm26_n13"
+    w = PCMMWorkload(hip_lib, name, seed=4, key_seed=17).setup()
+    s = w.scheme
+    pt = s.encode(w.selector, w.layer.level)
+    hip_lib.SetEncryptionCounter(3)
+    cid = hip_lib.EncryptSeeded(pt.ids[0], 0xC0FFEE)
+    hip_lib.DropAx(cid)
+    hip_lib.ExpandSeededAx(cid, 0xC0FFEE)
+    from helrm_amd import orion_host as oh
+    out = w.layer.forward(oh.CipherTensor(s, [cid], pt.n))
+    got = hip_lib.export_ciphertext(out.ids[0])
+    c = w.cfg
+    orc = O.Oracle(c["logn"], hip_lib.GetModuliChain(), hip_lib.GetAuxModuliChain(), h=c["h"], seed=17)
+    try:
+        level, scale = w.layer.level, float(1 << c["logscale"])
+        ct = orc.encrypt_seeded(orc.encode(w.selector, level, scale), level, 0xC0FFEE, 3)
+        want, l, sc = oracle_linear(orc, ct, level, scale, w.layer.diagonals[(0, 0)], w.layer.output_rotations,
+                                    c["logscale"])
+        assert_equal_u64(got, want, f"{name} seeded-upload PCMM output")
+    finally:
+        orc.close()
+    y = w.decrypt_output(out)
+    assert np.abs(y - w.expected).max() < TOL
+    hip_lib.DeleteScheme()
+
+
 def test_pcmm26_full_size_decrypts(hip_lib):
     print("[pcmm] pcmm26 (N=2^16): building", flush=True)
     w = PCMMWorkload(hip_lib, "pcmm26", seed=3, key_seed=17).setup()

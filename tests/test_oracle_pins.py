@@ -264,6 +264,34 @@ def test_encrypt_decrypt_noise(small):
     np.testing.assert_allclose(small.decode_f64(d, level, scale), vals, atol=1e-6)
 
 
+def test_seeded_encryption(small):
+    """Seeded secret-key encryption: b + a*s - m is a small error (exactly, by
+    CRT), `a` is the seed's expansion alone -- the same for any message,
+    encryption index and level (a server expands it at the ciphertext's own
+    level), different for another seed -- and its words spread over [0, q)."""
+    level = small.L - 1
+    rng = np.random.default_rng(23)
+    vals = rng.uniform(-1, 1, small.slots).astype(np.float32)
+    scale = 2.0 ** 30
+    pt = small.encode(vals, level, scale)
+    ct = small.encrypt_seeded(pt, level, 0x5EED, 4)
+    d = small.decrypt(ct, level)
+    diff = [(_crt(small.to_coeff(d, level)[:, x], small.q[:level + 1]) - _crt(small.to_coeff(pt, level)[:, x], small.q[:level + 1])) for x in range(small.N)]
+    Q = math.prod(small.q[:level + 1])
+    diff = [v - Q if v > Q // 2 else v for v in (dv % Q for dv in diff)]
+    assert 0 < max(abs(v) for v in diff) < 64
+    a = ct[1]
+    np.testing.assert_array_equal(a, small.expand_seeded_a(level, 0x5EED))
+    other = small.encrypt_seeded(small.encode(-vals, level, scale), level, 0x5EED, 9)
+    np.testing.assert_array_equal(other[1], a)
+    np.testing.assert_array_equal(small.expand_seeded_a(1, 0x5EED), a[:2])
+    assert not np.array_equal(small.expand_seeded_a(level, 0x5EEE), a)
+    for i in range(level + 1):
+        q = small.q[i]
+        assert a[i].max() < q and a[i].mean() / q == pytest.approx(0.5, abs=0.15)
+    np.testing.assert_allclose(small.decode_f64(d, level, scale), vals, atol=1e-6)
+
+
 def test_galois_key_relation(small):
     """b_d + a_d * s' = e_d + P * s on the digit's limbs (s' = sigma_{g^-1}(s))."""
     g = small.galois_element(1)
