@@ -31,6 +31,10 @@ class ArrayResultUInt64(ctypes.Structure):
     _fields_ = [("Data", ctypes.POINTER(ctypes.c_ulonglong)), ("Length", ctypes.c_ulonglong)]
 
 
+class ArrayResultByte(ctypes.Structure):
+    _fields_ = [("Data", ctypes.POINTER(ctypes.c_char)), ("Length", ctypes.c_ulong)]
+
+
 _ARRAY_TYPES = (ArrayResultInt, ArrayResultFloat, ArrayResultUInt64)
 
 
@@ -57,6 +61,18 @@ class HipFunction:
             else:
                 c_args.append(c_arg)
         res = self.func(*c_args)
+        if isinstance(res, ArrayResultByte):
+            # as LattigoFunction (bindings.py:86-94): (bytes as uint8, pointer); the caller frees
+            # the pointer with FreeCArray, the returned array is a copy and stays valid
+            if not res.Data:
+                if self.checked and HipFunction.lib is not None:
+                    msg = HipFunction.lib.GetLastError().decode()
+                    if msg:
+                        raise HipError(msg)
+                return np.zeros(0, dtype=np.uint8), res.Data
+            n = int(res.Length)
+            buf = ctypes.cast(res.Data, ctypes.POINTER(ctypes.c_ubyte * n)).contents
+            return np.frombuffer(buf, dtype=np.uint8).copy(), res.Data
         if isinstance(res, _ARRAY_TYPES):
             if not res.Data:
                 if self.checked and HipFunction.lib is not None:
@@ -87,6 +103,10 @@ class HipFunction:
             return ctypes.c_float(arg)
         if isinstance(arg, str):
             return arg.encode("utf-8")
+        if typ == ctypes.POINTER(ctypes.c_ubyte) and isinstance(arg, (bytes, bytearray, np.ndarray)):
+            a = np.ascontiguousarray(np.frombuffer(bytes(arg), dtype=np.uint8) if not isinstance(arg, np.ndarray)
+                                     else arg.reshape(-1).view(np.uint8))
+            return (a.ctypes.data_as(typ), len(a))
         if isinstance(arg, np.ndarray):
             if typ == ctypes.POINTER(ctypes.c_float):
                 a = np.ascontiguousarray(arg, dtype=np.float32)
@@ -111,6 +131,7 @@ _I = _c.c_int
 _PI = _c.POINTER(_c.c_int)
 _PF = _c.POINTER(_c.c_float)
 _PU64 = _c.POINTER(_c.c_uint64)
+_PB = _c.POINTER(_c.c_ubyte)
 
 # name -> (argtypes, restype); argtypes follow orion/backend/lattigo/bindings.py
 _SIGNATURES = {
@@ -137,6 +158,13 @@ _SIGNATURES = {
     "NewDecryptor": ([], _I),
     "Encrypt": ([_I], _I),
     "Decrypt": ([_I], _I),
+    "SerializeSecretKey": ([], ArrayResultByte),
+    "LoadSecretKey": ([_PB, _c.c_ulong], _I),
+    "GenerateAndSerializeRotationKey": ([_I], ArrayResultByte),
+    "LoadRotationKey": ([_PB, _c.c_ulong, _c.c_ulong], _I),
+    "SerializeDiagonal": ([_I, _I], ArrayResultByte),
+    "LoadPlaintextDiagonal": ([_PB, _c.c_ulong, _I, _c.c_ulong], _I),
+    "RemovePlaintextDiagonals": ([_I], _I),
     "EncryptSeeded": ([_I, _c.c_ulonglong], _I),
     "DropAx": ([_I], _I),
     "ExpandSeededAx": ([_I, _c.c_ulonglong], _I),

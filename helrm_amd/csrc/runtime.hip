@@ -234,6 +234,7 @@ struct LinTrans {
   std::vector<std::vector<int>> baby;    // sorted babies per group
   std::vector<int> plain_idx;            // diagonal index of each stored plaintext
   DU64 diags;                            // [np][level+1+K][N], Montgomery form
+  std::vector<char> resident;            // per stored plaintext: loaded (SerializeDiagonal / Remove drop it)
   DevArray<int> d_gpi, d_bzero, d_bslot;  // [ng][nbaby] plaintext index (absent: the zero plaintext); per-baby flags
   bool dense = false;                     // every giant group holds every baby step
   double scale = 0;
@@ -563,6 +564,8 @@ void ensure_galois_key(u64 galel) {
   launch_mont_convert(soR.p, 0, 1, rows_all(), s.d_mods.p, N, true, s.st);
   s.gkeys[galel] = gen_eval_key(s.sR.p, soR.p, [galel](int d) { return ST_GK_A(galel, (u64)d); },
                                  [galel](int d) { return ST_GK_E(galel, (u64)d); });
+  // transforms cache key addresses: a key created after a removal lives elsewhere
+  for (auto& kv : s.lts) kv.second->ptrs_ready = false;
 }
 // Relinearization key: s^2 -> s (Lattigo GenRelinearizationKey), same
 // generator as the oracle's, random streams ST_RLK_A/E(d).
@@ -1101,11 +1104,11 @@ std::vector<int> lt_rotations(const LinTrans& t) {
   return out;
 }
 
-int generate_lt(const int* idx, int nidx, const float* data, int ndata, int level, float ratio) {
+int generate_lt(const int* idx, int nidx, const float* data, int ndata, int level, float ratio, bool load_mode) {
   Scheme& s = sch();
   const int N = s.N, slots = N / 2, K = s.K;
   REQUIRE(nidx > 0, "no diagonals");
-  REQUIRE(ndata == nidx * slots, "diagonal data length must be len(diag_idxs) * slots");
+  REQUIRE(ndata == nidx * slots || (load_mode && ndata == 0), "diagonal data length must be len(diag_idxs) * slots");
   REQUIRE(level >= 0 && level < s.L, "invalid level");
   auto t = std::make_unique<LinTrans>();
   t->level = level; t->slots = slots;
@@ -1136,16 +1139,22 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
       for (int b : t->baby[g]) { int di = t->giant[g] + b; order.push_back({di, src_of(di)}); rotv.push_back((-t->giant[g]) & (slots - 1)); }
   }
   const int np = (int)order.size(), nqp_lt = level + 1 + K;
-  // one extra all-zero plaintext after the np diagonals: absent (group, baby) pairs point at it
-  t->diags = DU64((size_t)(np + 1) * nqp_lt * N);
-  HCHECK(hipMemsetAsync(t->diags.p + (size_t)np * nqp_lt * N, 0, (size_t)nqp_lt * N * 8, s.st));
-  RowMap rm{nqp_lt, level + 1, 0, s.L, 0, 0};
-  // special FFT, fixed point, residues in QP and NTT on the device, then the Montgomery conversion
-  std::vector<EncodeSrc> src(np);
-  for (int p = 0; p < np; p++) src[p] = EncodeSrc{order[p].second, rotv[p]};
-  encode_device(data, (size_t)ndata, src, slots, t->scale, rm, t->diags.p, (size_t)nqp_lt * N);
-  launch_mont_convert(t->diags.p, (size_t)nqp_lt * N, np, rm, s.d_mods.p, N, true, s.st);
   for (auto& o : order) t->plain_idx.push_back(o.first);
+  if (load_mode) {
+    // io_mode "load" (lineartransform.go:75-84): empty diagonal slots, filled by LoadPlaintextDiagonal
+    t->resident.assign(np, 0);
+  } else {
+    // one extra all-zero plaintext after the np diagonals: absent (group, baby) pairs point at it
+    t->diags = DU64((size_t)(np + 1) * nqp_lt * N);
+    HCHECK(hipMemsetAsync(t->diags.p + (size_t)np * nqp_lt * N, 0, (size_t)nqp_lt * N * 8, s.st));
+    RowMap rm{nqp_lt, level + 1, 0, s.L, 0, 0};
+    // special FFT, fixed point, residues in QP and NTT on the device, then the Montgomery conversion
+    std::vector<EncodeSrc> src(np);
+    for (int p = 0; p < np; p++) src[p] = EncodeSrc{order[p].second, rotv[p]};
+    encode_device(data, (size_t)ndata, src, slots, t->scale, rm, t->diags.p, (size_t)nqp_lt * N);
+    launch_mont_convert(t->diags.p, (size_t)nqp_lt * N, np, rm, s.d_mods.p, N, true, s.st);
+    t->resident.assign(np, 1);
+  }
   if (!t->naive) {
     const int ng = (int)t->giant.size(), nb = (int)t->rot2.size();
     std::vector<int> gpi((size_t)ng * nb, np), bzero(nb, 0), bslot(nb, 0);
@@ -1411,6 +1420,78 @@ template <class T> T* c_array(const std::vector<T>& v) {
 }
 unsigned long scale_to_ulong(double sc) { if (!(sc < 18446744073709551616.0)) return ~0UL; return sc < 0 ? 0UL : (unsigned long)sc; }
 
+// ---- binary wire format --------------------------------------------------------
+// The layout of Lattigo v6's WriteTo for the objects Orion serializes
+// (keygenerator.go:38-58, lineartransform.go:130-193), little-endian u64 words:
+//   ring.Poly    rows, then per row: N, N coefficients
+//   ringqp.Poly  ring.Poly over Q, then ring.Poly over P
+//   SecretKey    ringqp.Poly over the whole QP basis
+//   GaloisKey    galois element, NthRoot (2N), base-two decomposition (0),
+//                dnum, then per digit: 1, 2, (b, a) as ringqp.Poly
+//   diagonal     ringqp.Poly at the transform's level
+// Everything stays in the NTT domain and in Montgomery form (x * 2^64 mod q).
+struct Wire {
+  std::vector<uint8_t> b;
+  void u64v(u64 x) { for (int i = 0; i < 8; i++) b.push_back((uint8_t)(x >> (8 * i))); }
+  void words(const u64* p, size_t n) {
+    size_t o = b.size(); b.resize(o + 8 * n);
+    for (size_t i = 0; i < n; i++) for (int k = 0; k < 8; k++) b[o + 8 * i + k] = (uint8_t)(p[i] >> (8 * k));
+  }
+  void poly(const u64* rows, int nrows, int N) { u64v((u64)nrows); for (int r = 0; r < nrows; r++) { u64v((u64)N); words(rows + (size_t)r * N, N); } }
+  void qp(const u64* rows, int nq, int K, int N) { poly(rows, nq, N); poly(rows + (size_t)nq * N, K, N); }
+};
+struct WireIn {
+  const uint8_t* p; size_t n, off = 0;
+  u64 u64v() {
+    REQUIRE(off + 8 <= n, "serialized data truncated");
+    u64 x = 0; for (int i = 0; i < 8; i++) x |= (u64)p[off + i] << (8 * i);
+    off += 8; return x;
+  }
+  void words(u64* out, size_t cnt) {
+    REQUIRE(off + 8 * cnt <= n, "serialized data truncated");
+    for (size_t i = 0; i < cnt; i++) { u64 x = 0; for (int k = 0; k < 8; k++) x |= (u64)p[off + 8 * i + k] << (8 * k); out[i] = x; }
+    off += 8 * cnt;
+  }
+  void poly(u64* rows, int nrows, int N, const std::vector<u64>& mods, int m0) {
+    REQUIRE(u64v() == (u64)nrows, "serialized polynomial has the wrong number of limbs");
+    for (int r = 0; r < nrows; r++) {
+      REQUIRE(u64v() == (u64)N, "serialized polynomial has the wrong ring degree");
+      u64* row = rows + (size_t)r * N; words(row, N);
+      for (int x = 0; x < N; x++) REQUIRE(row[x] < mods[m0 + r], "serialized coefficient not reduced");
+    }
+  }
+  void qp(u64* rows, int nq, int K, int N, const std::vector<u64>& mods, int Lfull) {
+    poly(rows, nq, N, mods, 0);
+    poly(rows + (size_t)nq * N, K, N, mods, Lfull);
+  }
+  void end() { REQUIRE(off == n, "trailing bytes after the serialized object"); }
+};
+// the moduli of a QP polynomial at level l are q_0..q_l then p_0..p_{K-1}
+std::vector<u64> qp_mods(int l) {
+  Scheme& s = sch();
+  std::vector<u64> m(s.mod.begin(), s.mod.begin() + l + 1);
+  m.insert(m.end(), s.mod.begin() + s.L, s.mod.end());
+  return m;
+}
+ArrayResultByte bytes_result(const std::vector<uint8_t>& v) {
+  ArrayResultByte r;
+  r.Data = (char*)c_array(v); r.Length = v.size();
+  return r;
+}
+std::vector<uint8_t> serialize_galois_key(u64 galel, const DU64& key) {
+  Scheme& s = sch();
+  const int N = s.N, nm = s.L + s.K;
+  std::vector<u64> h((size_t)s.dnum * 2 * nm * N);
+  download(h.data(), key.p, h.size());
+  Wire w;
+  w.u64v(galel); w.u64v(2 * (u64)N); w.u64v(0); w.u64v((u64)s.dnum);
+  for (int d = 0; d < s.dnum; d++) {
+    w.u64v(1); w.u64v(2);
+    for (int p = 0; p < 2; p++) w.qp(h.data() + ((size_t)d * 2 + p) * nm * N, s.L, s.K, N);
+  }
+  return w.b;
+}
+
 }  // namespace
 
 // ============================================================================
@@ -1634,14 +1715,17 @@ int NewLinearTransformEvaluator(void) { return guard([&] { sch().lteval = true; 
 int GenerateLinearTransform(const int* diagIdxs, int diagIdxsLen, const float* diagData, int diagDataLen, int level,
                             float bsgsRatio, const char* ioMode) {
   return guard([&] {
-    REQUIRE(!ioMode || std::string(ioMode) == "none", "only io_mode 'none' is supported by the hip backend");
-    return generate_lt(diagIdxs, diagIdxsLen, diagData, diagDataLen, level, bsgsRatio);
+    const std::string mode = ioMode ? ioMode : "none";
+    REQUIRE(mode == "none" || mode == "save" || mode == "load", "io_mode must be 'none', 'save' or 'load'");
+    return generate_lt(diagIdxs, diagIdxsLen, diagData, diagDataLen, level, bsgsRatio, mode == "load");
   });
 }
 int EvaluateLinearTransform(int transformID, int ctxtID) {
   return guard([&] {
     LinTrans& t = get_lt(transformID);
     Cipher& c = get_ct(ctxtID);
+    REQUIRE(std::all_of(t.resident.begin(), t.resident.end(), [](char r) { return r != 0; }),
+            "plaintext diagonals not loaded (LoadPlaintextDiagonal)");
     auto out = t.naive ? eval_lt_naive(t, c) : eval_lt_bsgs(t, c);
     return push_ct(std::move(out));
   });
@@ -1662,7 +1746,157 @@ int GenerateLinearTransformRotationKey(int galEl) {
 int DeleteLinearTransform(int id) {
   return guard([&] { Scheme& s = sch(); sync(); if (s.lts.erase(id)) s.lt_ids.give(id); return 0; });
 }
-int RemoveRotationKeys(void) { return guard([&] { sch().lt_keys.clear(); return 0; }); }
+int RemoveRotationKeys(void) {
+  return guard([&] {
+    // the transforms lose their keys; keys that Rotate also uses stay (lineartransform.go:203-211)
+    Scheme& s = sch();
+    sync();
+    for (u64 g : s.lt_keys) if (!s.rot_keys.count(g)) s.gkeys.erase(g);
+    s.lt_keys.clear();
+    for (auto& kv : s.lts) kv.second->ptrs_ready = false;
+    return 0;
+  });
+}
+
+// ---- serialization (io_mode save / load) ----
+ArrayResultByte SerializeSecretKey(void) {
+  ArrayResultByte r{nullptr, 0};
+  guard([&] {
+    Scheme& s = sch();
+    REQUIRE(s.has_sk, "secret key not generated");
+    std::vector<u64> h((size_t)(s.L + s.K) * s.N);
+    download(h.data(), s.sR.p, h.size());
+    Wire w; w.qp(h.data(), s.L, s.K, s.N);
+    r = bytes_result(w.b);
+    return 0;
+  });
+  return r;
+}
+int LoadSecretKey(const unsigned char* data, unsigned long len) {
+  return guard([&] {
+    Scheme& s = sch();
+    const int N = s.N, nm = s.L + s.K;
+    REQUIRE(data, "no data");
+    std::vector<u64> h((size_t)nm * N);
+    WireIn in{data, (size_t)len};
+    in.qp(h.data(), s.L, s.K, N, s.mod, s.L);
+    in.end();
+    DU64 sR((size_t)nm * N); upload(sR.p, h.data(), h.size());
+    // the ternary coefficients (for Galois keys) from limb q_0: out of Montgomery form, inverse NTT, centred
+    DU64 c0((size_t)N); d2d(c0.p, sR.p, (size_t)N * 8);
+    launch_mont_convert(c0.p, 0, 1, rows_q(0), s.d_mods.p, N, false, s.st);
+    ntt(c0.p, 0, 1, rows_q(0), false);
+    std::vector<u64> coef(N); download(coef.data(), c0.p, N);
+    std::vector<int8_t> sv(N);
+    const u64 q0 = s.mod[0];
+    for (int x = 0; x < N; x++) {
+      const u64 v = coef[x];
+      REQUIRE(v <= 1 || v == q0 - 1, "secret key coefficients must be ternary");
+      sv[x] = v == 0 ? 0 : (v == 1 ? 1 : -1);
+    }
+    sync();
+    s.s = sv; s.sR = std::move(sR); s.has_sk = true;
+    // keys derived from a previous secret are stale
+    s.gkeys.clear(); s.rlk.reset();
+    for (auto& kv : s.lts) kv.second->ptrs_ready = false;
+    return 0;
+  });
+}
+ArrayResultByte GenerateAndSerializeRotationKey(int galEl) {
+  ArrayResultByte r{nullptr, 0};
+  guard([&] {
+    Scheme& s = sch();
+    const u64 g = (u64)(unsigned)galEl;
+    const bool had = s.gkeys.count(g) != 0;
+    ensure_galois_key(g);
+    r = bytes_result(serialize_galois_key(g, *s.gkeys.at(g)));
+    if (!had) s.gkeys.erase(g);  // the reference returns the key without keeping it
+    return 0;
+  });
+  return r;
+}
+int LoadRotationKey(const unsigned char* data, unsigned long len, unsigned long galEl) {
+  return guard([&] {
+    Scheme& s = sch();
+    const int N = s.N, nm = s.L + s.K;
+    REQUIRE(data, "no data");
+    WireIn in{data, (size_t)len};
+    REQUIRE(in.u64v() == (u64)galEl, "serialized key is for another Galois element");
+    REQUIRE(in.u64v() == 2 * (u64)N, "serialized key is for another ring degree");
+    REQUIRE(in.u64v() == 0, "base-two decomposition is not supported");
+    REQUIRE(in.u64v() == (u64)s.dnum, "serialized key has another number of digits");
+    std::vector<u64> h((size_t)s.dnum * 2 * nm * N);
+    for (int d = 0; d < s.dnum; d++) {
+      REQUIRE(in.u64v() == 1 && in.u64v() == 2, "malformed gadget ciphertext");
+      for (int p = 0; p < 2; p++) in.qp(h.data() + ((size_t)d * 2 + p) * nm * N, s.L, s.K, N, s.mod, s.L);
+    }
+    in.end();
+    auto k = std::make_unique<DU64>(h.size());
+    upload(k->p, h.data(), h.size());
+    s.gkeys[(u64)galEl] = std::move(k);
+    s.lt_keys.insert((u64)galEl);
+    // transforms cache key pointers: rebuild them on next use
+    for (auto& kv : s.lts) kv.second->ptrs_ready = false;
+    return 0;
+  });
+}
+ArrayResultByte SerializeDiagonal(int transformID, int diagIdx) {
+  ArrayResultByte r{nullptr, 0};
+  guard([&] {
+    Scheme& s = sch();
+    LinTrans& t = get_lt(transformID);
+    const int N = s.N, nqp = t.level + 1 + s.K;
+    const int d = ((diagIdx % t.slots) + t.slots) % t.slots;
+    auto it = std::find(t.plain_idx.begin(), t.plain_idx.end(), d);
+    REQUIRE(it != t.plain_idx.end(), "diagonal not in the transform");
+    const size_t p = it - t.plain_idx.begin();
+    REQUIRE(t.resident[p], "diagonal not loaded");
+    std::vector<u64> h((size_t)nqp * N);
+    download(h.data(), t.diags.p + p * nqp * N, h.size());
+    Wire w; w.qp(h.data(), t.level + 1, s.K, N);
+    r = bytes_result(w.b);
+    // as the reference, the serialized diagonal leaves the transform
+    t.resident[p] = 0;
+    if (std::none_of(t.resident.begin(), t.resident.end(), [](char x) { return x != 0; })) t.diags.reset();
+    return 0;
+  });
+  return r;
+}
+int LoadPlaintextDiagonal(const unsigned char* data, unsigned long len, int transformID, unsigned long diagIdx) {
+  return guard([&] {
+    Scheme& s = sch();
+    LinTrans& t = get_lt(transformID);
+    const int N = s.N, nqp = t.level + 1 + s.K, np = (int)t.plain_idx.size();
+    REQUIRE(data, "no data");
+    const int d = (int)(diagIdx % (unsigned long)t.slots);
+    auto it = std::find(t.plain_idx.begin(), t.plain_idx.end(), d);
+    REQUIRE(it != t.plain_idx.end(), "diagonal not in the transform");
+    const size_t p = it - t.plain_idx.begin();
+    std::vector<u64> h((size_t)nqp * N);
+    WireIn in{data, (size_t)len};
+    std::vector<u64> mods = qp_mods(t.level);
+    in.poly(h.data(), t.level + 1, N, mods, 0);
+    in.poly(h.data() + (size_t)(t.level + 1) * N, s.K, N, mods, t.level + 1);
+    in.end();
+    if (!t.diags.p) {
+      // storage was released with the last diagonal: np plaintexts + the all-zero one
+      t.diags = DU64((size_t)(np + 1) * nqp * N);
+      HCHECK(hipMemsetAsync(t.diags.p + (size_t)np * nqp * N, 0, (size_t)nqp * N * 8, s.st));
+    }
+    upload(t.diags.p + p * nqp * N, h.data(), h.size());
+    t.resident[p] = 1;
+    return 0;
+  });
+}
+int RemovePlaintextDiagonals(int transformID) {
+  return guard([&] {
+    LinTrans& t = get_lt(transformID);
+    sync();
+    std::fill(t.resident.begin(), t.resident.end(), 0);
+    t.diags.reset();
+    return 0;
+  });
+}
 
 // ---- tensors ----
 int DeletePlaintext(int id) { return guard([&] { Scheme& s = sch(); if (s.pts.erase(id)) s.pt_ids.give(id); return 0; }); }

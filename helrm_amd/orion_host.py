@@ -13,6 +13,7 @@ Everything here is host bookkeeping; all ciphertext arithmetic goes through
 the backend object (a HipLibrary, or any object with the Lattigo method set).
 """
 import math
+import os
 
 import numpy as np
 
@@ -23,11 +24,12 @@ import numpy as np
 
 class Params:
     def __init__(self, logn, logq, logp, logscale=None, h=192, ringtype="standard",
-                 embedding_method="hybrid", io_mode="none", seed=None):
+                 embedding_method="hybrid", io_mode="none", seed=None, keys_path="", diags_path=""):
         self.logn, self.logq, self.logp = int(logn), list(logq), list(logp)
         self.logscale = int(logscale or self.logq[-1])
         self.h, self.ringtype = int(h), ringtype.lower()
         self.embedding_method, self.io_mode, self.seed = embedding_method, io_mode, seed
+        self.keys_path, self.diags_path = keys_path, diags_path
 
     @classmethod
     def from_config(cls, cfg, seed=None):
@@ -48,8 +50,8 @@ class Params:
     def get_slots(self): return 1 << (self.logn - 1)
     def get_embedding_method(self): return self.embedding_method
     def get_io_mode(self): return self.io_mode
-    def get_keys_path(self): return ""
-    def get_diags_path(self): return ""
+    def get_keys_path(self): return self.keys_path
+    def get_diags_path(self): return self.diags_path
     def get_seed(self): return self.seed
 
 
@@ -177,17 +179,59 @@ def diagonalize(matrix, num_slots, embed_method="hybrid", is_last_layer=False):
 # scheme, tensors and the linear layer
 # --------------------------------------------------------------------------
 
+class WireStore:
+    """Named byte blobs standing in for the HDF5 files of Orion's io_mode
+    (keys_path: "sk" and one entry per Galois element; diags_path: one entry
+    per layer / block / diagonal, lt_evaluator.py:160-215, 440-497).  With a
+    path the store is a .npz file of uint8 arrays (written on flush, read
+    without pickle); without one it lives in memory."""
+
+    def __init__(self, path=""):
+        self.path = path
+        self.blobs = {}
+        if path and os.path.exists(path):
+            with np.load(path, allow_pickle=False) as z:
+                self.blobs = {k: z[k].copy() for k in z.files}
+
+    def __contains__(self, key):
+        return key in self.blobs
+
+    def __getitem__(self, key):
+        return self.blobs[key]
+
+    def __setitem__(self, key, data):
+        self.blobs[key] = np.asarray(data, dtype=np.uint8).copy()
+
+    def keys(self):
+        return self.blobs.keys()
+
+    def flush(self):
+        if self.path:
+            np.savez(self.path, **self.blobs)
+
+
 class Scheme:
     """Minimal counterpart of orion.core.orion.Scheme for this path: creates
     the backend, keys, encoder/encryptor/evaluator (init_scheme order,
-    orion/core/orion.py:66-126 and orion/backend/python/*)."""
+    orion/core/orion.py:66-126 and orion/backend/python/*).  io_mode "save"
+    serializes the secret key, rotation keys and diagonals into the stores,
+    "load" reads them back instead of generating them
+    (key_generator.py:17-31, lt_evaluator.py)."""
 
     def __init__(self, params, backend):
         self.params = params
         self.backend = backend
+        self.io_mode = params.get_io_mode()
+        self.key_store = WireStore(params.get_keys_path())
+        self.diag_store = WireStore(params.get_diags_path())
         backend.setup_bindings(params)
         backend.NewKeyGenerator()
-        backend.GenerateSecretKey()
+        if self.io_mode != "load":
+            backend.GenerateSecretKey()
+            if self.io_mode == "save":
+                self._store(self.key_store, "sk", backend.SerializeSecretKey())
+        else:
+            backend.LoadSecretKey(self.key_store["sk"])
         backend.GeneratePublicKey()
         backend.GenerateRelinearizationKey()
         backend.GenerateEvaluationKeys()
@@ -198,6 +242,17 @@ class Scheme:
         backend.NewLinearTransformEvaluator()
         backend.NewPolynomialEvaluator()
         self.saved_rotation_keys = set()
+
+    def _store(self, store, key, result):
+        data, ptr = result
+        try:
+            store[key] = data
+        finally:
+            self.backend.FreeCArray(ptr)
+
+    def flush(self):
+        self.key_store.flush()
+        self.diag_store.flush()
 
     # orion/backend/python/encoder.py:14-88 (real values, default path)
     def encode(self, values, level=None, scale=None):
@@ -276,8 +331,14 @@ class LinearLayer:
     """Linear / Embedding (orion/nn/linear.py:143-225, orion/nn/embedding.py:12-21)
     compiled at `level` with the hybrid packing; bias zeros for Embedding."""
 
-    def __init__(self, scheme, weight, bias=None, level=None, bsgs_ratio=2.0, last=False):
+    _count = 0
+
+    def __init__(self, scheme, weight, bias=None, level=None, bsgs_ratio=2.0, last=False, name=None):
         self.scheme = scheme
+        if name is None:
+            name = f"linear{LinearLayer._count}"
+            LinearLayer._count += 1
+        self.name = name
         self.weight = np.asarray(weight, dtype=np.float32)
         self.out_features = self.weight.shape[0]
         self.bias = np.zeros(self.out_features, dtype=np.float32) if bias is None else np.asarray(bias, np.float32)
@@ -299,23 +360,41 @@ class LinearLayer:
     # lt_evaluator.py:29-57
     def generate_transforms(self):
         b = self.scheme.backend
+        mode = self.scheme.io_mode
         ids = {}
         for (row, col), diags in self.diagonals.items():
             idxs = list(diags.keys())
             data = np.concatenate([diags[i] for i in idxs]).astype(np.float32)
-            tid = b.GenerateLinearTransform(idxs, data, self.level, self.bsgs_ratio, "none")
+            tid = b.GenerateLinearTransform(idxs, data, self.level, self.bsgs_ratio, mode)
             ids[(row, col)] = tid
             self.generate_rotation_keys(tid)
+            if mode == "save":
+                # lt_evaluator.py:453-464: each diagonal leaves the transform as bytes
+                for d in idxs:
+                    self.scheme._store(self.scheme.diag_store, f"{self.name}/{row}_{col}/{d}", b.SerializeDiagonal(tid, d))
         return ids
 
-    # lt_evaluator.py:132-146
+    # lt_evaluator.py:132-161
     def generate_rotation_keys(self, tid):
         b = self.scheme.backend
         keys = b.GetLinearTransformRotationKeys(tid)
         new = set(keys).difference(self.scheme.saved_rotation_keys)
         self.scheme.saved_rotation_keys.update(new)
         for k in new:
-            b.GenerateLinearTransformRotationKey(k)
+            if self.scheme.io_mode == "none":
+                b.GenerateLinearTransformRotationKey(k)
+            elif self.scheme.io_mode == "save" and str(k) not in self.scheme.key_store:
+                self.scheme._store(self.scheme.key_store, str(k), b.GenerateAndSerializeRotationKey(k))
+
+    # lt_evaluator.py:466-497
+    def load_transform(self, row, col, tid):
+        b = self.scheme.backend
+        for k in b.GetLinearTransformRotationKeys(tid):
+            b.LoadRotationKey(self.scheme.key_store[str(k)], int(k))
+        prefix = f"{self.name}/{row}_{col}/"
+        for key in self.scheme.diag_store.keys():
+            if key.startswith(prefix):
+                b.LoadPlaintextDiagonal(self.scheme.diag_store[key], tid, int(key[len(prefix):]))
 
     # lt_evaluator.py:224-275 (uniform path)
     def evaluate_lt(self, x):
@@ -325,10 +404,16 @@ class LinearLayer:
         rows = len(tids) // cols
         tids = tids.reshape(rows, cols)
         cts_out = []
+        io = self.scheme.io_mode != "none"
         for i in range(rows):
             ct_out = None
             for j in range(cols):
+                if io:
+                    self.load_transform(i, j, int(tids[i][j]))
                 res = CipherTensor(self.scheme, [b.EvaluateLinearTransform(int(tids[i][j]), x.ids[j])], x.n)
+                if io:
+                    b.RemoveRotationKeys()
+                    b.RemovePlaintextDiagonals(int(tids[i][j]))
                 if ct_out is None:
                     ct_out = res
                 else:

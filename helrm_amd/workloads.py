@@ -80,6 +80,7 @@ class LinearWorkload:
         self.input = None
         self.expected = None
         self.upload_seed = None
+        self.layer_name = "linear"
 
     def use_seeded_upload(self, seed):
         """Seeded selector upload (bench_sweep.py:381-403): the input is
@@ -102,7 +103,7 @@ class LinearWorkload:
 
     def setup(self):
         self.scheme = oh.Scheme(self.params, self.backend)
-        self.layer = oh.LinearLayer(self.scheme, self.matrix).compile()
+        self.layer = oh.LinearLayer(self.scheme, self.matrix, name=self.layer_name).compile()
         pt = self.scheme.encode(self.input, self.layer.level)
         self.ct_in = self.scheme.encrypt(pt)
         for i in pt.ids:
@@ -133,6 +134,7 @@ class PCMMWorkload(LinearWorkload):
 
     def __init__(self, backend, name="pcmm26", seed=0, key_seed=1):
         super().__init__(backend, name, key_seed)
+        self.layer_name = "sparse"
         c = self.cfg
         rng = np.random.default_rng(seed)
         base, dim = c["base"], c["dim"]
@@ -183,7 +185,8 @@ class SparseToTopWorkload(PCMMWorkload):
 
     def setup(self):
         super().setup()
-        self.repack = oh.LinearLayer(self.scheme, self.repack_matrix, level=self.layer.level - 1).compile()
+        self.repack = oh.LinearLayer(self.scheme, self.repack_matrix, level=self.layer.level - 1,
+                                     name="sparse_to_top").compile()
         return self
 
     def run(self):
@@ -350,14 +353,14 @@ class DLRMWorkload:
         L = self.levels
         mods = {}
         for k, (w, b) in enumerate(self.bottom_w):
-            mods[f"bottom.{2 * k}"] = oh.LinearLayer(s, w, b, level=L[f"bottom.{2 * k}"])
+            mods[f"bottom.{2 * k}"] = oh.LinearLayer(s, w, b, level=L[f"bottom.{2 * k}"], name=f"bottom.{2 * k}")
             mods[f"bottom.{2 * k + 1}"] = oh.Activation(s, self.coeffs)
-        mods["bottom_to_top"] = oh.LinearLayer(s, self.bottom_to_top_w, level=L["bottom_to_top"])
-        mods["sparse"] = oh.LinearLayer(s, self.emb.matrix, level=L["sparse"])
-        mods["sparse_to_top"] = oh.LinearLayer(s, self.sparse_to_top_w, level=L["sparse_to_top"])
+        mods["bottom_to_top"] = oh.LinearLayer(s, self.bottom_to_top_w, level=L["bottom_to_top"], name="bottom_to_top")
+        mods["sparse"] = oh.LinearLayer(s, self.emb.matrix, level=L["sparse"], name="sparse")
+        mods["sparse_to_top"] = oh.LinearLayer(s, self.sparse_to_top_w, level=L["sparse_to_top"], name="sparse_to_top")
         for k, (w, b) in enumerate(self.top_w):
             last = k == len(self.top_w) - 1
-            mods[f"top.{2 * k}"] = oh.LinearLayer(s, w, b, level=L[f"top.{2 * k}"], last=last)
+            mods[f"top.{2 * k}"] = oh.LinearLayer(s, w, b, level=L[f"top.{2 * k}"], last=last, name=f"top.{2 * k}")
             if not last:
                 mods[f"top.{2 * k + 1}"] = oh.Activation(s, self.coeffs)
         for m in mods.values():

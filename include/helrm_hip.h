@@ -30,6 +30,7 @@ extern "C" {
 typedef struct { int* Data; unsigned long Length; } ArrayResultInt;
 typedef struct { float* Data; unsigned long Length; } ArrayResultFloat;
 typedef struct { unsigned long long* Data; unsigned long long Length; } ArrayResultUInt64;
+typedef struct { char* Data; unsigned long Length; } ArrayResultByte;
 
 /* ---- scheme --------------------------------------------------------------- */
 /* orion/backend/lattigo/scheme.go:34-87 NewScheme (primes generated from the
@@ -55,6 +56,11 @@ int GenerateSecretKey(void);          /* keygenerator.go:17 */
 int GeneratePublicKey(void);          /* keygenerator.go:22 */
 int GenerateRelinearizationKey(void); /* keygenerator.go:27-30 (evaluation key s^2 -> s) */
 int GenerateEvaluationKeys(void);     /* keygenerator.go:32 */
+/* Serialization for Orion's io_mode save/load (key_generator.py:17-31).  Byte
+ * layout: Lattigo v6 WriteTo structure, little-endian u64 (see runtime.hip
+ * "binary wire format"); results are released with FreeCArray. */
+ArrayResultByte SerializeSecretKey(void);                        /* keygenerator.go:38-47 */
+int LoadSecretKey(const unsigned char* data, unsigned long len); /* keygenerator.go:49-58 */
 
 /* ---- encoder ------------------------------------------------------------------ */
 int NewEncoder(void);                                                      /* encoder.go:10 */
@@ -128,6 +134,13 @@ ArrayResultInt GetLinearTransformRotationKeys(int transformID);   /* lineartrans
 int GenerateLinearTransformRotationKey(int galEl);                /* lineartransform.go:124-128 */
 int DeleteLinearTransform(int id);                                /* lineartransform.go:25-28 */
 int RemoveRotationKeys(void);                                     /* lineartransform.go:203-211 */
+/* io_mode save / load of rotation keys and diagonals (lt_evaluator.py:133-161, 440-497) */
+ArrayResultByte GenerateAndSerializeRotationKey(int galEl);       /* lineartransform.go:130-140 (key not kept) */
+int LoadRotationKey(const unsigned char* data, unsigned long len, unsigned long galEl); /* lineartransform.go:142-160 */
+ArrayResultByte SerializeDiagonal(int transformID, int diagIdx);  /* lineartransform.go:162-177 (diagonal leaves the transform) */
+int LoadPlaintextDiagonal(const unsigned char* data, unsigned long len, int transformID,
+                          unsigned long diagIdx);                 /* lineartransform.go:179-193 */
+int RemovePlaintextDiagonals(int transformID);                    /* lineartransform.go:195-201 */
 
 /* ---- tensors -------------------------------------------------------------------- */
 int DeletePlaintext(int plaintextID);                       /* tensors.go:34-37 */

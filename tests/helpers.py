@@ -121,3 +121,35 @@ def oracle_dlrm(orc, w, dense_index=0, sparse_index=1, keep=False):
     for _, name in w.top_names:
         z = step(name, z)
     return z, trace
+
+
+def parse_wire_poly(buf, off, N):
+    """ring.Poly in the library's wire format: u64 rows, then per row u64 N
+    and N little-endian u64 words.  Returns (rows x N array, new offset)."""
+    buf = np.asarray(buf, dtype=np.uint8)
+    rows = int(buf[off:off + 8].view("<u8")[0])
+    off += 8
+    out = np.zeros((rows, N), dtype=np.uint64)
+    for r in range(rows):
+        n = int(buf[off:off + 8].view("<u8")[0])
+        assert n == N, f"row {r}: length {n}, expected {N}"
+        off += 8
+        out[r] = buf[off:off + 8 * N].view("<u8")
+        off += 8 * N
+    return out, off
+
+
+def parse_wire_qp(buf, off, N):
+    """ringqp.Poly: the Q part then the P part.  Returns ((Q, P), offset)."""
+    q, off = parse_wire_poly(buf, off, N)
+    p, off = parse_wire_poly(buf, off, N)
+    return (q, p), off
+
+
+def from_montgomery(rows, mods):
+    """x * 2^-64 mod q for each row (row i under mods[i])."""
+    out = np.zeros_like(rows)
+    for i, q in enumerate(mods):
+        rinv = pow(1 << 64, -1, int(q))
+        out[i] = np.array([(int(v) * rinv) % int(q) for v in rows[i]], dtype=np.uint64)
+    return out

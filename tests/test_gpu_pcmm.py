@@ -75,6 +75,36 @@ def test_pcmm_seeded_upload(hip_lib):
     hip_lib.DeleteScheme()
 
 
+def test_pcmm_io_mode_save_load(hip_lib, tmp_path):
+    """Orion's io_mode (key_generator.py:17-31, lt_evaluator.py:133-161,
+    224-262, 440-497) on the embedding PCMM: "save" serializes the secret key,
+    the rotation keys and every diagonal to files and evaluates from the
+    reloaded bytes; "load" in a new scheme instance reads them back instead of
+    generating them.  All three modes give the same output ciphertext, word
+    for word."""
+    name = "pcmm26_n13"
+    outs = {}
+    for mode in ("none", "save", "load"):
+        print(f"[pcmm] {name}: io_mode {mode}", flush=True)
+        w = PCMMWorkload(hip_lib, name, seed=6, key_seed=17)
+        w.params.io_mode = mode
+        w.params.keys_path = str(tmp_path / "keys.npz")
+        w.params.diags_path = str(tmp_path / "diags.npz")
+        w.setup()
+        out = w.run()
+        outs[mode] = hip_lib.export_ciphertext(out.ids[0])
+        if mode == "save":
+            w.scheme.flush()
+            assert "sk" in w.scheme.key_store
+            assert len([k for k in w.scheme.diag_store.keys()]) == w.shape_info()["diagonals"]
+        else:
+            y = w.decrypt_output(out)
+            assert np.abs(y - w.expected).max() < TOL
+        hip_lib.DeleteScheme()
+    assert_equal_u64(outs["save"], outs["none"], "io_mode save")
+    assert_equal_u64(outs["load"], outs["none"], "io_mode load")
+
+
 def test_pcmm26_full_size_decrypts(hip_lib):
     print("[pcmm] pcmm26 (N=2^16): building", flush=True)
     w = PCMMWorkload(hip_lib, "pcmm26", seed=3, key_seed=17).setup()

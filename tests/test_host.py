@@ -192,3 +192,20 @@ def test_dlrm_slot_algebra_matches_cleartext(name):
             z = w.act(z)
     assert abs(z[0] - w.expected[0]) < 1e-12
     assert np.abs(z[1:]).max() < 1e-12
+
+
+def test_wire_store_round_trip(tmp_path):
+    """The io_mode stores persist byte blobs as a .npz of uint8 arrays and read
+    them back without unpickling."""
+    path = str(tmp_path / "keys.npz")
+    st = oh.WireStore(path)
+    blobs = {"sk": np.arange(40, dtype=np.uint8), "5": np.frombuffer(b"\x00\xff" * 9, dtype=np.uint8),
+             "sparse/0_0/17": np.zeros(0, dtype=np.uint8)}
+    for k, v in blobs.items():
+        st[k] = v
+    st.flush()
+    back = oh.WireStore(path)
+    assert set(back.keys()) == set(blobs)
+    for k, v in blobs.items():
+        np.testing.assert_array_equal(back[k], v)
+        assert back[k].dtype == np.uint8
