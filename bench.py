@@ -164,6 +164,19 @@ def cpu_baseline_dlrm(q, p, w, threads):
         orc.close()
 
 
+def keyswitch_bytes(N, Lq, K, nb, ng, w=8):
+    """Algorithmic bytes of one launch of the BSGS key-switch kernels of a
+    Linear with Lq active Q limbs: keymac_baby (the nb-1 hoisted baby
+    rotations: their keys, the decomposed input once, P*c0 once, the rotated
+    QP pairs written) and giant_acc (the ng-1 giant groups: keys, decomposed
+    c1 parts and c0 accumulators read, one QP pair written)."""
+    nqp, dn = Lq + K, (Lq + K - 1) // K
+    nbr, ngk = max(nb - 1, 0), max(ng - 1, 0)
+    baby = nbr * dn * 2 * nqp * N * w + dn * nqp * N * w + Lq * N * w + nbr * 2 * nqp * N * w
+    giant = ngk * (dn * 2 + dn + 1) * nqp * N * w + 2 * nqp * N * w
+    return baby, giant
+
+
 def lt_roofline_bytes(lib, layer, N, K, w=8):
     """(whole-layer, diagonal-MAC) algorithmic bytes of one compiled Linear
     at its level: algorithmic_bytes with L = level + 1 active Q limbs and the
@@ -354,10 +367,14 @@ def main():
     launches = max(1, round(kt["diag_mac"]["launches"] / nprof)) if kt["diag_mac"]["launches"] else 1
     layers = w.linear_layers()
     step_bytes, mac_bytes, lt_shapes = 0, 0, []
+    ks_bytes = {"keymac_baby": 0, "giant_acc": 0}
     for layer in layers:
         (b_layer, b_mac), lti = lt_roofline_bytes(lib, layer, N, K)
         step_bytes += b_layer
         mac_bytes += b_mac
+        kb, kg = keyswitch_bytes(N, layer.level + 1, K, lti["baby"], lti["giant"])
+        ks_bytes["keymac_baby"] += kb if lti["baby"] > 1 else 0
+        ks_bytes["giant_acc"] += kg if lti["giant"] > 1 else 0
         lt_shapes.append({"level": layer.level, "diagonals": lti["plaintexts"], "baby": lti["baby"],
                           "giant": lti["giant"], "fold": layer.output_rotations})
     if cfg["kind"] == "dlrm":
@@ -375,6 +392,17 @@ def main():
                 "kernel": "diag_mac_kernel", "algorithmic_bytes_per_launch": mac_per_launch,
                 "launches_per_step": launches}
     lti = lib.lt_info(list(layers[0].transform_ids.values())[0])
+    # the key-switch kernels of the transforms against the same peak
+    kernel_rooflines = {"diag_mac": {"algorithmic_bytes_per_launch": mac_per_launch, "avg_ms": mac_ms,
+                                     "achieved_GBs": achieved, "frac": roofline["frac"]}}
+    for name, total in ks_bytes.items():
+        n_l = kt[name]["launches"] / nprof if kt[name]["launches"] else 0
+        if not n_l or not kt[name]["avg_ms"]:
+            continue
+        per = total / n_l
+        gbs = per / (kt[name]["avg_ms"] / 1000.0) / 1e9
+        kernel_rooflines[name] = {"algorithmic_bytes_per_launch": per, "avg_ms": kt[name]["avg_ms"],
+                                  "achieved_GBs": gbs, "frac": gbs / HBM_PEAK_GBS}
 
     cpu = None
     if not args.no_cpu_baseline and cfg["kind"] == "dlrm":
@@ -414,6 +442,7 @@ def main():
         "linear_transforms": lt_shapes,
         "selector_upload": upload,
         "roofline": roofline,
+        "kernel_rooflines": kernel_rooflines,
         "cpu_baseline": cpu,
         "max_abs_err_vs_plaintext": err,
         "ntt_microbench": ntt,

@@ -137,6 +137,58 @@ __device__ __forceinline__ void acc_mac_s(Acc128& A, u64 a, u64 b) {
         [ca] "=&s"(ca), [cb] "=&s"(cb), [cc] "=&s"(cc), [cd] "=&s"(cd)
       : [a0] "v"(a0), [a1] "v"(a1), [b0] "s"(b0), [b1] "s"(b1));
 }
+// Exact sum of at most 8 products of words below 2^61 (every modulus here is
+// below 2^61).  Split at 32 bits the high halves are below 2^29, so a middle
+// column of 4 products (8 terms below 2^61) and the top column of 8 products
+// (below 2^58 each) cannot overflow: only the low column counts carries, and
+// the middle column is kept in two halves (products 0-3 and 4-7).  5 VALU
+// instructions per product instead of 7.
+struct Acc61 { u64 s0, s1a, s1b, s2; uint32_t c0; };
+__device__ __forceinline__ void acc61_zero(Acc61& A) { A.s0 = A.s1a = A.s1b = A.s2 = 0; A.c0 = 0; }
+// the first product of an accumulator (and of its second middle half) sets
+// the columns instead of adding to zeros
+__device__ __forceinline__ void acc61_first_s(Acc61& A, u64 a, u64 b) {
+  const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32), b0 = (uint32_t)b, b1 = (uint32_t)(b >> 32);
+  u64 junk;
+  asm("v_mad_u64_u32 %[s0], %[j], %[b0], %[a0], 0\n\t"
+      "v_mad_u64_u32 %[s1], %[j], %[b1], %[a0], 0\n\t"
+      "v_mad_u64_u32 %[s1], %[j], %[b0], %[a1], %[s1]\n\t"
+      "v_mad_u64_u32 %[s2], %[j], %[b1], %[a1], 0"
+      : [s0] "=&v"(A.s0), [s1] "=&v"(A.s1a), [s2] "=&v"(A.s2), [j] "=&s"(junk)
+      : [a0] "v"(a0), [a1] "v"(a1), [b0] "s"(b0), [b1] "s"(b1));
+  A.c0 = 0;
+}
+__device__ __forceinline__ void acc61_first_half_s(Acc61& A, u64 a, u64 b) {
+  const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32), b0 = (uint32_t)b, b1 = (uint32_t)(b >> 32);
+  u64 ca, junk;
+  asm("v_mad_u64_u32 %[s0], %[ca], %[b0], %[a0], %[s0]\n\t"
+      "v_mad_u64_u32 %[s1], %[j], %[b1], %[a0], 0\n\t"
+      "v_mad_u64_u32 %[s1], %[j], %[b0], %[a1], %[s1]\n\t"
+      "v_mad_u64_u32 %[s2], %[j], %[b1], %[a1], %[s2]\n\t"
+      "v_addc_co_u32_e64 %[c0], %[j], 0, %[c0], %[ca]"
+      : [s0] "+v"(A.s0), [s1] "=&v"(A.s1b), [s2] "+v"(A.s2), [c0] "+v"(A.c0), [ca] "=&s"(ca), [j] "=&s"(junk)
+      : [a0] "v"(a0), [a1] "v"(a1), [b0] "s"(b0), [b1] "s"(b1));
+}
+template <int HALF>
+__device__ __forceinline__ void acc61_mac_s(Acc61& A, u64 a, u64 b) {
+  const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32), b0 = (uint32_t)b, b1 = (uint32_t)(b >> 32);
+  u64& s1 = HALF ? A.s1b : A.s1a;
+  u64 ca, junk;
+  asm("v_mad_u64_u32 %[s0], %[ca], %[b0], %[a0], %[s0]\n\t"
+      "v_mad_u64_u32 %[s1], %[j], %[b1], %[a0], %[s1]\n\t"
+      "v_mad_u64_u32 %[s1], %[j], %[b0], %[a1], %[s1]\n\t"
+      "v_mad_u64_u32 %[s2], %[j], %[b1], %[a1], %[s2]\n\t"
+      "v_addc_co_u32_e64 %[c0], %[j], 0, %[c0], %[ca]"
+      : [s0] "+v"(A.s0), [s1] "+v"(s1), [s2] "+v"(A.s2), [c0] "+v"(A.c0), [ca] "=&s"(ca), [j] "=&s"(junk)
+      : [a0] "v"(a0), [a1] "v"(a1), [b0] "s"(b0), [b1] "s"(b1));
+}
+__device__ __forceinline__ void acc61_value(const Acc61& A, u64& lo, u64& hi) {
+  const u64 s1 = A.s1a + A.s1b;
+  const u64 s1c = s1 < A.s1a ? 1 : 0;
+  const u64 t = s1 << 32;
+  lo = A.s0 + t;
+  hi = A.s2 + A.c0 + (s1 >> 32) + (s1c << 32) + (lo < t ? 1 : 0);
+}
 // the 128-bit value (lo, hi) of an accumulator
 __device__ __forceinline__ void acc_value(const Acc128& A, u64& lo, u64& hi) {
   const u64 t = A.s1 << 32;

@@ -179,14 +179,18 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
     // exact column sums of 16 products (words < 2^62), folded below q
     u64 res;
     if (MAXS <= 8) {
-      // y[i] < 2^62 and h[i] < q: at most 8 products sum below 2^65 * q, so
-      // hi < 2q and a single subtraction brings it below q for the REDC
-      Acc128 A;
-      acc_zero(A);
+      // y[i] < q_i < 2^61 and h[i] < q < 2^61: 8 products sum below 2^64 q,
+      // so hi < q as the REDC needs (the subtraction below is a safeguard)
+      Acc61 A;
 #pragma unroll
-      for (int i = 0; i < MAXS; i++) acc_mac_s(A, y[i], h[i]);  // y[i] = 0 past ns
+      for (int i = 0; i < MAXS; i++) {  // y[i] = 0 past ns
+        if (i == 0) acc61_first_s(A, y[i], h[i]);
+        else if (i < 4) acc61_mac_s<0>(A, y[i], h[i]);
+        else if (i == 4) acc61_first_half_s(A, y[i], h[i]);
+        else acc61_mac_s<1>(A, y[i], h[i]);
+      }
       u64 lo, hi;
-      acc_value(A, lo, hi);
+      acc61_value(A, lo, hi);
       res = redc(lo, csub64(hi, mc.q), mc.q, mc.qinv);
     } else {
       u128 acc = 0;

@@ -54,7 +54,12 @@ def test_linear_transform_argument_checks(lib):
     with pytest.raises(HipError, match="len\\(diag_idxs\\) \\* slots"):
         lib.GenerateLinearTransform([0, 1], np.zeros(S, np.float32), 3, 2.0, "none")
     with pytest.raises(HipError, match="io_mode"):
-        lib.GenerateLinearTransform([0], np.zeros(S, np.float32), 3, 2.0, "save")
+        lib.GenerateLinearTransform([0], np.zeros(S, np.float32), 3, 2.0, "stream")
+    # io_mode "load": no diagonals yet, so evaluation is refused until they are loaded
+    tl = lib.GenerateLinearTransform([0], np.zeros(S, np.float32), 3, 2.0, "load")
+    with pytest.raises(HipError, match="not loaded"):
+        lib.EvaluateLinearTransform(tl, fresh(lib))
+    lib.DeleteLinearTransform(tl)
     # rotation keys never generated for this transform: refused before any kernel runs
     tid = lib.GenerateLinearTransform([0, 7, 300], np.ones(3 * S, np.float32), 3, 2.0, "none")
     with pytest.raises(HipError, match="missing Galois key"):
