@@ -234,8 +234,10 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
   if (FWD) {
     RoundTw<4> T1;
     round_tw_load<true, 4>(T1, A, S - 4, Nn, tw);
+    // data words are touched once per pass: streamed past L2 so the twiddle
+    // table, shared by every limb of a modulus in the launch, stays cached
 #pragma unroll
-    for (int i = 0; i < 16; i++) v[i] = poly[j + P * i];
+    for (int i = 0; i < 16; i++) v[i] = __builtin_nontemporal_load(&poly[j + P * i]);
     ntt_round<true, 4>(v, T1, q);
 #pragma unroll
     for (int i = 0; i < 16; i++) srow[swz(j + P * i)] = v[i];
@@ -263,10 +265,10 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
       u64 xv[16], av[16];
       uint32_t dst[16];
 #pragma unroll
-      for (int i = 0; i < 16; i++) xv[i] = xr[j + P * i];
+      for (int i = 0; i < 16; i++) xv[i] = __builtin_nontemporal_load(&xr[j + P * i]);
       if (ar) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) av[i] = ar[j + P * i];
+        for (int i = 0; i < 16; i++) av[i] = __builtin_nontemporal_load(&ar[j + P * i]);
       } else {
 #pragma unroll
         for (int i = 0; i < 16; i++) av[i] = 0;
@@ -282,18 +284,18 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
       for (int i = 0; i < 16; i++) {
         const int pos = j + P * i;
         const u64 o = shoup_mul(sub_mod(xv[i], srow[swz(pos)], q), pi, pip, q);
-        orow[dst[i]] = add_mod(o, av[i], q);
+        __builtin_nontemporal_store(add_mod(o, av[i], q), &orow[dst[i]]);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; i++) poly[j + P * i] = srow[swz(j + P * i)];
+      for (int i = 0; i < 16; i++) __builtin_nontemporal_store(srow[swz(j + P * i)], &poly[j + P * i]);
     }
   } else {
     const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + (size_t)r * C;
     // all 16 loads in flight before the LDS writes; the first round's
     // twiddles are issued behind them and arrive during the barrier
 #pragma unroll
-    for (int i = 0; i < 16; i++) v[i] = in[j + P * i];
+    for (int i = 0; i < 16; i++) v[i] = __builtin_nontemporal_load(&in[j + P * i]);
 #pragma unroll
     for (int i = 0; i < 16; i++) srow[swz(j + P * i)] = v[i];
     RoundTw<S - 4> T1;
@@ -311,7 +313,7 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
     for (int i = 0; i < 16; i++) v[i] = srow[swz(j + P * i)];
     ntt_round<false, 4>(v, T2, q);
 #pragma unroll
-    for (int i = 0; i < 16; i++) poly[j + P * i] = v[i];
+    for (int i = 0; i < 16; i++) __builtin_nontemporal_store(v[i], &poly[j + P * i]);
   }
 }
 
