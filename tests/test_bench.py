@@ -1,0 +1,48 @@
+"""bench.py's contract pieces that need no GPU: the refusal of more than one
+GPU and the algorithmic byte counts its rooflines divide by."""
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr or "single MI355X" in r.stderr
+
+
+def test_pcmm26_algorithmic_bytes():
+    """N=2^16, L=24, K=8, D=512, 16 baby x 32 giant steps, 6 fold rotations,
+    dnum=3: diagonals + 52 rotation keys + input + output ciphertexts, and the
+    diagonal-MAC launch (diagonals, 15 hoisted rotations, P*c, 32 QP
+    accumulator pairs)."""
+    pcmm, mac = bench.algorithmic_bytes()
+    assert pcmm == 13_873_709_056
+    assert mac == 10_192_158_720
+    N, w, nqp = 1 << 16, 8, 32
+    assert mac == 512 * nqp * N * w + 15 * 2 * nqp * N * w + 2 * 24 * N * w + 32 * 2 * nqp * N * w
+
+
+def test_keyswitch_kernel_bytes():
+    """keymac_baby: 15 keys of 3 digits x 2 parts x 32 QP rows, the 3 digits
+    once, P*c0 (24 rows) once, 15 rotated QP pairs; giant_acc: 31 keys, their
+    digits and c0 accumulators, one QP pair out."""
+    baby, giant = bench.keyswitch_bytes(1 << 16, 24, 8, 16, 32)
+    row = (1 << 16) * 8
+    assert baby == (15 * 3 * 2 * 32 + 3 * 32 + 24 + 15 * 2 * 32) * row
+    assert giant == (31 * (3 * 2 + 3 + 1) * 32 + 2 * 32) * row
+
+
+@pytest.mark.parametrize("lq,nb,ng", [(1, 1, 1), (8, 4, 4)])
+def test_keyswitch_bytes_without_rotations(lq, nb, ng):
+    baby, giant = bench.keyswitch_bytes(1 << 13, lq, 8, nb, ng)
+    assert baby >= 0 and giant >= 0
+    if nb == 1:
+        assert baby == ((lq + 7) // 8) * (lq + 8) * (1 << 13) * 8 + lq * (1 << 13) * 8
