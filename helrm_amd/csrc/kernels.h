@@ -128,7 +128,6 @@ void launch_sample_uniform(u64* out, RowMap rm, u64 seed, u64 stream, const ModC
 void launch_sample_cbd(u64* out, RowMap rm, u64 seed, u64 stream, const ModC* mods, int N, bool add, hipStream_t st);
 void launch_signed_rows(u64* out, RowMap rm, const int8_t* v, const ModC* mods, int N, hipStream_t st);
 void launch_gk_combine(u64* b, const u64* a, const u64* soR, const u64* sR, int own0, int own1, const u64* pmod, int rows, const ModC* mods, int N, hipStream_t st);
-void launch_encode_residues(u64* out, RowMap rm, const u64* rec, const ModC* mods, int N, hipStream_t st);
 // Device encoder (encoder.hip): plaintext p of a batch takes element k from
 // data[src * slots + ((k + rot) mod slots)] (zero past nvals), runs the special
 // inverse FFT in float64 (work buffers re/im, pstride words per plaintext),

@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
     u64 res;
     if (MAXS <= 8) {
       // y[i] < q_i < 2^61 and h[i] < q < 2^61: 8 products sum below 2^64 q,
-      // so hi < q as the REDC needs (the subtraction below is a safeguard)
+      // so hi < q as the REDC needs
       Acc61 A;
 #pragma unroll
       for (int i = 0; i < MAXS; i++) {  // y[i] = 0 past ns
@@ -191,7 +191,7 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
       }
       u64 lo, hi;
       acc61_value(A, lo, hi);
-      res = redc(lo, csub64(hi, mc.q), mc.q, mc.qinv);
+      res = redc(lo, hi, mc.q, mc.qinv);
     } else {
       u128 acc = 0;
 #pragma unroll
@@ -607,19 +607,3 @@ void launch_gk_combine(u64* b, const u64* a, const u64* soR, const u64* sR, int 
   hipLaunchKernelGGL(gk_combine_kernel, dim3(N / 256, rows, 1), dim3(256), 0, st, b, a, soR, sR, own0, own1, pmod, mods, N);
 }
 
-// Encoder: fixed-point coefficients -> residues.  rec[x] = {mag, exp|flags}
-// where a big value is mag * 2^exp; negative values are negated mod q.
-__global__ void encode_residues_kernel(u64* __restrict__ out, RowMap rm, const u64* __restrict__ rec, const ModC* __restrict__ mods, int N) {
-  int x = blockIdx.x * blockDim.x + threadIdx.x;
-  int row = rm.row(blockIdx.y);
-  ModC mc = mods[rm.mod(row)];
-  u64 mag = rec[2 * x], meta = rec[2 * x + 1];
-  int neg = (int)(meta & 1), exp = (int)(meta >> 8);
-  u64 r = mont_mul(mag, mc.rmod, mc.q, mc.qinv);  // mag mod q
-  for (int e = 0; e < exp; e++) r = add_mod(r, r, mc.q);
-  if (neg && r) r = mc.q - r;
-  out[(size_t)row * N + x] = r;
-}
-void launch_encode_residues(u64* out, RowMap rm, const u64* rec, const ModC* mods, int N, hipStream_t st) {
-  hipLaunchKernelGGL(encode_residues_kernel, dim3(N / 256, rm.nact(), 1), dim3(256), 0, st, out, rm, rec, mods, N);
-}
