@@ -293,7 +293,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: the PCMM runs on a single MI355X (asked for --gpus {args.gpus}, "
-              f"WORLD_SIZE {world}); multi-GPU sharding is described in DESIGN.md but not built.", file=sys.stderr)
+              f"WORLD_SIZE {world}); sharding the PCMM over several GPUs is not built.", file=sys.stderr)
         sys.exit(2)
 
     from helrm_amd.backend import HipLibrary

@@ -1293,16 +1293,12 @@ std::unique_ptr<Cipher> eval_lt_naive(const LinTrans& t, const Cipher& ct) {
     a.out0 = R.p; a.out1 = R.p + qp; a.out_bstride = 2 * qp; a.mods = s.d_mods.p;
     a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
     launch_keymac(a, n, s.st);
-    RowMap rm = rows_qp(l);
-    RowMap prm{nqp, l + 1, 0, t.level + 1, 0, 0};  // unused mapping helper
-    (void)prm;
     for (int i = 0; i < n; i++) {
       const u64* dp = t.diags.p + (size_t)nz[i] * dstride;
       // the diagonal's P rows sit after its own Q rows (level t.level); multiply Q and P parts separately
       launch_mont_mul(acc.p, qp, R.p + (size_t)i * 2 * qp, qp, dp, 0, 2, rows_q(l), s.d_mods.p, N, true, s.st);
       launch_mont_mul(acc.p + (size_t)(l + 1) * N, qp, R.p + (size_t)i * 2 * qp + (size_t)(l + 1) * N, qp, dp + (size_t)(t.level + 1) * N, 0, 2,
                       RowMap{K, 0, 0, s.L, 0, 0}, s.d_mods.p, N, true, s.st);
-      (void)rm;
     }
   }
   auto out = new_ct(l, ct.scale * t.scale); out->logslots = ct.logslots;
