@@ -343,6 +343,7 @@ def main():
         o, st = w.run_staged(lib.Synchronize, time.perf_counter)
         o.free()
         stages = {k: v * 1000.0 for k, v in st.items()}
+        layer_ms = {k: v * 1000.0 for k, v in w.layer_s.items()}
 
     # per-kernel HIP-event timings (separate, untimed passes): a 50 ms idle gap
     # on either side marks them in a kernel trace of this run; the first step
@@ -453,6 +454,7 @@ def main():
     }
     if cfg["kind"] == "dlrm":
         line["stage_ms"] = stages
+        line["layer_ms"] = layer_ms
         line["levels"] = {"input": w.input_level, "add": w.add_level, "output": 0}
     else:
         line["config"].update({"diagonals": info["diagonals"], "baby_steps": lti["baby"], "giant_steps": lti["giant"],

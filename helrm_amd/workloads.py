@@ -421,8 +421,9 @@ class DLRMWorkload:
     def run_staged(self, sync, clock):
         """One forward with `sync()` before each timestamp around every
         layer (the stage hooks of bench_sweep.py:195-219); returns (output,
-        {stage: seconds})."""
+        {stage: seconds}); the per-layer seconds are kept in self.layer_s."""
         times = {}
+        self.layer_s = {}
         m = self.modules
         if self.upload_seed is not None:
             for cid in self.ct_sparse.ids:
@@ -434,7 +435,9 @@ class DLRMWorkload:
             y = m[name].forward(x) if name != "add" else x[0].add(x[1])
             sync()
             st = self.stage_of(name)
-            times[st] = times.get(st, 0.0) + clock() - t0
+            dt = clock() - t0
+            times[st] = times.get(st, 0.0) + dt
+            self.layer_s[name] = dt
             if free_in:
                 for c in (x if isinstance(x, tuple) else (x,)):
                     c.free()
