@@ -223,7 +223,7 @@ void launch_bconv(const u64* in, size_t in_bstride, BConvJobs jobs, u64* out, si
   // all destination rows in one thread unless that leaves too few workgroups
   const int cols = N / 256;
   int ny = 1;
-  while (ny < nrows && (long)cols * batch * jobs.n * ny < 2048) ny *= 2;
+  while (ny < nrows && (long)cols * batch * jobs.n * ny < 768) ny *= 2;
   jobs.rows_per_block = (nrows + ny - 1) / ny;
   ny = (nrows + jobs.rows_per_block - 1) / jobs.rows_per_block;
   dim3 grid(cols, ny, batch * jobs.n);
