@@ -165,6 +165,13 @@ _SIGNATURES = {
     "SerializeDiagonal": ([_I, _I], ArrayResultByte),
     "LoadPlaintextDiagonal": ([_PB, _c.c_ulong, _I, _c.c_ulong], _I),
     "RemovePlaintextDiagonals": ([_I], _I),
+    "EncodeComplex": ([_PF, _I, _I, _c.c_ulong], _I),
+    "DecodeComplex": ([_I], ArrayResultFloat),
+    "MulImaginaryUnit": ([_I], _I),
+    "MulImaginaryUnitNew": ([_I], _I),
+    "LiveHeapBytes": ([], _c.c_ulonglong),
+    "StartLiveHeapSampler": ([_I], _I),
+    "StopLiveHeapSampler": ([], _c.c_ulonglong),
     "EncryptSeeded": ([_I, _c.c_ulonglong], _I),
     "DropAx": ([_I], _I),
     "ExpandSeededAx": ([_I, _c.c_ulonglong], _I),

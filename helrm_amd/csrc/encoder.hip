@@ -22,17 +22,26 @@
 
 namespace {
 
-// plaintext p, element k: data[src * slots + ((k + rot) mod slots)], or 0 past nvals
+// plaintext p, element k: data[src * slots + ((k + rot) mod slots)], or 0 past
+// nvals; complex input: (re, im) pairs at data[2k], data[2k + 1]
 __global__ void encode_load_kernel(double* __restrict__ re, double* __restrict__ im, size_t pstride,
-                                   const float* __restrict__ data, const EncodeSrc* __restrict__ src, int n, int nvals) {
+                                   const float* __restrict__ data, const EncodeSrc* __restrict__ src, int n, int nvals,
+                                   int complex_in) {
   const int k = blockIdx.x * blockDim.x + threadIdx.x;
   const int p = blockIdx.y;
   if (k >= n) return;
   const EncodeSrc e = src[p];
-  double v = 0.0;
-  if (k < nvals) v = (double)data[(size_t)e.src * n + ((k + e.rot) & (n - 1))];
+  double v = 0.0, vi = 0.0;
+  if (k < nvals) {
+    if (complex_in) {
+      v = (double)data[2 * (size_t)k];
+      vi = (double)data[2 * (size_t)k + 1];
+    } else {
+      v = (double)data[(size_t)e.src * n + ((k + e.rot) & (n - 1))];
+    }
+  }
   re[(size_t)p * pstride + k] = v;
-  im[(size_t)p * pstride + k] = 0.0;
+  im[(size_t)p * pstride + k] = vi;
 }
 
 // one DIF stage of the special inverse FFT: blocks of len, pairs (k, k + len/2)
@@ -106,10 +115,11 @@ __global__ void encode_finish_kernel(u64* __restrict__ out, size_t out_pstride, 
 
 void launch_encode_fft(u64* out, size_t out_pstride, RowMap rm, const float* data, const EncodeSrc* src, int np, int nvals,
                        double scale, double* re, double* im, size_t pstride, const int* rotgroup, const double* rre,
-                       const double* rim, const ModC* mods, int logN, hipStream_t st) {
+                       const double* rim, const ModC* mods, int logN, hipStream_t st, bool complex_in) {
   const int N = 1 << logN, n = N >> 1, M = 2 * N, logn = logN - 1;
   const int tpb = 256;
-  hipLaunchKernelGGL(encode_load_kernel, dim3((n + tpb - 1) / tpb, np), dim3(tpb), 0, st, re, im, pstride, data, src, n, nvals);
+  hipLaunchKernelGGL(encode_load_kernel, dim3((n + tpb - 1) / tpb, np), dim3(tpb), 0, st, re, im, pstride, data, src, n, nvals,
+                     complex_in ? 1 : 0);
   for (int len = n; len >= 2; len >>= 1)
     hipLaunchKernelGGL(special_ifft_stage_kernel, dim3((n / 2 + tpb - 1) / tpb, np), dim3(tpb), 0, st, re, im, pstride, n, len,
                        M, rotgroup, rre, rim);

@@ -136,6 +136,10 @@ void launch_gk_combine(u64* b, const u64* a, const u64* soR, const u64* sR, int 
 struct EncodeSrc { int src, rot; };
 void launch_encode_fft(u64* out, size_t out_pstride, RowMap rm, const float* data, const EncodeSrc* src, int np, int nvals,
                        double scale, double* re, double* im, size_t pstride, const int* rotgroup, const double* rre,
-                       const double* rim, const ModC* mods, int logN, hipStream_t st);
+                       const double* rim, const ModC* mods, int logN, hipStream_t st, bool complex_in = false);
+// multiplication by the imaginary unit (the monomial X^(N/2)) in the NTT domain:
+// slot x < N/2 times iu[m], slot x >= N/2 times q - iu[m] (Shoup pairs iu / iup, niu / niup)
+void launch_mul_i(u64* out, const u64* in, size_t bstride, int batch, RowMap rm, const u64* iu, const u64* iup,
+                  const u64* niu, const u64* niup, const ModC* mods, int N, hipStream_t st);
 // out[r][x] = sum_{p < npoly} a[p][r][x] * b[p][r][x] mod q_r, rows r < nrows of the modulus table
 void launch_mulacc(const u64* a, const u64* b, u64* out, int npoly, int nrows, const ModC* mods, int N, hipStream_t st);

@@ -242,6 +242,22 @@ void launch_bconv(const u64* in, size_t in_bstride, int ns, const BConvTable* dt
   launch_bconv(in, in_bstride, jobs, out, out_bstride, batch, mods, N, st);
 }
 
+__global__ void mul_i_kernel(u64* __restrict__ out, const u64* __restrict__ in, size_t bstride, RowMap rm,
+                             const u64* __restrict__ iu, const u64* __restrict__ iup, const u64* __restrict__ niu,
+                             const u64* __restrict__ niup, const ModC* __restrict__ mods, int N) {
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
+  const int row = rm.row(blockIdx.y), m = rm.mod(row);
+  const size_t o = (size_t)blockIdx.z * bstride + (size_t)row * N + x;
+  const bool lo = x < (N >> 1);
+  out[o] = shoup_mul(in[o], lo ? iu[m] : niu[m], lo ? iup[m] : niup[m], mods[m].q);
+}
+void launch_mul_i(u64* out, const u64* in, size_t bstride, int batch, RowMap rm, const u64* iu, const u64* iup,
+                  const u64* niu, const u64* niup, const ModC* mods, int N, hipStream_t st) {
+  if (batch <= 0 || rm.nact() <= 0) return;
+  hipLaunchKernelGGL(mul_i_kernel, dim3(N / 256, rm.nact(), batch), dim3(256), 0, st, out, in, bstride, rm, iu, iup, niu, niup,
+                     mods, N);
+}
+
 // ModDown combine: out = (x - ext) * P^-1 (+ add) [gathered through perm]
 // x rows = Q rows of a QP poly (stride x_bstride), ext rows = Q rows.
 __global__ void moddown_combine_kernel(u64* __restrict__ out, size_t o_bstride, const u64* __restrict__ x, size_t x_bstride,

@@ -260,6 +260,7 @@ struct Scheme {
   // per-modulus constants (Shoup pairs indexed by modulus)
   DU64 pmod_w, pmod_wp, pinv_w, pinv_wp, p0inv_w, p0inv_wp, pmod_plain;
   DU64 rs_inv, rs_invp;  // [l][i] q_l^-1 mod q_i
+  DU64 iu, iup, niu, niup;  // [mod] psi^(N/2) (a square root of -1), its negation, Shoup companions
   std::map<std::pair<int, int>, std::unique_ptr<BConvHost>> bconv;
   std::map<u64, DevArray<uint32_t>> perms, perm_invs;
   std::map<std::tuple<int, int, size_t>, std::unique_ptr<struct DigitRows>> digit_rows;
@@ -628,7 +629,7 @@ void special_fft(const Scheme& s, std::vector<double>& re, std::vector<double>& 
 // rm of out + p * out_pstride, then the forward NTT.  Batches of up to 64
 // plaintexts share one work buffer.
 void encode_device(const float* h_data, size_t ndata, const std::vector<EncodeSrc>& src, int nvals, double scale, RowMap rm,
-                   u64* out, size_t out_pstride) {
+                   u64* out, size_t out_pstride, bool complex_in = false) {
   Scheme& s = sch();
   const int N = s.N, slots = N / 2;
   DevArray<float> dd(std::max<size_t>(ndata, 1));
@@ -640,7 +641,7 @@ void encode_device(const float* h_data, size_t ndata, const std::vector<EncodeSr
     const int nb = std::min(chunk, np - c0);
     u64* o = out + (size_t)c0 * out_pstride;
     launch_encode_fft(o, out_pstride, rm, dd.p, ds.p + c0, nb, nvals, scale, re.p, im.p, slots, s.d_rotgroup.p, s.d_rre.p,
-                      s.d_rim.p, s.d_mods.p, s.logN, s.st);
+                      s.d_rim.p, s.d_mods.p, s.logN, s.st, complex_in);
     ntt(o, out_pstride, nb, rm, true);
   }
   sync();
@@ -683,7 +684,7 @@ double big_to_double(const Big& a) {  // nearest, ties to even
   return std::ldexp((double)hi, sh);
 }
 // Lattigo Encoder.Decode (float64): centred CRT value / scale, SpecialFFT, real part
-std::vector<double> decode_host(const std::vector<u64>& coef, int level, double scale) {
+std::vector<double> decode_host(const std::vector<u64>& coef, int level, double scale, std::vector<double>* imag = nullptr) {
   Scheme& s = sch();
   const int N = s.N, slots = N / 2, nl = level + 1;
   std::vector<double> vals(N);
@@ -725,6 +726,7 @@ std::vector<double> decode_host(const std::vector<u64>& coef, int level, double 
   std::vector<double> re(slots), im(slots);
   for (int i = 0; i < slots; i++) { re[i] = vals[i]; im[i] = vals[i + slots]; }
   special_fft(s, re, im, slots);
+  if (imag) *imag = im;
   return re;
 }
 
@@ -761,6 +763,7 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
     }
     s.d_mods = DevArray<ModC>(nm); upload(s.d_mods.p, s.hmods.data(), nm);
     std::vector<u64> htw((size_t)nm * N * 2), hitw((size_t)nm * N * 2), hn(nm), hnp(nm);
+    std::vector<u64> hiu(nm), hiup(nm), hniu(nm), hniup(nm);
     for (int m = 0; m < nm; m++) {
       u64 qq = s.mod[m];
       u64 g = smallest_generator(qq);
@@ -775,8 +778,11 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
         hitw[o] = ipw[r]; hitw[o + 1] = shoup(ipw[r], qq);
       }
       hn[m] = invmod((u64)N, qq); hnp[m] = shoup(hn[m], qq);
+      hiu[m] = pw[N / 2]; hiup[m] = shoup(hiu[m], qq);
+      hniu[m] = qq - pw[N / 2]; hniup[m] = shoup(hniu[m], qq);
     }
     auto up = [&](DU64& d, const std::vector<u64>& h) { d = DU64(h.size()); upload(d.p, h.data(), h.size()); };
+    up(s.iu, hiu); up(s.iup, hiup); up(s.niu, hniu); up(s.niup, hniup);
     // lane-interleaved copies of the twiddles of the row pass's round over 16
     // consecutive words: [mod][R][slot][lane], slots in the kernel's order
     int SA, SB;
@@ -1397,7 +1403,20 @@ std::unique_ptr<Plain> encode_values(const float* v, int n, int level, double sc
   encode_device(buf.data(), buf.size(), {EncodeSrc{0, 0}}, n, scale, rows_q(level), p->d.p, 0);
   return p;
 }
-std::vector<double> decode_pt(const Plain& p) {
+// complex slot values, interleaved (re, im) pairs as EncodeComplex passes them
+std::unique_ptr<Plain> encode_complex_values(const float* v, int n, int level, double scale) {
+  Scheme& s = sch();
+  REQUIRE(level >= 0 && level < s.L, "invalid level");
+  REQUIRE(n >= 0 && n <= s.N / 2, "too many values for the slot count");
+  auto p = std::make_unique<Plain>();
+  p->level = level; p->scale = scale; p->logslots = s.logN - 1;
+  p->d = DU64((size_t)(level + 1) * s.N);
+  std::vector<float> buf((size_t)s.N, 0.0f);
+  std::copy(v, v + 2 * (size_t)n, buf.begin());
+  encode_device(buf.data(), buf.size(), {EncodeSrc{0, 0}}, n, scale, rows_q(level), p->d.p, 0, true);
+  return p;
+}
+std::vector<double> decode_pt(const Plain& p, std::vector<double>* imag = nullptr) {
   Scheme& s = sch();
   const int N = s.N, l = p.level;
   DU64 tmp((size_t)(l + 1) * N);
@@ -1405,7 +1424,7 @@ std::vector<double> decode_pt(const Plain& p) {
   ntt(tmp.p, 0, 1, rows_q(l), false);
   std::vector<u64> coef((size_t)(l + 1) * N);
   download(coef.data(), tmp.p, coef.size());
-  return decode_host(coef, l, p.scale);
+  return decode_host(coef, l, p.scale, imag);
 }
 
 template <class T> T* c_array(const std::vector<T>& v) {
@@ -1567,6 +1586,25 @@ int DecodeDouble(int plaintextID, double* out, int len) {
   });
 }
 
+int EncodeComplex(const float* values, int lenValues, int level, unsigned long scale) {
+  return guard([&] {
+    REQUIRE(lenValues % 2 == 0, "complex values come as (re, im) pairs");
+    return push_pt(encode_complex_values(values, lenValues / 2, level, (double)scale));
+  });
+}
+ArrayResultFloat DecodeComplex(int plaintextID) {
+  ArrayResultFloat r{nullptr, 0};
+  guard([&] {
+    std::vector<double> im;
+    std::vector<double> re = decode_pt(get_pt(plaintextID), &im);
+    std::vector<float> f(2 * re.size());
+    for (size_t i = 0; i < re.size(); i++) { f[2 * i] = (float)re[i]; f[2 * i + 1] = (float)im[i]; }
+    r.Data = c_array(f); r.Length = f.size();
+    return 0;
+  });
+  return r;
+}
+
 // ---- encryptor ----
 int NewEncryptor(void) { return guard([&] { sch().encryptor = true; return 0; }); }
 int NewDecryptor(void) { return guard([&] { sch().decryptor = true; return 0; }); }
@@ -1662,6 +1700,15 @@ int SubScalar(int ct, float v) { return guard([&] { add_const_inplace(get_ct(ct)
 int SubScalarNew(int ct, float v) {
   return guard([&] { auto c = copy_ct(get_ct(ct)); add_const_inplace(*c, (double)v, true); return push_ct(std::move(c)); });
 }
+// multiplication by i = by the monomial X^(N/2), key-free, in the NTT domain
+void mul_i_inplace(Cipher& c) {
+  Scheme& s = sch();
+  const size_t ps = (size_t)(c.level + 1) * s.N;
+  launch_mul_i(c.d.p, c.d.p, ps, 2, rows_q(c.level), s.iu.p, s.iup.p, s.niu.p, s.niup.p, s.d_mods.p, s.N, s.st);
+  sync();
+}
+int MulImaginaryUnit(int ct) { return guard([&] { mul_i_inplace(get_ct(ct)); return ct; }); }
+int MulImaginaryUnitNew(int ct) { return guard([&] { auto c = copy_ct(get_ct(ct)); mul_i_inplace(*c); return push_ct(std::move(c)); }); }
 int Negate(int ct) { return guard([&] { auto c = copy_ct(get_ct(ct)); mul_float_inplace(*c, -1.0); return push_ct(std::move(c)); }); }
 int MulRelinCiphertext(int a, int b) {
   return guard([&] { Cipher& c = get_ct(a); auto r = mul_relin_ct(c, get_ct(b)); c = std::move(*r); return a; });
@@ -2085,6 +2132,18 @@ int KernelTimingGet(const char* name, long* count, double* total_ms) {
     *total_ms = it == s.timing.acc.end() ? 0.0 : it->second.second;
     return 0;
   });
+}
+// device-memory counterparts of the reference's Go heap sampler: the pool
+// tracks every allocation, so the peak is exact rather than sampled
+unsigned long long LiveHeapBytes(void) { return g_pool ? (unsigned long long)g_pool->live : 0ULL; }
+int StartLiveHeapSampler(int intervalMs) {
+  (void)intervalMs;
+  return guard([&] { REQUIRE(g_pool, "no device pool"); sync(); g_pool->peak = g_pool->live; return 0; });
+}
+unsigned long long StopLiveHeapSampler(void) {
+  unsigned long long v = 0;
+  guard([&] { REQUIRE(g_pool, "no device pool"); sync(); v = g_pool->peak; return 0; });
+  return v;
 }
 int GetMemoryStats(uint64_t* live, uint64_t* cached, uint64_t* peak) {
   return guard([&] { REQUIRE(g_pool, "no device pool"); *live = g_pool->live; *cached = g_pool->cached; *peak = g_pool->peak; return 0; });

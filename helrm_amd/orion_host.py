@@ -475,6 +475,65 @@ class Activation:
         return CipherTensor(self.scheme, [b.EvaluatePolynomial(c, self.poly, int(scale)) for c in x.ids], x.n)
 
 
+# --------------------------------------------------------------------------
+# complex-lane upload (orion/core/lane_packing.py)
+# --------------------------------------------------------------------------
+
+def plan_packing(num_elements, num_slots):
+    """(real ciphertexts, packed ciphertexts) of a real vector (lane_packing.py:42-51)."""
+    num_real = -(-num_elements // num_slots)
+    return num_real, -(-num_real // 2)
+
+
+def pack_lanes(values, num_slots):
+    """Client side (lane_packing.py:59-81): chunk 2m in the real lane and chunk
+    2m+1 in the imaginary lane of packed chunk m, pre-scaled by 0.5.  Returns
+    (complex values, number of real chunks)."""
+    flat = np.asarray(values, dtype=np.float64).reshape(-1)
+    pad = (-len(flat)) % num_slots
+    if pad:
+        flat = np.concatenate([flat, np.zeros(pad)])
+    chunks = flat.reshape(-1, num_slots)
+    num_real = chunks.shape[0]
+    if num_real % 2:
+        chunks = np.concatenate([chunks, np.zeros((1, num_slots))])
+    return (0.5 * (chunks[0::2] + 1j * chunks[1::2])).reshape(-1), num_real
+
+
+def encode_complex(scheme, values, level, scale=None):
+    """Complex values, one plaintext per `slots` of them (EncodeComplex takes
+    interleaved fp32 (re, im) pairs)."""
+    z = np.asarray(values, dtype=np.complex128).reshape(-1)
+    slots = scheme.params.get_slots()
+    scale = scale or scheme.params.get_default_scale()
+    ids = []
+    for i in range(0, len(z), slots):
+        c = z[i:i + slots]
+        v = np.empty(2 * len(c), dtype=np.float32)
+        v[0::2], v[1::2] = c.real, c.imag
+        ids.append(scheme.backend.EncodeComplex(v, level, int(scale)))
+    return PlainTensor(scheme, ids, len(z))
+
+
+def unpack_lanes(scheme, packed, num_real):
+    """Server side (lane_packing.py:84-114): x = p + conj(p), y = -i (p - conj(p))
+    per packed ciphertext, the zero-padded partner of an odd count dropped."""
+    b = scheme.backend
+    real_ids = []
+    for pid in packed.ids:
+        conj = b.ConjugateNew(pid)
+        even = b.AddCiphertextNew(pid, conj)
+        diff = b.SubCiphertextNew(pid, conj)
+        b.MulImaginaryUnit(diff)
+        odd = b.Negate(diff)
+        b.DeleteCiphertext(conj)
+        b.DeleteCiphertext(diff)
+        real_ids.extend([even, odd])
+    for extra in real_ids[num_real:]:
+        b.DeleteCiphertext(extra)
+    return CipherTensor(scheme, real_ids[:num_real], num_real * scheme.params.get_slots())
+
+
 def embedding_pcmm(scheme, layer, selector):
     """One query: encode + encrypt the selector at the layer's level and run
     the embedding PCMM (HELRM.sparse, dlrm.py:226-230).  Returns (ct, pt_in)."""

@@ -67,6 +67,8 @@ int NewEncoder(void);                                                      /* en
 int Encode(const float* values, int lenValues, int level, unsigned long scale); /* encoder.go:15-30 */
 ArrayResultFloat Decode(int plaintextID);                                  /* encoder.go:32-47 */
 int DecodeDouble(int plaintextID, double* out, int len);                   /* [ext] Decode before the float cast */
+int EncodeComplex(const float* values, int lenValues, int level, unsigned long scale); /* encoder.go:50-70 ((re, im) pairs) */
+ArrayResultFloat DecodeComplex(int plaintextID);                           /* encoder.go:72-91 (interleaved re, im) */
 
 /* ---- encryptor -------------------------------------------------------------- */
 int NewEncryptor(void);              /* encryptor.go:9 */
@@ -102,6 +104,8 @@ int AddCiphertextNew(int ctID0, int ctID1);              /* evaluator.go:306-318
 int SubCiphertext(int ctID0, int ctID1);                 /* evaluator.go:320-327 */
 int SubCiphertextNew(int ctID0, int ctID1);              /* evaluator.go:329-341 */
 int Negate(int ciphertextID);                            /* evaluator.go:68-78 (Mul by -1.0: a new ciphertext) */
+int MulImaginaryUnitNew(int ciphertextID); /* cheddar_pybind.cu:1827-1833 (times i = X^(N/2), key-free) */
+int MulImaginaryUnit(int ciphertextID);    /* cheddar_pybind.cu:1834-1840 (in place) */
 int AddScalar(int ciphertextID, float scalar);           /* evaluator.go:148-154 (round(scalar * scale) into part 0) */
 int AddScalarNew(int ciphertextID, float scalar);        /* evaluator.go:156-166 */
 int SubScalar(int ciphertextID, float scalar);           /* evaluator.go:168-174 */
@@ -195,6 +199,11 @@ void* GetStream(void);                                            /* hipStream_t
 int KernelTimingEnable(int on);                                   /* HIP events around named launches */
 int KernelTimingGet(const char* name, long* count, double* total_ms);
 int GetMemoryStats(uint64_t* live, uint64_t* cached, uint64_t* peak);
+/* memstats.go:40-86: device-memory bytes held by the library's allocator (the
+ * reference samples the Go heap); the peak between Start and Stop is exact */
+unsigned long long LiveHeapBytes(void);
+int StartLiveHeapSampler(int intervalMs);
+unsigned long long StopLiveHeapSampler(void);
 
 #ifdef __cplusplus
 }

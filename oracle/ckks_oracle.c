@@ -564,10 +564,13 @@ static void fixed_point_crt(const orc_ctx* c, double value, double scale, const 
         }
     }
 }
-void orc_encode_f64(const orc_ctx* c, const double* v, int n, int level, double scale, int with_p, uint64_t* out) {
+/* Complex slots (Lattigo Encoder.Encode of []complex128, encoder.go:50-70):
+ * vi may be NULL (real input). */
+void orc_encode_complex_f64(const orc_ctx* c, const double* v, const double* vi, int n, int level, double scale, int with_p,
+                            uint64_t* out) {
     int N = c->N, slots = N / 2;
     double* re = (double*)xcalloc(sizeof(double) * slots); double* im = (double*)xcalloc(sizeof(double) * slots);
-    for (int i = 0; i < n && i < slots; i++) re[i] = v[i];
+    for (int i = 0; i < n && i < slots; i++) { re[i] = v[i]; if (vi) im[i] = vi[i]; }
     special_ifft(c, re, im, slots);
     int mi[MAXMOD]; int nm = with_p ? qp_list(c, level, mi) : q_list(c, level, mi);
     for (int i = 0; i < slots; i++) {
@@ -575,6 +578,17 @@ void orc_encode_f64(const orc_ctx* c, const double* v, int n, int level, double 
         fixed_point_crt(c, im[i], scale, mi, nm, out + i + slots, (size_t)N);
     }
     ntt_limbs(c, out, mi, nm);
+    free(re); free(im);
+}
+void orc_encode_f64(const orc_ctx* c, const double* v, int n, int level, double scale, int with_p, uint64_t* out) {
+    orc_encode_complex_f64(c, v, NULL, n, level, scale, with_p, out);
+}
+/* EncodeComplex's fp32 interleaved input [re0, im0, re1, im1, ...] of n values */
+void orc_encode_complex(const orc_ctx* c, const float* v, int n, int level, double scale, uint64_t* out) {
+    double* re = (double*)xmalloc(sizeof(double) * (n > 0 ? n : 1));
+    double* im = (double*)xmalloc(sizeof(double) * (n > 0 ? n : 1));
+    for (int i = 0; i < n; i++) { re[i] = (double)v[2 * i]; im[i] = (double)v[2 * i + 1]; }
+    orc_encode_complex_f64(c, re, im, n, level, scale, 0, out);
     free(re); free(im);
 }
 void orc_encode(const orc_ctx* c, const float* v, int n, int level, double scale, int with_p, uint64_t* out) {
@@ -637,7 +651,19 @@ static double big_to_double(const big_t* a) {
 
 /* Lattigo Encoder.Decode (float64 path): iNTT, centred CRT reconstruction to
  * a big integer, nearest double, divide by the scale, SpecialFFT. */
+static void decode_core(const orc_ctx* c, const uint64_t* pt, int level, double scale, double* out, double* out_im);
 void orc_decode_f64(const orc_ctx* c, const uint64_t* pt, int level, double scale, double* out) {
+    decode_core(c, pt, level, scale, out, NULL);
+}
+/* DecodeComplex (encoder.go:72-91): interleaved [re0, im0, re1, im1, ...] */
+void orc_decode_complex_f64(const orc_ctx* c, const uint64_t* pt, int level, double scale, double* out) {
+    int slots = c->N / 2;
+    double* re = (double*)xmalloc(sizeof(double) * slots); double* im = (double*)xmalloc(sizeof(double) * slots);
+    decode_core(c, pt, level, scale, re, im);
+    for (int i = 0; i < slots; i++) { out[2 * i] = re[i]; out[2 * i + 1] = im[i]; }
+    free(re); free(im);
+}
+static void decode_core(const orc_ctx* c, const uint64_t* pt, int level, double scale, double* out, double* out_im) {
     int N = c->N, slots = N / 2, nl = level + 1;
     int ql[MAXMOD]; q_list(c, level, ql);
     u64* coef = (u64*)xmalloc(8 * (size_t)nl * N);
@@ -680,6 +706,7 @@ void orc_decode_f64(const orc_ctx* c, const uint64_t* pt, int level, double scal
     for (int i = 0; i < slots; i++) { re[i] = vals[i]; im[i] = vals[i + slots]; }
     special_fft(c, re, im, slots);
     for (int i = 0; i < slots; i++) out[i] = re[i];
+    if (out_im) for (int i = 0; i < slots; i++) out_im[i] = im[i];
     free(re); free(im); free(vals); free(coef);
 }
 void orc_decode(const orc_ctx* c, const uint64_t* pt, int level, double scale, float* out) {
@@ -861,6 +888,21 @@ void orc_encrypt_seeded(const orc_ctx* c, const uint64_t* pt, int l, uint64_t se
         b[o] = addmod(submod(b[o], mulmod_b(&c->bar[i], a[o], c->s_ntt[o]), q), pt[o], q);
     }
     free(e);
+}
+/* Multiplication by the imaginary unit: by the monomial X^(N/2) (it takes
+ * the value i at every root zeta^(5^k)), key-free.  In the NTT domain slot j
+ * holds the evaluation at psi^e, e = 2 brv(j) + 1, where X^(N/2) is
+ * (psi^(N/2))^e = I^(e mod 4): I = psi^(N/2) for j < N/2, -I for j >= N/2. */
+void orc_mul_i(const orc_ctx* c, const uint64_t* ct, int l, int npoly, uint64_t* out) {
+    int N = c->N;
+    for (int i = 0; i <= l; i++) {
+        u64 q = c->mod[i];
+        u64 I = c->psi[(size_t)i * N + 1], nI = q - I;  /* table slot brv(N/2) = 1 holds psi^(N/2) */
+        for (int p = 0; p < npoly; p++) for (int x = 0; x < N; x++) {
+            size_t o = ((size_t)p * (l + 1) + i) * N + x;
+            out[o] = mulmod_b(&c->bar[i], ct[o], x < N / 2 ? I : nI);
+        }
+    }
 }
 void orc_decrypt(const orc_ctx* c, const uint64_t* ct, int l, uint64_t* pt) {
     int N = c->N; const u64* c0 = ct; const u64* c1 = ct + (size_t)(l + 1) * N;

@@ -79,6 +79,11 @@ void orc_decode_f64(const orc_ctx* c, const uint64_t* pt, int level,
 /* ---- encryptor --------------------------------------------------------- */
 void orc_encrypt(const orc_ctx* c, const uint64_t* pt, int level,
                  uint64_t enc_index, uint64_t* ct);
+void orc_encode_complex_f64(const orc_ctx* c, const double* v, const double* vi, int n, int level, double scale, int with_p,
+                            uint64_t* out);
+void orc_encode_complex(const orc_ctx* c, const float* v, int n, int level, double scale, uint64_t* out);
+void orc_decode_complex_f64(const orc_ctx* c, const uint64_t* pt, int level, double scale, double* out);
+void orc_mul_i(const orc_ctx* c, const uint64_t* ct, int l, int npoly, uint64_t* out);
 void orc_expand_seeded_a(const orc_ctx* c, int l, uint64_t seed, uint64_t* a);
 void orc_encrypt_seeded(const orc_ctx* c, const uint64_t* pt, int l, uint64_t seed, uint64_t enc, uint64_t* ct);
 void orc_decrypt(const orc_ctx* c, const uint64_t* ct, int level, uint64_t* pt);

@@ -62,6 +62,9 @@ def lib():
             "orc_encrypt": ([vp, u64p, ctypes.c_int, ctypes.c_uint64, u64p], None),
             "orc_decrypt": ([vp, u64p, ctypes.c_int, u64p], None),
             "orc_expand_seeded_a": ([vp, ctypes.c_int, ctypes.c_uint64, u64p], None),
+            "orc_encode_complex": ([vp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_double, u64p], None),
+            "orc_decode_complex_f64": ([vp, u64p, ctypes.c_int, ctypes.c_double, dp], None),
+            "orc_mul_i": ([vp, u64p, ctypes.c_int, ctypes.c_int, u64p], None),
             "orc_encrypt_seeded": ([vp, u64p, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64, u64p], None),
             "orc_add": ([vp, u64p, u64p, ctypes.c_int, ctypes.c_int, u64p], None),
             "orc_rescale": ([vp, u64p, ctypes.c_int, u64p], None),
@@ -243,6 +246,29 @@ class Oracle:
         lib().orc_encrypt(self.ctx, _p(pt), level, int(enc_index), _p(ct))
         return ct
 
+    def encode_complex(self, values, level, scale):
+        """EncodeComplex: complex slot values (fp32 real and imaginary parts, as
+        they cross the ABI interleaved)."""
+        z = np.asarray(values, dtype=np.complex128).reshape(-1)
+        v = np.empty(2 * len(z), dtype=np.float32)
+        v[0::2], v[1::2] = z.real, z.imag
+        out = np.zeros((level + 1, self.N), dtype=np.uint64)
+        lib().orc_encode_complex(self.ctx, _p(v, fp), len(z), level, float(scale), _p(out))
+        return out
+
+    def decode_complex(self, pt, level, scale):
+        pt = np.ascontiguousarray(pt, dtype=np.uint64)
+        out = np.zeros(2 * self.slots, dtype=np.float64)
+        lib().orc_decode_complex_f64(self.ctx, _p(pt), level, float(scale), _p(out, dp))
+        return out[0::2] + 1j * out[1::2]
+
+    def mul_i(self, ct, level):
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        npoly = ct.size // ((level + 1) * self.N)
+        out = np.zeros_like(ct)
+        lib().orc_mul_i(self.ctx, _p(ct), level, npoly, _p(out))
+        return out
+
     def encrypt_seeded(self, pt, level, seed, enc_index):
         """Secret-key encryption whose `a` part is expanded from `seed`."""
         pt = np.ascontiguousarray(pt, dtype=np.uint64)
@@ -334,6 +360,13 @@ class Oracle:
         ct = np.ascontiguousarray(ct, dtype=np.uint64)
         out = np.zeros((2, level, self.N), dtype=np.uint64)
         lib().orc_rescale(self.ctx, _p(ct), level, _p(out))
+        return out
+
+    def automorphism(self, ct, level, galel):
+        """Key-switched automorphism X -> X^galel (2N - 1: complex conjugation)."""
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        out = np.zeros((2, level + 1, self.N), dtype=np.uint64)
+        lib().orc_automorphism_ct(self.ctx, _p(ct), level, int(galel), _p(out))
         return out
 
     def rotate(self, ct, level, k):

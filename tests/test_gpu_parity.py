@@ -133,6 +133,114 @@ def test_encrypt_seeded(ctx):
         ctx.lib.DeletePlaintext(pt)
 
 
+def test_encode_complex(ctx):
+    """EncodeComplex / DecodeComplex (encoder.go:50-91): complex slots as
+    interleaved fp32 pairs, bit-exact with the restatement; a partly filled
+    vector; decodes to the input."""
+    level = ctx.L - 1
+    for n in (ctx.slots, ctx.slots // 3):
+        z = (ctx.rng.uniform(-1, 1, n) + 1j * ctx.rng.uniform(-1, 1, n)).astype(np.complex64)
+        v = np.empty(2 * n, dtype=np.float32)
+        v[0::2], v[1::2] = z.real, z.imag
+        scale = 1 << ctx.logscale
+        pt = ctx.lib.EncodeComplex(v, level, scale)
+        assert_equal_u64(ctx.lib.export_plaintext(pt), ctx.orc.encode_complex(z, level, float(scale)), f"EncodeComplex {n}")
+        dec = np.asarray(ctx.lib.DecodeComplex(pt), dtype=np.float64)
+        want = ctx.orc.decode_complex(ctx.orc.encode_complex(z, level, float(scale)), level, float(scale))
+        np.testing.assert_array_equal(dec[0::2].astype(np.float32), want.real.astype(np.float32))
+        np.testing.assert_array_equal(dec[1::2].astype(np.float32), want.imag.astype(np.float32))
+        assert np.abs((dec[0::2] + 1j * dec[1::2])[:n] - z).max() < 1e-4
+        ctx.lib.DeletePlaintext(pt)
+
+
+def test_conjugate_and_mul_imaginary_unit(ctx):
+    """ConjugateNew (evaluator.go:116-128, X -> X^(2N-1) key-switched) and
+    MulImaginaryUnit(New) (times X^(N/2)) bit-exact with the restatement."""
+    level = ctx.L - 1
+    z = (ctx.rng.uniform(-1, 1, ctx.slots) + 1j * ctx.rng.uniform(-1, 1, ctx.slots)).astype(np.complex64)
+    v = np.empty(2 * ctx.slots, dtype=np.float32)
+    v[0::2], v[1::2] = z.real, z.imag
+    scale = 1 << ctx.logscale
+    pt = ctx.lib.EncodeComplex(v, level, scale)
+    ctx.lib.SetEncryptionCounter(11)
+    ct = ctx.lib.Encrypt(pt)
+    ref = ctx.orc.encrypt(ctx.orc.encode_complex(z, level, float(scale)), level, 11)
+    assert_equal_u64(ctx.lib.export_ciphertext(ct), ref, "encrypt complex")
+    cj = ctx.lib.ConjugateNew(ct)
+    assert_equal_u64(ctx.lib.export_ciphertext(cj), ctx.orc.automorphism(ref, level, 2 * ctx.N - 1), "ConjugateNew")
+    mi = ctx.lib.MulImaginaryUnitNew(ct)
+    want_i = ctx.orc.mul_i(ref, level)
+    assert_equal_u64(ctx.lib.export_ciphertext(mi), want_i, "MulImaginaryUnitNew")
+    assert ctx.lib.MulImaginaryUnit(ct) == ct
+    assert_equal_u64(ctx.lib.export_ciphertext(ct), want_i, "MulImaginaryUnit")
+    dec = np.asarray(ctx.lib.DecodeComplex(ctx.lib.Decrypt(ct)), dtype=np.float64)
+    assert np.abs((dec[0::2] + 1j * dec[1::2]) - 1j * z).max() < 1e-3
+    for c in (cj, mi, ct):
+        ctx.lib.DeleteCiphertext(c)
+    ctx.lib.DeletePlaintext(pt)
+
+
+def test_lane_packed_upload(ctx):
+    """orion/core/lane_packing.py: a real vector of 3 ciphertext chunks goes up
+    as 2 complex-lane ciphertexts (0.5 pre-scale), and the server splits them
+    with one conjugation each: x = p + conj(p), y = -(i (p - conj(p))).  Each
+    rebuilt ciphertext is bit-exact with the same steps on the restatement and
+    decrypts to its chunk."""
+    from helrm_amd import orion_host as oh
+    level = ctx.L - 1
+    S = ctx.slots
+    vals = ctx.rng.uniform(-1, 1, 3 * S - 5)
+    packed, nreal = oh.pack_lanes(vals, S)
+    assert nreal == 3 and len(packed) == 2 * S
+
+    class _Params:
+        def get_slots(self):
+            return S
+
+        def get_default_scale(self):
+            return 1 << ctx.logscale
+
+    class _Scheme:
+        backend, params = ctx.lib, _Params()
+    sch = _Scheme()
+    pt = oh.encode_complex(sch, packed, level)
+    ctx.lib.SetEncryptionCounter(20)
+    up = oh.CipherTensor(sch, [ctx.lib.Encrypt(i) for i in pt.ids], pt.n)
+    real = oh.unpack_lanes(sch, up, nreal)
+    assert len(real.ids) == 3
+    scale = float(1 << ctx.logscale)
+    q = np.array(ctx.q[:level + 1], dtype=np.uint64)[None, :, None]
+    want = []
+    for m in range(2):
+        p = ctx.orc.encrypt(ctx.orc.encode_complex(packed[m * S:(m + 1) * S], level, scale), level, 20 + m)
+        cj = ctx.orc.automorphism(p, level, 2 * ctx.N - 1)
+        even = ctx.orc.add(p, cj, level)
+        diff = ctx.orc.add(p, (q - cj) % q, level)
+        odd = (q - ctx.orc.mul_i(diff, level)) % q
+        want += [even, odd]
+    padded = np.concatenate([vals, np.zeros(3 * S - len(vals))])
+    for r, cid in enumerate(real.ids):
+        assert_equal_u64(ctx.lib.export_ciphertext(cid), want[r], f"rebuilt chunk {r}")
+        dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(cid)), dtype=np.float64)
+        assert np.abs(dec - padded[r * S:(r + 1) * S]).max() < 1e-3
+    real.free()
+    up.free()
+
+
+def test_live_heap_sampler(ctx):
+    """memstats.go:40-86 counterparts: live device bytes, and the exact peak
+    between StartLiveHeapSampler and StopLiveHeapSampler."""
+    live0 = ctx.lib.LiveHeapBytes()
+    assert live0 > 0
+    assert ctx.lib.StartLiveHeapSampler(10) == 0
+    pt = ctx.lib.Encode([0.5] * 8, ctx.L - 1, 1 << ctx.logscale)
+    ct = ctx.lib.Encrypt(pt)
+    ctx.lib.DeleteCiphertext(ct)
+    ctx.lib.DeletePlaintext(pt)
+    peak = ctx.lib.StopLiveHeapSampler()
+    assert peak >= live0 + 2 * ctx.L * ctx.N * 8
+
+
 def test_encrypt_decrypt(ctx):
     level = ctx.L - 1
     ct, ref, vals = ctx.fresh_ct(level, 3)

@@ -246,6 +246,56 @@ def test_encoding_is_canonical_embedding(small):
     np.testing.assert_allclose(small.decode_f64(pt, 0, scale), vals, atol=1e-6)
 
 
+def test_complex_encoding_is_canonical_embedding(small):
+    """EncodeComplex: the polynomial takes the complex slot value z_j at
+    zeta^(5^j) (and its conjugate at zeta^(-5^j)); DecodeComplex returns it."""
+    N, S = small.N, small.slots
+    rng = np.random.default_rng(18)
+    z = (rng.uniform(-1, 1, S) + 1j * rng.uniform(-1, 1, S)).astype(np.complex64)
+    scale = 2.0 ** 30
+    pt = small.encode_complex(z, 0, scale)
+    coeff = small.to_coeff(pt, 0)[0]
+    q = small.q[0]
+    c = np.array([int(v) - q if int(v) > q // 2 else int(v) for v in coeff], dtype=np.float64)
+    for j in range(S):
+        r = np.exp(1j * np.pi * pow(5, j, 2 * N) / N)
+        slot = np.sum(c * r ** np.arange(N)) / scale
+        assert abs(slot - z[j]) < 1e-6
+        assert abs(np.sum(c * np.conj(r) ** np.arange(N)) / scale - np.conj(z[j])) < 1e-6
+    np.testing.assert_allclose(small.decode_complex(pt, 0, scale), z, atol=1e-6)
+    # a purely real input encodes exactly as Encode does
+    zr = z.real.astype(np.float32)
+    np.testing.assert_array_equal(small.encode_complex(zr.astype(np.complex64), 2, scale), small.encode(zr, 2, scale))
+
+
+def test_mul_i_is_the_monomial_x_to_the_n_over_2(small):
+    """Multiplication by i is multiplication by X^(N/2): decrypted, every
+    coefficient moves N/2 places up, negated when it wraps (X^N = -1)."""
+    level = small.L - 1
+    N = small.N
+    vals = np.random.default_rng(21).uniform(-1, 1, small.slots).astype(np.float32)
+    ct = small.encrypt(small.encode(vals, level, 2.0 ** 30), level, 2)
+    got = small.to_coeff(small.decrypt(small.mul_i(ct, level), level), level)
+    base = small.to_coeff(small.decrypt(ct, level), level)
+    for i, q in enumerate(small.q[:level + 1]):
+        want = np.concatenate([(q - base[i][N // 2:]) % q, base[i][:N // 2]]).astype(np.uint64)
+        np.testing.assert_array_equal(got[i], want)
+    dec = small.decode_complex(small.decrypt(small.mul_i(ct, level), level), level, 2.0 ** 30)
+    np.testing.assert_allclose(dec, 1j * vals, atol=1e-5)
+
+
+def test_conjugation_conjugates_every_slot(mid):
+    """The automorphism X -> X^(2N-1) (Lattigo Conjugate) decrypts to the
+    complex conjugate of every slot."""
+    level = mid.L - 1
+    rng = np.random.default_rng(33)
+    z = (rng.uniform(-1, 1, mid.slots) + 1j * rng.uniform(-1, 1, mid.slots)).astype(np.complex64)
+    scale = 2.0 ** 30
+    ct = mid.encrypt(mid.encode_complex(z, level, scale), level, 4)
+    out = mid.automorphism(ct, level, 2 * mid.N - 1)
+    np.testing.assert_allclose(mid.decode_complex(mid.decrypt(out, level), level, scale), np.conj(z), atol=1e-4)
+
+
 # ---------------------------------------------------------------- encryption, keys
 
 
