@@ -209,3 +209,21 @@ def test_wire_store_round_trip(tmp_path):
     for k, v in blobs.items():
         np.testing.assert_array_equal(back[k], v)
         assert back[k].dtype == np.uint8
+
+
+@pytest.mark.parametrize("n,slots", [(10, 4), (8, 4), (3, 4), (4096 * 3 - 5, 4096)])
+def test_pack_lanes_pairs_chunks(n, slots):
+    """lane_packing.py:42-81: chunk 2m in the real lane, chunk 2m+1 in the
+    imaginary lane of packed chunk m, pre-scaled by 0.5; an odd chunk count is
+    padded with a zero partner; p + conj(p) and -i (p - conj(p)) give the chunks
+    back."""
+    v = np.random.default_rng(n).uniform(-1, 1, n)
+    packed, nreal = oh.pack_lanes(v, slots)
+    assert nreal == -(-n // slots)
+    assert oh.plan_packing(n, slots) == (nreal, -(-nreal // 2))
+    assert len(packed) == -(-nreal // 2) * slots
+    flat = np.concatenate([v, np.zeros(-(-nreal // 2) * 2 * slots - n)])
+    for m in range(len(packed) // slots):
+        p = packed[m * slots:(m + 1) * slots]
+        np.testing.assert_allclose(p + np.conj(p), flat[2 * m * slots:(2 * m + 1) * slots], atol=1e-15)
+        np.testing.assert_allclose((-1j * (p - np.conj(p))).real, flat[(2 * m + 1) * slots:(2 * m + 2) * slots], atol=1e-15)
