@@ -188,6 +188,18 @@ def lt_roofline_bytes(lib, layer, N, K, w=8):
                              f=layer.output_rotations, dnum=(Lq + K - 1) // K, w=w), lti
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def describe(cfg):
     if cfg["kind"] == "dlrm":
         return ("encrypted HE-LRM forward at batch 1: bottom MLP 13-512-256-64-16, 26-table embedding PCMM "
@@ -281,6 +293,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ntt-microbench", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-single-thread-baseline", action="store_true",
+                    help="skip the one-thread timing of the CPU restatement's sample")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--seeded-upload", action="store_true",
                     help="upload the selector as (b, seed) and rebuild a on the device inside every step")
@@ -420,7 +434,12 @@ def main():
         v, t_cpu, sample, tm = cpu_baseline(lib.GetModuliChain(), lib.GetAuxModuliChain(), cfg["h"], 1, d,
                                              w.input, w.layer.level, cfg["logscale"], threads, per_step)
         cpu = {"value": v, "unit": unit, "cores": threads, "kind": "port", "sample": sample,
-               "seconds_per_pcmm": t_cpu}
+               "seconds_per_pcmm": t_cpu, "cpu_model": cpu_model(), "host_cpus": os.cpu_count()}
+        if not args.no_single_thread_baseline:
+            # the reference's Lattigo timing runs with GOMAXPROCS=1 (one core)
+            v1, t1, sample1, _ = cpu_baseline(lib.GetModuliChain(), lib.GetAuxModuliChain(), cfg["h"], 1, d,
+                                              w.input, w.layer.level, cfg["logscale"], 1, per_step)
+            cpu["single_thread"] = {"value": v1, "seconds_per_pcmm": t1, "sample": sample1}
 
     ntt = None if args.no_ntt_microbench else ntt_microbench(lib)
 
