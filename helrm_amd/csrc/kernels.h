@@ -123,7 +123,6 @@ void launch_keymac(const KeyMacArgs& a, int batch, hipStream_t st);
 void launch_giant_acc(const GiantAccArgs& a, hipStream_t st);
 void launch_diag_mac(const DiagMacArgs& a, hipStream_t st);
 void launch_rescale_spread(u64* t, const u64* u, int l, u64 half, const ModC* mods, int N, hipStream_t st);
-void launch_rescale_combine(u64* out, const u64* x, const u64* t, int l, const u64* inv, const u64* invp, const ModC* mods, int N, hipStream_t st);
 void launch_sample_uniform(u64* out, RowMap rm, u64 seed, u64 stream, const ModC* mods, int N, hipStream_t st);
 void launch_sample_cbd(u64* out, RowMap rm, u64 seed, u64 stream, const ModC* mods, int N, bool add, hipStream_t st);
 void launch_signed_rows(u64* out, RowMap rm, const int8_t* v, const ModC* mods, int N, hipStream_t st);

@@ -544,17 +544,6 @@ __global__ void rescale_spread_kernel(u64* __restrict__ t, const u64* __restrict
 void launch_rescale_spread(u64* t, const u64* u, int l, u64 half, const ModC* mods, int N, hipStream_t st) {
   hipLaunchKernelGGL(rescale_spread_kernel, dim3(N / 256, l, 2), dim3(256), 0, st, t, u, l, half, mods, N);
 }
-__global__ void rescale_combine_kernel(u64* __restrict__ out, const u64* __restrict__ x, const u64* __restrict__ t, int l,
-                                       const u64* __restrict__ inv, const u64* __restrict__ invp, const ModC* __restrict__ mods, int N) {
-  int j = blockIdx.x * blockDim.x + threadIdx.x;
-  int i = blockIdx.y, p = blockIdx.z;
-  u64 q = mods[i].q;
-  u64 v = sub_mod(x[((size_t)p * (l + 1) + i) * N + j], t[((size_t)p * l + i) * N + j], q);
-  out[((size_t)p * l + i) * N + j] = shoup_mul(v, inv[i], invp[i], q);
-}
-void launch_rescale_combine(u64* out, const u64* x, const u64* t, int l, const u64* inv, const u64* invp, const ModC* mods, int N, hipStream_t st) {
-  hipLaunchKernelGGL(rescale_combine_kernel, dim3(N / 256, l, 2), dim3(256), 0, st, out, x, t, l, inv, invp, mods, N);
-}
 
 // ---------------------------------------------------------------------------
 // Sampling (counter PRNG shared with the key/encryption specification):

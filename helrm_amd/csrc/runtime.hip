@@ -1044,9 +1044,10 @@ std::unique_ptr<Cipher> rescale_ct(const Cipher& ct) {
   DU64 u((size_t)2 * N), t((size_t)2 * l * N);
   ntt_oop(ct.d.p + (size_t)l * N, (size_t)(l + 1) * N, u.p, N, 2, RowMap{1, 1, l, 0, 0, 0}, false);
   launch_rescale_spread(t.p, u.p, l, s.mod[l] >> 1, s.d_mods.p, N, s.st);
-  ntt(t.p, (size_t)l * N, 2, rows_q(l - 1), true);
   auto out = new_ct(l - 1, ct.scale / (double)s.mod[l]); out->logslots = ct.logslots;
-  launch_rescale_combine(out->d.p, ct.d.p, t.p, l, s.rs_inv.p + (size_t)l * s.L, s.rs_invp.p + (size_t)l * s.L, s.d_mods.p, N, s.st);
+  // forward transform of t whose row pass ends in out_i = (x_i - t_i) * q_l^-1
+  launch_ntt_moddown(t.p, (size_t)l * N, 2, l - 1, s.logN, ct.d.p, (size_t)(l + 1) * N, out->d.p, (size_t)l * N, nullptr, 0, 0,
+                     nullptr, s.rs_inv.p + (size_t)l * s.L, s.rs_invp.p + (size_t)l * s.L, s.tw, s.st);
   return out;
 }
 // Lattigo ckks Rescale: divide by the last moduli while the scale stays >= default/2
