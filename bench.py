@@ -298,6 +298,10 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--seeded-upload", action="store_true",
                     help="upload the selector as (b, seed) and rebuild a on the device inside every step")
+    ap.add_argument("--no-lt-prerescale", action="store_true",
+                    help="transforms return the un-rescaled result and the host rescales (Lattigo's convention); "
+                         "by default they return the rescaled one (lt_output_prerescaled: the first rescale fused "
+                         "into the final ModDown, the same residues)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (PMC counter calibration) and exit")
     args = ap.parse_args()
@@ -319,6 +323,8 @@ def main():
     t_setup = time.perf_counter() - t_setup
     info = w.shape_info()
     cfg = CONFIGS[args.workload]
+    lib.set_lt_output_prerescaled(not args.no_lt_prerescale)
+    prerescaled = bool(lib.lt_output_prerescaled)
     if args.seeded_upload:
         w.use_seeded_upload(0x5EED + args.seed)
     sel = w.ct_sparse if cfg["kind"] == "dlrm" else w.ct_in
@@ -464,6 +470,7 @@ def main():
         "kernels": kt,
         "linear_transforms": lt_shapes,
         "selector_upload": upload,
+        "lt_output_prerescaled": prerescaled,
         "roofline": roofline,
         "kernel_rooflines": kernel_rooflines,
         "cpu_baseline": cpu,

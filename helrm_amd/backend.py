@@ -217,6 +217,8 @@ _SIGNATURES = {
     "NewLinearTransformEvaluator": ([], _I),
     "GenerateLinearTransform": ([_PI, _I, _PF, _I, _I, _c.c_float, _c.c_char_p], _I),
     "EvaluateLinearTransform": ([_I, _I], _I),
+    "SetLinearTransformPrerescale": ([_I], _I),
+    "GetLinearTransformPrerescale": ([], _I),
     "GetLinearTransformRotationKeys": ([_I], ArrayResultInt),
     "GenerateLinearTransformRotationKey": ([_I], _I),
     "DeleteLinearTransform": ([_I], _I),
@@ -305,14 +307,24 @@ class DeviceBuffer:
 class HipLibrary:
     """Drop-in for orion.backend.lattigo.bindings.LattigoLibrary."""
 
-    # EvaluateLinearTransform returns an un-rescaled ciphertext, as Lattigo's
-    # (orion/backend/python/lt_evaluator.py:268-273 reads this flag).
-    lt_output_prerescaled = False
-
     def __init__(self):
         self.lib = load_library()
         for name, (argtypes, restype) in _SIGNATURES.items():
             setattr(self, name, HipFunction(getattr(self.lib, name), list(argtypes), restype))
+
+    # orion/backend/python/lt_evaluator.py:262-273 reads this flag: False (the
+    # default, Lattigo's convention) -- EvaluateLinearTransform returns the
+    # un-rescaled result and the caller rescales; True (the convention of the
+    # reference's double-hoisted Cheddar path, cheddar/bindings.py:183-187) --
+    # the result comes back rescaled, here with the first division fused into
+    # the transform's final ModDown and the same residues as the two steps.
+    # The flag belongs to the current scheme (a new scheme starts at False).
+    @property
+    def lt_output_prerescaled(self):
+        return self.lib.GetLinearTransformPrerescale() == 1
+
+    def set_lt_output_prerescaled(self, on):
+        self.SetLinearTransformPrerescale(1 if on else 0)
 
     # orion/backend/lattigo/bindings.py:127-138
     def setup_bindings(self, orion_params):

@@ -123,6 +123,12 @@ void launch_keymac(const KeyMacArgs& a, int batch, hipStream_t st);
 void launch_giant_acc(const GiantAccArgs& a, hipStream_t st);
 void launch_diag_mac(const DiagMacArgs& a, hipStream_t st);
 void launch_rescale_spread(u64* t, const u64* u, int l, u64 half, const ModC* mods, int N, hipStream_t st);
+// ModDown + rescale: rows i < l of the coefficient-domain extension ext become
+// ext_i + P * t_i, t the rescale's spread of the ModDown result's row l
+// ((xl - ext_l) * P^-1 mod q_l); ext and xl have `batch` entries.
+void launch_moddown_rescale_spread(u64* ext, size_t e_bstride, const u64* xl, size_t x_bstride, int l, u64 half, u64 pinvl,
+                                   u64 pinvlp, const u64* pmod_w, const u64* pmod_wp, const ModC* mods, int N, int batch,
+                                   hipStream_t st);
 void launch_sample_uniform(u64* out, RowMap rm, u64 seed, u64 stream, const ModC* mods, int N, hipStream_t st);
 void launch_sample_cbd(u64* out, RowMap rm, u64 seed, u64 stream, const ModC* mods, int N, bool add, hipStream_t st);
 void launch_signed_rows(u64* out, RowMap rm, const int8_t* v, const ModC* mods, int N, hipStream_t st);

@@ -545,6 +545,38 @@ void launch_rescale_spread(u64* t, const u64* u, int l, u64 half, const ModC* mo
   hipLaunchKernelGGL(rescale_spread_kernel, dim3(N / 256, l, 2), dim3(256), 0, st, t, u, l, half, mods, N);
 }
 
+// ModDown followed by a rescale, in the coefficient domain of the extension.
+// ext[p] holds [x]_P extended to rows q_0..q_l (coefficient domain) and
+// xl[p] row l of x (coefficient domain).  Row l of the ModDown result is
+//   y = (xl - ext_l) * P^-1 mod q_l
+// (the coefficients the rescale would get from the inverse NTT of that row),
+// and the rescale subtracts t_i = ([y + half]_{q_l} - half) mod q_i; so that
+// one forward NTT and one (P q_l)^-1 finish both steps, rows i < l become
+//   ext_i + P * t_i mod q_i                (in place).
+__global__ void moddown_rescale_spread_kernel(u64* __restrict__ ext, size_t e_bstride, const u64* __restrict__ xl,
+                                              size_t x_bstride, int l, u64 half, u64 pinvl, u64 pinvlp,
+                                              const u64* __restrict__ pmod_w, const u64* __restrict__ pmod_wp,
+                                              const ModC* __restrict__ mods, int N) {
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
+  const int i = blockIdx.y, p = blockIdx.z;
+  u64* e = ext + (size_t)p * e_bstride;
+  const u64 ql = mods[l].q;
+  const u64 y = shoup_mul(sub_mod(xl[(size_t)p * x_bstride + x], e[(size_t)l * N + x], ql), pinvl, pinvlp, ql);
+  const u64 w = add_mod(y, half, ql);
+  const ModC mc = mods[i];
+  const u64 wr = mont_mul(w, mc.rmod, mc.q, mc.qinv);  // w mod q_i
+  const u64 hr = mont_mul(half, mc.rmod, mc.q, mc.qinv);
+  const u64 t = sub_mod(wr, hr, mc.q);
+  u64* ei = e + (size_t)i * N + x;
+  *ei = add_mod(*ei, shoup_mul(t, pmod_w[i], pmod_wp[i], mc.q), mc.q);
+}
+void launch_moddown_rescale_spread(u64* ext, size_t e_bstride, const u64* xl, size_t x_bstride, int l, u64 half, u64 pinvl,
+                                   u64 pinvlp, const u64* pmod_w, const u64* pmod_wp, const ModC* mods, int N, int batch,
+                                   hipStream_t st) {
+  hipLaunchKernelGGL(moddown_rescale_spread_kernel, dim3(N / 256, l, batch), dim3(256), 0, st, ext, e_bstride, xl, x_bstride,
+                     l, half, pinvl, pinvlp, pmod_w, pmod_wp, mods, N);
+}
+
 // ---------------------------------------------------------------------------
 // Sampling (counter PRNG shared with the key/encryption specification):
 //   rand64(seed, stream, ctr) = mix(mix(seed + G*(stream+1)) ^ (ctr*M1 + M2))

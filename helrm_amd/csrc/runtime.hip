@@ -260,6 +260,11 @@ struct Scheme {
   // per-modulus constants (Shoup pairs indexed by modulus)
   DU64 pmod_w, pmod_wp, pinv_w, pinv_wp, p0inv_w, p0inv_wp, pmod_plain;
   DU64 rs_inv, rs_invp;  // [l][i] q_l^-1 mod q_i
+  DU64 prs_inv, prs_invp;  // [l][i] (P q_l)^-1 mod q_i
+  std::vector<u64> pinv_h, pinv_hp;  // [i] P^-1 mod q_i and its Shoup companion (host copies)
+  // EvaluateLinearTransform returns the rescaled result (ModDown and rescale
+  // fused), as backends that advertise lt_output_prerescaled do
+  bool lt_prerescale = false;
   DU64 iu, iup, niu, niup;  // [mod] psi^(N/2) (a square root of -1), its negation, Shoup companions
   std::map<std::pair<int, int>, std::unique_ptr<BConvHost>> bconv;
   std::map<u64, DevArray<uint32_t>> perms, perm_invs;
@@ -487,6 +492,29 @@ void mod_down(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t
   // forward transform of the extension fused with (x - ext) * P^-1 (+ add), gathered through perm
   launch_ntt_moddown(ext.p, (size_t)(l + 1) * N, batch, l, s.logN, x, x_bstride, out, o_bstride, add, a_bstride,
                      add_batches, perm_inv, s.pinv_w.p, s.pinv_wp.p, s.tw, s.st);
+}
+
+// out[b] (Q rows 0..l-1, stride o_bstride) = Rescale(ModDown(x[b])) for the
+// QP polynomials x[b] at level l, word for word what mod_down followed by
+// rescale_ct computes: the ModDown result's row l is formed in the coefficient
+// domain from the inverse transform of x's row l and the extension of [x]_P,
+// the rescale's correction t is spread from it, and one forward transform of
+// ext_i + P t_i ends in (x_i - NTT(ext_i + P t_i)) * (P q_l)^-1 -- the
+// rescale's own inverse and forward transforms are not needed.
+void mod_down_rescale(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t o_bstride) {
+  Scheme& s = sch();
+  const int N = s.N, K = s.K;
+  REQUIRE(l >= 1, "cannot rescale: ciphertext already at level 0");
+  DU64 pcq((size_t)batch * (K + 1) * N), ext((size_t)batch * (l + 1) * N);
+  // rows l (q_l) and l+1.. (P) of x are consecutive: one inverse transform
+  ntt_oop(x + (size_t)l * N, x_bstride, pcq.p, (size_t)(K + 1) * N, batch, RowMap{K + 1, 1, l, s.L, 0, 0}, false);
+  BConvHost& bt = bconv_table(s.L, s.L + K);
+  launch_bconv(pcq.p + N, (size_t)(K + 1) * N, K, bt.dtab.p, ext.p, (size_t)(l + 1) * N, batch, rows_q(l), s.d_mods.p, N, false,
+               s.st);
+  launch_moddown_rescale_spread(ext.p, (size_t)(l + 1) * N, pcq.p, (size_t)(K + 1) * N, l, s.mod[l] >> 1, s.pinv_h[l],
+                                s.pinv_hp[l], s.pmod_w.p, s.pmod_wp.p, s.d_mods.p, N, batch, s.st);
+  launch_ntt_moddown(ext.p, (size_t)(l + 1) * N, batch, l - 1, s.logN, x, x_bstride, out, o_bstride, nullptr, 0, 0, nullptr,
+                     s.prs_inv.p + (size_t)l * s.L, s.prs_invp.p + (size_t)l * s.L, s.tw, s.st);
 }
 
 const u64* key_ptr(u64 galel, bool for_lt) {
@@ -824,6 +852,14 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
     for (int l = 1; l < s.L; l++)
       for (int i = 0; i < l; i++) { u64 v = invmod(s.mod[l] % s.mod[i], s.mod[i]); ri[(size_t)l * s.L + i] = v; rip[(size_t)l * s.L + i] = shoup(v, s.mod[i]); }
     up(s.rs_inv, ri); up(s.rs_invp, rip);
+    std::vector<u64> pri((size_t)s.L * s.L, 0), prip((size_t)s.L * s.L, 0);
+    for (int l = 1; l < s.L; l++)
+      for (int i = 0; i < l; i++) {
+        const u64 v = mulmod(pin[i], ri[(size_t)l * s.L + i], s.mod[i]);
+        pri[(size_t)l * s.L + i] = v; prip[(size_t)l * s.L + i] = shoup(v, s.mod[i]);
+      }
+    up(s.prs_inv, pri); up(s.prs_invp, prip);
+    s.pinv_h.assign(pin.begin(), pin.end()); s.pinv_hp.assign(pinp.begin(), pinp.end());
     init_encoder(s);
   } catch (...) {
     S = old;
@@ -1050,13 +1086,18 @@ std::unique_ptr<Cipher> rescale_ct(const Cipher& ct) {
                      nullptr, s.rs_inv.p + (size_t)l * s.L, s.rs_invp.p + (size_t)l * s.L, s.tw, s.st);
   return out;
 }
-// Lattigo ckks Rescale: divide by the last moduli while the scale stays >= default/2
-std::unique_ptr<Cipher> rescale_lattigo(const Cipher& ct) {
+// Number of moduli Lattigo's ckks Rescale divides by: the last ones, while
+// the scale stays >= default/2
+int lattigo_rescale_count(double scale, int level) {
   Scheme& s = sch();
-  REQUIRE(ct.level >= 1, "cannot rescale: ciphertext already at level 0");
-  double minscale = std::ldexp(1.0, s.logscale) / 2.0;
-  double sc = ct.scale; int lvl = ct.level, nb = 0;
+  const double minscale = std::ldexp(1.0, s.logscale) / 2.0;
+  double sc = scale; int lvl = level, nb = 0;
   while (lvl >= 1) { double ns = sc / (double)s.mod[lvl]; if (ns < minscale) break; sc = ns; lvl--; nb++; }
+  return nb;
+}
+std::unique_ptr<Cipher> rescale_lattigo(const Cipher& ct) {
+  REQUIRE(ct.level >= 1, "cannot rescale: ciphertext already at level 0");
+  const int nb = lattigo_rescale_count(ct.scale, ct.level);
   if (nb == 0) return copy_ct(ct);
   std::unique_ptr<Cipher> cur = rescale_ct(ct);
   for (int i = 1; i < nb; i++) cur = rescale_ct(*cur);
@@ -1189,7 +1230,9 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
 // baby rotations, one fused diagonal-MAC pass producing every giant group's
 // QP accumulators, batched ModDown + decomposition of the giant groups' c1
 // parts, one fused key-product/automorphism/accumulate pass, final ModDown.
-std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct) {
+// rescale: return Rescale(result) (Lattigo's ckks Rescale), with the first
+// division fused into the final ModDown
+std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct, bool rescale) {
   Scheme& s = sch();
   const int N = s.N, K = s.K;
   const int l = std::min(ct.level, t.level), nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
@@ -1265,9 +1308,19 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct) {
   } else {
     d2d(acc.p, T.p, 2 * qp * 8);
   }
-  // 5. final ModDown of both parts
-  auto out = new_ct(l, ct.scale * t.scale); out->logslots = ct.logslots;
-  mod_down(l, acc.p, qp, 2, out->d.p, (size_t)(l + 1) * N);
+  // 5. final ModDown of both parts (with the first rescale when the result is
+  // to be returned rescaled)
+  const double sc = ct.scale * t.scale;
+  REQUIRE(!rescale || l >= 1, "cannot rescale: ciphertext already at level 0");
+  const int nres = rescale ? lattigo_rescale_count(sc, l) : 0;
+  if (nres == 0) {
+    auto out = new_ct(l, sc); out->logslots = ct.logslots;
+    mod_down(l, acc.p, qp, 2, out->d.p, (size_t)(l + 1) * N);
+    return out;
+  }
+  auto out = new_ct(l - 1, sc / (double)s.mod[l]); out->logslots = ct.logslots;
+  mod_down_rescale(l, acc.p, qp, 2, out->d.p, (size_t)l * N);
+  for (int i = 1; i < nres; i++) out = rescale_ct(*out);
   return out;
 }
 // MultiplyByDiagMatrix (naive, N1 = 0)
@@ -1770,10 +1823,16 @@ int EvaluateLinearTransform(int transformID, int ctxtID) {
     Cipher& c = get_ct(ctxtID);
     REQUIRE(std::all_of(t.resident.begin(), t.resident.end(), [](char r) { return r != 0; }),
             "plaintext diagonals not loaded (LoadPlaintextDiagonal)");
-    auto out = t.naive ? eval_lt_naive(t, c) : eval_lt_bsgs(t, c);
+    const bool rescale = sch().lt_prerescale;
+    auto out = t.naive ? eval_lt_naive(t, c) : eval_lt_bsgs(t, c, rescale);
+    if (rescale && t.naive) out = rescale_lattigo(*out);
     return push_ct(std::move(out));
   });
 }
+int SetLinearTransformPrerescale(int on) {
+  return guard([&] { sch().lt_prerescale = on != 0; return 0; });
+}
+int GetLinearTransformPrerescale() { return S && S->lt_prerescale ? 1 : 0; }
 ArrayResultInt GetLinearTransformRotationKeys(int transformID) {
   ArrayResultInt r{nullptr, 0};
   guard([&] {

@@ -134,6 +134,13 @@ int NewLinearTransformEvaluator(void);   /* lineartransform.go:30-34 */
 int GenerateLinearTransform(const int* diagIdxs, int diagIdxsLen, const float* diagData,
                             int diagDataLen, int level, float bsgsRatio, const char* ioMode);
 int EvaluateLinearTransform(int transformID, int ctxtID);         /* lineartransform.go:95-113 */
+/* [ext] on != 0: EvaluateLinearTransform returns Rescale(result) (the
+ * lt_output_prerescaled convention of cheddar/bindings.py:183-187, read by
+ * lt_evaluator.py:262-273), the first division fused into the final ModDown,
+ * residues identical to EvaluateLinearTransform followed by Rescale.  Per
+ * scheme, default 0.  Get returns the current setting (0 without a scheme). */
+int SetLinearTransformPrerescale(int on);
+int GetLinearTransformPrerescale(void);
 ArrayResultInt GetLinearTransformRotationKeys(int transformID);   /* lineartransform.go:115-122 */
 int GenerateLinearTransformRotationKey(int galEl);                /* lineartransform.go:124-128 */
 int DeleteLinearTransform(int id);                                /* lineartransform.go:25-28 */

@@ -20,10 +20,14 @@ pytestmark = pytest.mark.gpu
 TOL = 2.0 ** -20
 
 
-def test_dlrm_n13_bitexact_vs_oracle(hip_lib):
+@pytest.mark.parametrize("prerescale", [False, True])
+def test_dlrm_n13_bitexact_vs_oracle(hip_lib, prerescale):
+    """prerescale: every Linear's transform returns its rescaled result
+    (lt_output_prerescaled) -- the same residues layer by layer."""
     name = "dlrm_n13"
-    print(f"[dlrm] {name}: building", flush=True)
+    print(f"[dlrm] {name} prerescale={prerescale}: building", flush=True)
     w = DLRMWorkload(hip_lib, name, seed=3, key_seed=17).setup()
+    hip_lib.set_lt_output_prerescaled(prerescale)
     print(f"[dlrm] {name}: {w.shape_info()}", flush=True)
     out, kept = w.run_stages(keep=True)
     got = {n: (hip_lib.export_ciphertext(t.ids[0]), hip_lib.GetCiphertextLevel(t.ids[0]),

@@ -44,6 +44,52 @@ def test_pcmm_bitexact_vs_oracle(hip_lib, name):
     hip_lib.DeleteScheme()
 
 
+@pytest.mark.parametrize("name", ["single_table", "pcmm26_n13"])
+def test_pcmm_prerescaled_bitexact_vs_oracle(hip_lib, name):
+    """lt_output_prerescaled (lt_evaluator.py:262-273): EvaluateLinearTransform
+    returns the rescaled result, its first division fused into the final
+    ModDown, and the host skips its Rescale; the PCMM output stays bit-exact
+    with the restatement's transform-then-rescale flow."""
+    print(f"[pcmm] {name} prerescaled: building", flush=True)
+    w = PCMMWorkload(hip_lib, name, seed=5, key_seed=17).setup()
+    hip_lib.set_lt_output_prerescaled(True)
+    assert hip_lib.lt_output_prerescaled
+    out = w.run()
+    got = hip_lib.export_ciphertext(out.ids[0])
+    c = w.cfg
+    orc = O.Oracle(c["logn"], hip_lib.GetModuliChain(), hip_lib.GetAuxModuliChain(), h=c["h"], seed=17)
+    try:
+        want, l, sc = oracle_pcmm(orc, w.layer.diagonals[(0, 0)], w.layer.output_rotations, w.layer.level,
+                                  w.selector, c["logscale"], 0)
+        assert hip_lib.GetCiphertextLevel(out.ids[0]) == l
+        assert hip_lib.GetCiphertextScaleDouble(out.ids[0]) == sc
+        assert_equal_u64(got, want, f"{name} prerescaled PCMM output")
+    finally:
+        orc.close()
+    assert np.abs(w.decrypt_output(out) - w.expected).max() < TOL
+    hip_lib.DeleteScheme()
+    assert not hip_lib.lt_output_prerescaled  # the setting belongs to the scheme
+
+
+def test_lt_prerescaled_equals_transform_then_rescale(hip_lib):
+    """At the 26-table size (N=2^16, 24 limbs): the prerescaled transform
+    returns, word for word, RescaleNew of the plain transform's output."""
+    print("[pcmm] pcmm26 prerescaled vs transform + RescaleNew", flush=True)
+    w = PCMMWorkload(hip_lib, "pcmm26", seed=6, key_seed=17).setup()
+    tid = int(list(w.layer.transform_ids.values())[0])
+    cid = w.ct_in.ids[0]
+    a = hip_lib.EvaluateLinearTransform(tid, cid)
+    r = hip_lib.RescaleNew(a)
+    want = hip_lib.export_ciphertext(r)
+    want_level, want_scale = hip_lib.GetCiphertextLevel(r), hip_lib.GetCiphertextScaleDouble(r)
+    hip_lib.set_lt_output_prerescaled(True)
+    b = hip_lib.EvaluateLinearTransform(tid, cid)
+    assert hip_lib.GetCiphertextLevel(b) == want_level
+    assert hip_lib.GetCiphertextScaleDouble(b) == want_scale
+    assert_equal_u64(hip_lib.export_ciphertext(b), want, "prerescaled transform")
+    hip_lib.DeleteScheme()
+
+
 def test_pcmm_seeded_upload(hip_lib):
     """bench_sweep.py:381-399 seeded upload: the selector is encrypted with a
     seeded `a`, `a` is dropped (only b crossed the wire) and rebuilt on the
