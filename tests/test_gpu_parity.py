@@ -333,6 +333,17 @@ def test_linear_transform(ctx, case):
     assert np.abs(dec - exp).max() < 0.05
     if case in ("identity", "shift", "wrap"):
         np.testing.assert_allclose(dec, np.roll(vals.astype(np.float64), -idx[0]), atol=1e-3)
+    # lt_output_prerescaled (lt_evaluator.py:262-273): the transform itself
+    # returns RescaleNew's residues (BSGS: the rescale fused into the final
+    # ModDown; naive: rescaled after it)
+    ctx.lib.set_lt_output_prerescaled(True)
+    try:
+        pr = ctx.lib.EvaluateLinearTransform(tid, ct)
+    finally:
+        ctx.lib.set_lt_output_prerescaled(False)
+    assert ctx.lib.GetCiphertextLevel(pr) == ctx.lib.GetCiphertextLevel(r)
+    assert _ct_scale(ctx, pr) == _ct_scale(ctx, r)
+    assert_equal_u64(ctx.lib.export_ciphertext(pr), ctx.lib.export_ciphertext(r), f"prerescaled linear transform {case}")
     ctx.lib.DeleteLinearTransform(tid)
 
 
