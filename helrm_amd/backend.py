@@ -253,6 +253,8 @@ _SIGNATURES = {
     "GetLinearTransformInfo": ([_I, _PI, _I], _I),
     "GetSchemeInfo": ([_PI, _I], _I),
     "Synchronize": ([], _I),
+    "SetStream": ([_I], _I),
+    "JoinStream": ([_I], _I),
     "DeviceAlloc": ([_c.c_size_t], _c.c_void_p),
     "DeviceFree": ([_c.c_void_p], _I),
     "CopyToDevice": ([_c.c_void_p, _c.c_void_p, _c.c_size_t], _I),

@@ -167,15 +167,23 @@ std::vector<int8_t> ternary_hw(u64 seed, u64 stream, int N, int h) {
 // ============================================================================
 // device memory: size-bucketed cache (no hipFree on the hot path)
 // ============================================================================
+// Size-bucketed cache of device buffers, one free list per HIP stream of the
+// scheme: a buffer returned while stream i is current is handed out again
+// only to later work on stream i, which runs after everything stream i was
+// given before (work of the other stream that touched the buffer must have
+// been joined first -- JoinStream -- before it is freed on stream i).
 struct Pool {
-  std::multimap<size_t, void*> free_;
+  static constexpr int NSTREAMS = 2;
+  std::multimap<size_t, void*> free_[NSTREAMS];
   std::unordered_map<void*, size_t> size_;
   size_t live = 0, cached = 0, peak = 0;
+  int cur = 0;  // the scheme's current stream
   void* get(size_t bytes) {
     bytes = (bytes + 255) & ~(size_t)255;
     if (bytes == 0) bytes = 256;
-    auto it = free_.find(bytes);
-    if (it != free_.end()) { void* p = it->second; free_.erase(it); cached -= bytes; live += bytes; peak = std::max(peak, live); return p; }
+    auto& fl = free_[cur];
+    auto it = fl.find(bytes);
+    if (it != fl.end()) { void* p = it->second; fl.erase(it); cached -= bytes; live += bytes; peak = std::max(peak, live); return p; }
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, bytes);
     if (e != hipSuccess) { (void)hipGetLastError(); trim(); HCHECK(hipMalloc(&p, bytes)); }
@@ -185,17 +193,21 @@ struct Pool {
   void put(void* p) {
     if (!p) return;
     size_t b = size_.at(p);
-    free_.emplace(b, p); live -= b; cached += b;
+    free_[cur].emplace(b, p); live -= b; cached += b;
   }
   void trim() {
     (void)hipDeviceSynchronize();
-    for (auto& kv : free_) { (void)hipFree(kv.second); size_.erase(kv.second); }
-    free_.clear(); cached = 0;
+    for (auto& fl : free_) {
+      for (auto& kv : fl) { (void)hipFree(kv.second); size_.erase(kv.second); }
+      fl.clear();
+    }
+    cached = 0;
   }
   void release_all() {
     (void)hipDeviceSynchronize();
     for (auto& kv : size_) (void)hipFree(kv.first);
-    free_.clear(); size_.clear(); live = cached = 0;
+    for (auto& fl : free_) fl.clear();
+    size_.clear(); live = cached = 0; cur = 0;
   }
 };
 Pool* g_pool = nullptr;
@@ -251,7 +263,11 @@ struct Scheme {
   int logN = 0, N = 0, L = 0, K = 0, dnum = 0, logscale = 0, h = 0;
   u64 seed = 0;
   std::vector<u64> mod;
-  hipStream_t st = nullptr;  // every public call is ordered on st
+  hipStream_t st = nullptr;  // the current stream: every public call is ordered on it
+  // streams[0] is created with the scheme, streams[1] on the first SetStream(1);
+  // both at the default priority
+  hipStream_t streams[2] = {nullptr, nullptr};
+  hipEvent_t join_ev[2] = {nullptr, nullptr};  // recorded on streams[i] by JoinStream(i)
   DevArray<ModC> d_mods;
   DU64 tw2, itw2, ninv, ninvp;  // interleaved (w, w') twiddle pairs [mod][N][2]
   DU64 twr2, itwr2;             // row-pass consecutive-round twiddles, lane-interleaved
@@ -291,7 +307,10 @@ struct Scheme {
   Timing timing;
   bool encoder = false, encryptor = false, decryptor = false, evaluator = false, lteval = false;
   ~Scheme() {
-    if (st) { (void)hipStreamSynchronize(st); (void)hipStreamDestroy(st); }
+    for (hipStream_t& x : streams)
+      if (x) { (void)hipStreamSynchronize(x); (void)hipStreamDestroy(x); x = nullptr; }
+    for (hipEvent_t& e : join_ev)
+      if (e) { (void)hipEventDestroy(e); e = nullptr; }
   }
 };
 Scheme* S = nullptr;
@@ -779,6 +798,8 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
   }
   for (size_t i = 0; i < s.mod.size(); i++) for (size_t j = i + 1; j < s.mod.size(); j++) REQUIRE(s.mod[i] != s.mod[j], "moduli must be distinct");
   HCHECK(hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking));
+  s.streams[0] = s.st;
+  if (g_pool) g_pool->cur = 0;
   Scheme* old = S; S = sp.get();
   try {
     const int N = s.N, nm = s.L + s.K;
@@ -2181,7 +2202,36 @@ int MulAccDevice(const uint64_t* a, const uint64_t* b, uint64_t* out, int npoly,
 }
 
 // ---- stream / timing ----
-int Synchronize(void) { return guard([&] { sync(); return 0; }); }
+int Synchronize(void) {
+  return guard([&] {
+    for (hipStream_t x : sch().streams)
+      if (x) HCHECK(hipStreamSynchronize(x));
+    return 0;
+  });
+}
+int SetStream(int idx) {
+  return guard([&] {
+    Scheme& s = sch();
+    REQUIRE(idx == 0 || idx == 1, "stream index must be 0 or 1");
+    if (!s.streams[idx]) HCHECK(hipStreamCreateWithFlags(&s.streams[idx], hipStreamNonBlocking));
+    s.st = s.streams[idx];
+    g_pool->cur = idx;
+    return 0;
+  });
+}
+int JoinStream(int idx) {
+  return guard([&] {
+    Scheme& s = sch();
+    REQUIRE(idx == 0 || idx == 1, "stream index must be 0 or 1");
+    hipStream_t other = s.streams[idx];
+    if (!other || other == s.st) return 0;
+    if (!s.join_ev[idx]) HCHECK(hipEventCreateWithFlags(&s.join_ev[idx], hipEventDisableTiming));
+    // the wait takes the event as recorded now; a later JoinStream records it anew
+    HCHECK(hipEventRecord(s.join_ev[idx], other));
+    HCHECK(hipStreamWaitEvent(s.st, s.join_ev[idx], 0));
+    return 0;
+  });
+}
 void* GetStream(void) { return S ? (void*)S->st : nullptr; }
 int KernelTimingEnable(int on) { return guard([&] { Scheme& s = sch(); sync(); timing_collect(); s.timing.acc.clear(); s.timing.on = on != 0; return 0; }); }
 int KernelTimingGet(const char* name, long* count, double* total_ms) {

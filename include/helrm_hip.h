@@ -201,8 +201,17 @@ int NttDevice(uint64_t* data, int npoly, int nrows, int forward);  /* in place; 
 int MulAccDevice(const uint64_t* a, const uint64_t* b, uint64_t* out, int npoly, int nrows); /* out = sum_p a_p*b_p */
 
 /* ---- [ext] stream and measurement ------------------------------------------------ */
-int Synchronize(void);
-void* GetStream(void);                                            /* hipStream_t of the scheme */
+int Synchronize(void);                                            /* waits for both streams */
+void* GetStream(void);                                            /* hipStream_t the scheme's calls run on now */
+/* [ext] two HIP streams per scheme, for independent chains of calls (no
+ * counterpart in the reference, whose forward is one sequence).  SetStream(i)
+ * makes stream i (0 or 1; 1 is created on first use, default priority) the
+ * one every later call is ordered on; JoinStream(i) makes the current stream
+ * wait for all work given to stream i so far.  Device buffers freed while
+ * stream i is current are reused only by stream i: free an object while the
+ * stream that last used it is current, or after joining that stream. */
+int SetStream(int idx);
+int JoinStream(int idx);
 int KernelTimingEnable(int on);                                   /* HIP events around named launches */
 int KernelTimingGet(const char* name, long* count, double* total_ms);
 int GetMemoryStats(uint64_t* live, uint64_t* cached, uint64_t* peak);

@@ -47,6 +47,17 @@ def test_dlrm_n13_bitexact_vs_oracle(hip_lib, prerescale):
             dec = orc.decode_f64(orc.decrypt(ct, lv), lv, s)[: len(ref)]
             assert np.abs(dec - ref).max() < TOL, n
         print(f"[dlrm] {name}: {len(trace)} layer outputs bit-exact", flush=True)
+        # the lookup path on the second stream beside the bottom MLP (run()),
+        # twice, so that the second forward reuses buffers both streams freed
+        final = w.top_names[-1][1]
+        want_ct, want_l, want_s = trace[final]
+        w.concurrent = True
+        for rep in range(2):
+            o = w.run()
+            assert hip_lib.GetCiphertextLevel(o.ids[0]) == want_l
+            assert hip_lib.GetCiphertextScaleDouble(o.ids[0]) == want_s
+            assert_equal_u64(hip_lib.export_ciphertext(o.ids[0]), want_ct, f"{name} concurrent forward {rep}")
+            o.free()
     finally:
         orc.close()
     err = np.abs(y - w.expected).max()
@@ -64,7 +75,12 @@ def test_dlrm_full_size_decrypts(hip_lib):
     print(f"[dlrm] dlrm: {info}", flush=True)
     assert info["bottom.0"]["diagonals"] == 512 and info["sparse"]["diagonals"] == 512
     assert info["top.4"]["output_rotations"] == 0
-    out = w.run()
+    assert w.concurrent  # run(): the lookup path on the second stream
+    first = w.run()
+    ref = hip_lib.export_ciphertext(first.ids[0])
+    first.free()
+    out = w.run()  # reuses the buffers both streams freed: the same words
+    assert_equal_u64(hip_lib.export_ciphertext(out.ids[0]), ref, "second concurrent forward")
     assert hip_lib.GetCiphertextLevel(out.ids[0]) == 0
     y = w.decrypt_output(out)
     err = np.abs(y - w.expected).max()

@@ -76,3 +76,22 @@ def test_library_keeps_working_after_errors(lib):
         lib.AddCiphertext(ct, 4242)
     dec = np.asarray(lib.Decode(lib.Decrypt(ct)))
     np.testing.assert_allclose(dec[:16], np.linspace(-1, 1, 16), atol=1e-4)
+
+
+def test_stream_selection(lib):
+    """SetStream / JoinStream take stream 0 or 1; work given to stream 1 and
+    joined is seen by stream 0 (a sum computed there, used on stream 0)."""
+    with pytest.raises(HipError, match="stream index"):
+        lib.SetStream(2)
+    with pytest.raises(HipError, match="stream index"):
+        lib.JoinStream(-1)
+    ct = fresh(lib)
+    lib.SetStream(1)
+    lib.JoinStream(0)
+    two = lib.AddCiphertextNew(ct, ct)
+    lib.SetStream(0)
+    lib.JoinStream(1)
+    three = lib.AddCiphertextNew(two, ct)
+    lib.Synchronize()
+    dec = np.asarray(lib.Decode(lib.Decrypt(three)))
+    np.testing.assert_allclose(dec[:16], 3 * np.linspace(-1, 1, 16), atol=1e-3)
