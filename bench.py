@@ -25,18 +25,23 @@ METRIC = "encrypted embedding lookups/sec (26-table PCMM, N=2^16)"
 HBM_PEAK_GBS = 8000.0
 
 
-def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=8, chunks=1):
+def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=8, chunks=1, fused_babies=True):
     """Per-PCMM and per-diag-MAC-launch algorithmic HBM bytes (every word once).
 
     PCMM: the diagonals, each of the R rotation keys, the input and the output
     ciphertext.  Diagonal MAC launch (the giant groups split evenly over
-    `chunks` launches): its share of the diagonals, the n1-1 hoisted baby
-    rotations (2 QP polys each) and P*c (2 Q polys, baby step 0) read, one QP
-    accumulator pair per giant group of the launch written."""
+    `chunks` launches): its share of the diagonals and P*c (2 Q polys, baby
+    step 0) read, one QP accumulator pair per giant group of the launch
+    written, and the n1-1 hoisted baby rotations -- computed in the kernel's
+    prologue from their keys (dnum*2 QP polys each) and the decomposed input
+    (dnum QP polys, once) when fused_babies, else read (2 QP polys each)."""
     R = (n1 - 1) + (n2 - 1) + f
     pcmm = D * (L + K) * N * w + R * dnum * 2 * (L + K) * N * w + 2 * L * N * w + 2 * (L - 1) * N * w
-    diag_mac = (D * (L + K) * N * w + n2 * 2 * (L + K) * N * w) // chunks \
-        + (n1 - 1) * 2 * (L + K) * N * w + 2 * L * N * w
+    if fused_babies:
+        babies = (n1 - 1) * dnum * 2 * (L + K) * N * w + (dnum * (L + K) * N * w if n1 > 1 else 0)
+    else:
+        babies = (n1 - 1) * 2 * (L + K) * N * w
+    diag_mac = (D * (L + K) * N * w + n2 * 2 * (L + K) * N * w) // chunks + babies + 2 * L * N * w
     return pcmm, diag_mac
 
 
@@ -177,7 +182,7 @@ def keyswitch_bytes(N, Lq, K, nb, ng, w=8):
     return baby, giant
 
 
-def lt_roofline_bytes(lib, layer, N, K, w=8):
+def lt_roofline_bytes(lib, layer, N, K, w=8, fused_babies=True):
     """(whole-layer, diagonal-MAC) algorithmic bytes of one compiled Linear
     at its level: algorithmic_bytes with L = level + 1 active Q limbs and the
     transform's own baby / giant counts and fold rotations."""
@@ -185,7 +190,7 @@ def lt_roofline_bytes(lib, layer, N, K, w=8):
     lti = lib.lt_info(tid)
     Lq = layer.level + 1
     return algorithmic_bytes(N=N, L=Lq, K=K, D=lti["plaintexts"], n1=lti["baby"], n2=lti["giant"],
-                             f=layer.output_rotations, dnum=(Lq + K - 1) // K, w=w), lti
+                             f=layer.output_rotations, dnum=(Lq + K - 1) // K, w=w, fused_babies=fused_babies), lti
 
 
 def cpu_model():
@@ -402,8 +407,10 @@ def main():
     layers = w.linear_layers()
     step_bytes, mac_bytes, lt_shapes = 0, 0, []
     ks_bytes = {"keymac_baby": 0, "giant_acc": 0}
+    # the baby rotations run inside the diagonal MAC unless keymac_baby launches showed up
+    fused_babies = not kt["keymac_baby"]["launches"]
     for layer in layers:
-        (b_layer, b_mac), lti = lt_roofline_bytes(lib, layer, N, K)
+        (b_layer, b_mac), lti = lt_roofline_bytes(lib, layer, N, K, fused_babies=fused_babies)
         step_bytes += b_layer
         mac_bytes += b_mac
         kb, kg = keyswitch_bytes(N, layer.level + 1, K, lti["baby"], lti["giant"])

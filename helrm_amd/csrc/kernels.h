@@ -75,6 +75,13 @@ struct DiagMacArgs {
   const ModC* mods;
   int N, l, L, K, nqp, lt_level, ng, nbaby, b0, nb_chunk;
   int g0, g1;               // giant groups [g0, g1) of this launch
+  // R == nullptr: the hoisted baby rotations are computed in the kernel's
+  // prologue (keymac_kernel's arithmetic) instead of being read from R
+  const u64* digits;              // [dn][nqp][N] decomposition of c1 (NTT)
+  const u64* const* bkey;         // per baby slot: Galois key [dnum][2][L+K][N], Montgomery form
+  const uint32_t* const* bperm;   // per baby slot: automorphism gather
+  const u64* own;                 // c1 (Q rows, NTT): a digit's own rows
+  int dn;
 };
 
 // In-place NTT (forward) / inverse NTT of rows rm of `batch` polynomials.

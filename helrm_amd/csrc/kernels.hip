@@ -454,7 +454,35 @@ __device__ __forceinline__ void mac_group(const DiagMacArgs& a, const u64 (&d)[N
   __builtin_nontemporal_store(r1, &T[a.T_pstride]);
 }
 
-template <int NB, bool DENSE>
+// One word of a hoisted baby rotation, keymac_kernel's arithmetic at (row k,
+// position x): src = perm[x], sum_d digit_d[k][src] * key[d][p][kl][src]
+// (+ P c0[k][src] in part 0), one REDC per part.
+__device__ __forceinline__ void baby_rotation_at(const DiagMacArgs& a, int slot, int k, int kl, int x, const ModC& mc,
+                                                 u64& r0, u64& r1) {
+  const int N = a.N;
+  const int src = (int)a.bperm[slot][x];
+  const u64* key = a.bkey[slot];
+  const int own_d = k <= a.l ? k / a.K : -1;
+  const size_t kstride = (size_t)(a.L + a.K) * N;
+  Acc128 A0, A1;
+  acc_zero(A0); acc_zero(A1);
+  for (int d = 0; d < a.dn; d++) {
+    const u64 v = d == own_d ? a.own[(size_t)k * N + src] : a.digits[((size_t)d * a.nqp + k) * N + src];
+    const u64* kb = key + (size_t)d * 2 * kstride + (size_t)kl * N + src;
+    acc_mac(A0, v, __builtin_nontemporal_load(&kb[0]));
+    acc_mac(A1, v, __builtin_nontemporal_load(&kb[kstride]));
+  }
+  u64 lo0, hi0, lo1, hi1;
+  acc_value(A0, lo0, hi0);
+  acc_value(A1, lo1, hi1);
+  hi0 = fold_hi4(hi0, mc.q);
+  hi1 = fold_hi4(hi1, mc.q);
+  if (k <= a.l) hi0 = add_mod(hi0, a.pc[(size_t)k * N + src], mc.q);
+  r0 = redc(lo0, hi0, mc.q, mc.qinv);
+  r1 = redc(lo1, hi1, mc.q, mc.qinv);
+}
+
+template <int NB, bool DENSE, bool FUSED>
 __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
   const int x = blockIdx.x * blockDim.x + threadIdx.x;
   const int k = blockIdx.y;
@@ -471,6 +499,8 @@ __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
     if (bb < a.nbaby) {
       if (a.baby_is_zero[bb]) {
         if (k <= a.l) { s0[b] = a.pc[(size_t)k * N + x]; s1[b] = a.pc[a.pc_pstride + (size_t)k * N + x]; }
+      } else if (FUSED) {
+        baby_rotation_at(a, a.baby_slot[bb], k, kl, x, mc, s0[b], s1[b]);
       } else {
         const u64* r = a.R + (size_t)a.baby_slot[bb] * a.R_bstride + (size_t)k * N + x;
         s0[b] = r[0];
@@ -490,14 +520,19 @@ __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
     mac_group<NB>(a, dB, s0, s1, mc, Tb + (size_t)(g + 1) * a.T_gstride);
   }
 }
-void launch_diag_mac(const DiagMacArgs& a, hipStream_t st) {
-  if (a.g1 <= a.g0) return;
+template <bool FUSED>
+static void launch_diag_mac_t(const DiagMacArgs& a, hipStream_t st) {
   dim3 grid(a.N / 256, a.nqp, 1);
   const bool dense = a.dense && a.nb_chunk == 16 && a.b0 + 16 <= a.nbaby;
-  if (dense) hipLaunchKernelGGL((diag_mac_kernel<16, true>), grid, dim3(256), 0, st, a);
-  else if (a.nb_chunk <= 8) hipLaunchKernelGGL((diag_mac_kernel<8, false>), grid, dim3(256), 0, st, a);
-  else if (a.nb_chunk <= 16) hipLaunchKernelGGL((diag_mac_kernel<16, false>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((diag_mac_kernel<32, false>), grid, dim3(256), 0, st, a);
+  if (dense) hipLaunchKernelGGL((diag_mac_kernel<16, true, FUSED>), grid, dim3(256), 0, st, a);
+  else if (a.nb_chunk <= 8) hipLaunchKernelGGL((diag_mac_kernel<8, false, FUSED>), grid, dim3(256), 0, st, a);
+  else if (a.nb_chunk <= 16) hipLaunchKernelGGL((diag_mac_kernel<16, false, FUSED>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((diag_mac_kernel<32, false, FUSED>), grid, dim3(256), 0, st, a);
+}
+void launch_diag_mac(const DiagMacArgs& a, hipStream_t st) {
+  if (a.g1 <= a.g0) return;
+  if (a.R) launch_diag_mac_t<false>(a, st);
+  else launch_diag_mac_t<true>(a, st);
 }
 
 // RNS multiply-accumulate over a batch: out[r][x] = sum_p a[p][r][x] * b[p][r][x]

@@ -1247,6 +1247,7 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
   return id;
 }
 
+constexpr bool kFuseBabyRotations = true;
 // MultiplyByDiagMatrixBSGS on the GPU: one decomposition, batched hoisted
 // baby rotations, one fused diagonal-MAC pass producing every giant group's
 // QP accumulators, batched ModDown + decomposition of the giant groups' c1
@@ -1288,8 +1289,11 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct, bool r
       tm.ptrs_ready = true;
     }
   }
-  DU64 R((size_t)std::max(nbr, 1) * 2 * qp);
-  if (nbr > 0) {
+  // The diagonal MAC computes the hoisted baby rotations in its own prologue
+  // (keymac_kernel's arithmetic per word), so they never go through memory.
+  const bool fuse_babies = kFuseBabyRotations;
+  DU64 R(fuse_babies ? 0 : (size_t)std::max(nbr, 1) * 2 * qp);
+  if (nbr > 0 && !fuse_babies) {
     KeyMacArgs a{};
     a.digits = digits.p; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = t.d_bkey.p; a.perm = t.d_bperm.p; a.add0 = pc.p;
     a.own = c1; a.own_bstride = 0;
@@ -1301,7 +1305,8 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct, bool r
   DU64 T((size_t)ng * 2 * qp);
   DiagMacArgs dm{};
   dm.diag = t.diags.p; dm.diag_stride = (size_t)(t.level + 1 + K) * N;
-  dm.R = R.p; dm.R_bstride = 2 * qp; dm.R_pstride = qp;
+  dm.R = fuse_babies ? nullptr : R.p; dm.R_bstride = 2 * qp; dm.R_pstride = qp;
+  dm.digits = digits.p; dm.bkey = t.d_bkey.p; dm.bperm = t.d_bperm.p; dm.own = c1; dm.dn = dn;
   dm.pc = pc.p; dm.pc_pstride = (size_t)(l + 1) * N;
   dm.baby_is_zero = t.d_bzero.p; dm.baby_slot = t.d_bslot.p; dm.gpi = t.d_gpi.p; dm.dense = t.dense ? 1 : 0;
   dm.zero_pidx = (int)t.plain_idx.size();

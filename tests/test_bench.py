@@ -21,13 +21,18 @@ def test_more_than_one_gpu_is_refused():
 def test_pcmm26_algorithmic_bytes():
     """N=2^16, L=24, K=8, D=512, 16 baby x 32 giant steps, 6 fold rotations,
     dnum=3: diagonals + 52 rotation keys + input + output ciphertexts, and the
-    diagonal-MAC launch (diagonals, 15 hoisted rotations, P*c, 32 QP
-    accumulator pairs)."""
+    diagonal-MAC launch: diagonals, the keys of the 15 hoisted baby rotations
+    and the 3 decomposed digits (the rotations are computed in its prologue),
+    P*c, 32 QP accumulator pairs; with the rotations read instead, 15 rotated
+    QP pairs take the place of keys and digits."""
     pcmm, mac = bench.algorithmic_bytes()
     assert pcmm == 13_873_709_056
-    assert mac == 10_192_158_720
+    assert mac == 11_249_123_328
     N, w, nqp = 1 << 16, 8, 32
-    assert mac == 512 * nqp * N * w + 15 * 2 * nqp * N * w + 2 * 24 * N * w + 32 * 2 * nqp * N * w
+    assert mac == (512 * nqp + 15 * 3 * 2 * nqp + 3 * nqp + 32 * 2 * nqp) * N * w + 2 * 24 * N * w
+    _, unfused = bench.algorithmic_bytes(fused_babies=False)
+    assert unfused == 10_192_158_720
+    assert unfused == 512 * nqp * N * w + 15 * 2 * nqp * N * w + 2 * 24 * N * w + 32 * 2 * nqp * N * w
 
 
 def test_keyswitch_kernel_bytes():
