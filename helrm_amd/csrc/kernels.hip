@@ -402,7 +402,10 @@ void launch_giant_acc(const GiantAccArgs& a, hipStream_t st) {
 // streams every plaintext diagonal once, writing one accumulator pair per
 // giant group:
 //   T[g][p][k][x] = sum_{b in baby(g)} diag_{g,b}[k][x] * S_b[p][k][x]
-// S_0 = P*c (Q rows only), S_b = hoisted rotation b (QP).  The next group's
+// S_0 = P*c (Q rows only), S_b = hoisted rotation b (QP), which the FUSED
+// variant computes in its prologue from the rotation's key and the decomposed
+// input (so the rotations are never written to or read from memory) and the
+// other variant reads from R.  The next group's
 // diagonals are loaded while the current group is multiplied (NB loads in
 // flight per thread).  Products are summed exactly in 128 bits (16 products
 // of words < 2^62 cannot overflow; the high word is folded below 4q after
