@@ -90,3 +90,24 @@ def test_dlrm_full_size_decrypts(hip_lib):
     full = np.asarray(w.scheme.decode(w.scheme.decrypt(out.__class__(w.scheme, out.ids, 4096))))
     assert np.abs(full[1:]).max() < TOL
     hip_lib.DeleteScheme()
+
+
+def test_dlrm_n13_seeded_upload_concurrent(hip_lib):
+    """The selector uploaded as (b, seed) (bench_sweep.py:381-403): every
+    forward rebuilds `a` on the device -- on the second stream when the lookup
+    path runs beside the bottom MLP.  Concurrent and one-stream forwards give
+    the same words, twice each."""
+    w = DLRMWorkload(hip_lib, "dlrm_n13", seed=5, key_seed=17).setup()
+    hip_lib.set_lt_output_prerescaled(True)
+    w.use_seeded_upload(0x5EED)
+    outs = []
+    for concurrent in (False, True, False, True):
+        w.concurrent = concurrent
+        o = w.run()
+        outs.append(hip_lib.export_ciphertext(o.ids[0]))
+        if concurrent:
+            assert np.abs(w.decrypt_output(o) - w.expected).max() < TOL
+        o.free()
+    for i, g in enumerate(outs[1:], 1):
+        assert_equal_u64(g, outs[0], f"seeded-upload forward {i}")
+    hip_lib.DeleteScheme()
