@@ -182,7 +182,7 @@ def keyswitch_bytes(N, Lq, K, nb, ng, w=8):
     return baby, giant
 
 
-def lt_roofline_bytes(lib, layer, N, K, w=8, fused_babies=True):
+def lt_roofline_bytes(lib, layer, N, K, w=8):
     """(whole-layer, diagonal-MAC) algorithmic bytes of one compiled Linear
     at its level: algorithmic_bytes with L = level + 1 active Q limbs and the
     transform's own baby / giant counts and fold rotations."""
@@ -190,7 +190,7 @@ def lt_roofline_bytes(lib, layer, N, K, w=8, fused_babies=True):
     lti = lib.lt_info(tid)
     Lq = layer.level + 1
     return algorithmic_bytes(N=N, L=Lq, K=K, D=lti["plaintexts"], n1=lti["baby"], n2=lti["giant"],
-                             f=layer.output_rotations, dnum=(Lq + K - 1) // K, w=w, fused_babies=fused_babies), lti
+                             f=layer.output_rotations, dnum=(Lq + K - 1) // K, w=w), lti
 
 
 def cpu_model():
@@ -392,7 +392,7 @@ def main():
         o.free()
     lib.Synchronize()
     kt = {}
-    for name in ("diag_mac", "giant_acc", "keymac_baby"):
+    for name in ("diag_mac", "giant_acc"):
         c, tot = lib.kernel_time(name)
         kt[name] = {"launches": c, "avg_ms": tot / c if c else None}
     lib.KernelTimingEnable(0)
@@ -406,15 +406,12 @@ def main():
     launches = max(1, round(kt["diag_mac"]["launches"] / nprof)) if kt["diag_mac"]["launches"] else 1
     layers = w.linear_layers()
     step_bytes, mac_bytes, lt_shapes = 0, 0, []
-    ks_bytes = {"keymac_baby": 0, "giant_acc": 0}
-    # the baby rotations run inside the diagonal MAC unless keymac_baby launches showed up
-    fused_babies = not kt["keymac_baby"]["launches"]
+    ks_bytes = {"giant_acc": 0}
     for layer in layers:
-        (b_layer, b_mac), lti = lt_roofline_bytes(lib, layer, N, K, fused_babies=fused_babies)
+        (b_layer, b_mac), lti = lt_roofline_bytes(lib, layer, N, K)
         step_bytes += b_layer
         mac_bytes += b_mac
-        kb, kg = keyswitch_bytes(N, layer.level + 1, K, lti["baby"], lti["giant"])
-        ks_bytes["keymac_baby"] += kb if lti["baby"] > 1 else 0
+        _, kg = keyswitch_bytes(N, layer.level + 1, K, lti["baby"], lti["giant"])
         ks_bytes["giant_acc"] += kg if lti["giant"] > 1 else 0
         lt_shapes.append({"level": layer.level, "diagonals": lti["plaintexts"], "baby": lti["baby"],
                           "giant": lti["giant"], "fold": layer.output_rotations})

@@ -61,8 +61,6 @@ struct GiantAccArgs {
 struct DiagMacArgs {
   const u64* diag;        // [np][lt_level+1+K][N] Montgomery form
   size_t diag_stride;
-  const u64* R;           // hoisted rotations [slot][2][nqp][N]
-  size_t R_bstride, R_pstride;
   const u64* pc;          // P*c0, P*c1 : [2][l+1][N]
   size_t pc_pstride;
   const int* baby_is_zero;  // [nbaby]
@@ -75,8 +73,8 @@ struct DiagMacArgs {
   const ModC* mods;
   int N, l, L, K, nqp, lt_level, ng, nbaby, b0, nb_chunk;
   int g0, g1;               // giant groups [g0, g1) of this launch
-  // R == nullptr: the hoisted baby rotations are computed in the kernel's
-  // prologue (keymac_kernel's arithmetic) instead of being read from R
+  // the hoisted baby rotations, computed in the kernel's prologue
+  // (keymac_kernel's arithmetic per word)
   const u64* digits;              // [dn][nqp][N] decomposition of c1 (NTT)
   const u64* const* bkey;         // per baby slot: Galois key [dnum][2][L+K][N], Montgomery form
   const uint32_t* const* bperm;   // per baby slot: automorphism gather

@@ -402,10 +402,9 @@ void launch_giant_acc(const GiantAccArgs& a, hipStream_t st) {
 // streams every plaintext diagonal once, writing one accumulator pair per
 // giant group:
 //   T[g][p][k][x] = sum_{b in baby(g)} diag_{g,b}[k][x] * S_b[p][k][x]
-// S_0 = P*c (Q rows only), S_b = hoisted rotation b (QP), which the FUSED
-// variant computes in its prologue from the rotation's key and the decomposed
-// input (so the rotations are never written to or read from memory) and the
-// other variant reads from R.  The next group's
+// S_0 = P*c (Q rows only), S_b = hoisted rotation b (QP), computed in the
+// prologue from the rotation's key and the decomposed input (the rotations
+// are never written to or read from memory).  The next group's
 // diagonals are loaded while the current group is multiplied (NB loads in
 // flight per thread).  Products are summed exactly in 128 bits (16 products
 // of words < 2^62 cannot overflow; the high word is folded below 4q after
@@ -485,7 +484,7 @@ __device__ __forceinline__ void baby_rotation_at(const DiagMacArgs& a, int slot,
   r1 = redc(lo1, hi1, mc.q, mc.qinv);
 }
 
-template <int NB, bool DENSE, bool FUSED>
+template <int NB, bool DENSE>
 __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
   const int x = blockIdx.x * blockDim.x + threadIdx.x;
   const int k = blockIdx.y;
@@ -502,12 +501,8 @@ __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
     if (bb < a.nbaby) {
       if (a.baby_is_zero[bb]) {
         if (k <= a.l) { s0[b] = a.pc[(size_t)k * N + x]; s1[b] = a.pc[a.pc_pstride + (size_t)k * N + x]; }
-      } else if (FUSED) {
-        baby_rotation_at(a, a.baby_slot[bb], k, kl, x, mc, s0[b], s1[b]);
       } else {
-        const u64* r = a.R + (size_t)a.baby_slot[bb] * a.R_bstride + (size_t)k * N + x;
-        s0[b] = r[0];
-        s1[b] = r[a.R_pstride];
+        baby_rotation_at(a, a.baby_slot[bb], k, kl, x, mc, s0[b], s1[b]);
       }
     }
   }
@@ -523,19 +518,14 @@ __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
     mac_group<NB>(a, dB, s0, s1, mc, Tb + (size_t)(g + 1) * a.T_gstride);
   }
 }
-template <bool FUSED>
-static void launch_diag_mac_t(const DiagMacArgs& a, hipStream_t st) {
-  dim3 grid(a.N / 256, a.nqp, 1);
-  const bool dense = a.dense && a.nb_chunk == 16 && a.b0 + 16 <= a.nbaby;
-  if (dense) hipLaunchKernelGGL((diag_mac_kernel<16, true, FUSED>), grid, dim3(256), 0, st, a);
-  else if (a.nb_chunk <= 8) hipLaunchKernelGGL((diag_mac_kernel<8, false, FUSED>), grid, dim3(256), 0, st, a);
-  else if (a.nb_chunk <= 16) hipLaunchKernelGGL((diag_mac_kernel<16, false, FUSED>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((diag_mac_kernel<32, false, FUSED>), grid, dim3(256), 0, st, a);
-}
 void launch_diag_mac(const DiagMacArgs& a, hipStream_t st) {
   if (a.g1 <= a.g0) return;
-  if (a.R) launch_diag_mac_t<false>(a, st);
-  else launch_diag_mac_t<true>(a, st);
+  dim3 grid(a.N / 256, a.nqp, 1);
+  const bool dense = a.dense && a.nb_chunk == 16 && a.b0 + 16 <= a.nbaby;
+  if (dense) hipLaunchKernelGGL((diag_mac_kernel<16, true>), grid, dim3(256), 0, st, a);
+  else if (a.nb_chunk <= 8) hipLaunchKernelGGL((diag_mac_kernel<8, false>), grid, dim3(256), 0, st, a);
+  else if (a.nb_chunk <= 16) hipLaunchKernelGGL((diag_mac_kernel<16, false>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((diag_mac_kernel<32, false>), grid, dim3(256), 0, st, a);
 }
 
 // RNS multiply-accumulate over a batch: out[r][x] = sum_p a[p][r][x] * b[p][r][x]

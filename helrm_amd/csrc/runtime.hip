@@ -1247,10 +1247,9 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
   return id;
 }
 
-constexpr bool kFuseBabyRotations = true;
-// MultiplyByDiagMatrixBSGS on the GPU: one decomposition, batched hoisted
-// baby rotations, one fused diagonal-MAC pass producing every giant group's
-// QP accumulators, batched ModDown + decomposition of the giant groups' c1
+// MultiplyByDiagMatrixBSGS on the GPU: one decomposition, one fused pass that
+// computes the hoisted baby rotations and the diagonal MAC producing every
+// giant group's QP accumulators, batched ModDown + decomposition of the giant groups' c1
 // parts, one fused key-product/automorphism/accumulate pass, final ModDown.
 // rescale: return Rescale(result) (Lattigo's ckks Rescale), with the first
 // division fused into the final ModDown
@@ -1267,7 +1266,6 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct, bool r
   DU64 pc((size_t)2 * (l + 1) * N);
   launch_mul_const(pc.p, c0, 0, 1, rows_q(l), s.pmod_w.p, s.pmod_wp.p, s.d_mods.p, N, s.st);
   launch_mul_const(pc.p + (size_t)(l + 1) * N, c1, 0, 1, rows_q(l), s.pmod_w.p, s.pmod_wp.p, s.d_mods.p, N, s.st);
-  // 2. hoisted baby rotations (sigma(d0 + P c0), sigma(d1)) in QP
   std::vector<int> babies;
   for (int b : t.rot2) if (b != 0) babies.push_back(b);
   const int nbr = (int)babies.size();
@@ -1289,23 +1287,13 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct, bool r
       tm.ptrs_ready = true;
     }
   }
-  // The diagonal MAC computes the hoisted baby rotations in its own prologue
-  // (keymac_kernel's arithmetic per word), so they never go through memory.
-  const bool fuse_babies = kFuseBabyRotations;
-  DU64 R(fuse_babies ? 0 : (size_t)std::max(nbr, 1) * 2 * qp);
-  if (nbr > 0 && !fuse_babies) {
-    KeyMacArgs a{};
-    a.digits = digits.p; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = t.d_bkey.p; a.perm = t.d_bperm.p; a.add0 = pc.p;
-    a.own = c1; a.own_bstride = 0;
-    a.out0 = R.p; a.out1 = R.p + qp; a.out_bstride = 2 * qp; a.mods = s.d_mods.p;
-    a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
-    timed("keymac_baby", [&] { launch_keymac(a, nbr, s.st); });
-  }
+  // 2. the hoisted baby rotations (sigma(d0 + P c0), sigma(d1)) are computed by
+  // the diagonal MAC in its prologue (keymac_kernel's arithmetic per word), so
+  // they never go through memory
   // 3. fused diagonal MAC -> T[g][2][nqp][N]
   DU64 T((size_t)ng * 2 * qp);
   DiagMacArgs dm{};
   dm.diag = t.diags.p; dm.diag_stride = (size_t)(t.level + 1 + K) * N;
-  dm.R = fuse_babies ? nullptr : R.p; dm.R_bstride = 2 * qp; dm.R_pstride = qp;
   dm.digits = digits.p; dm.bkey = t.d_bkey.p; dm.bperm = t.d_bperm.p; dm.own = c1; dm.dn = dn;
   dm.pc = pc.p; dm.pc_pstride = (size_t)(l + 1) * N;
   dm.baby_is_zero = t.d_bzero.p; dm.baby_slot = t.d_bslot.p; dm.gpi = t.d_gpi.p; dm.dense = t.dense ? 1 : 0;
