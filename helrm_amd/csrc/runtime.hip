@@ -248,6 +248,7 @@ struct LinTrans {
   DU64 diags;                            // [np][level+1+K][N], Montgomery form
   std::vector<char> resident;            // per stored plaintext: loaded (SerializeDiagonal / Remove drop it)
   DevArray<int> d_gpi, d_bzero, d_bslot;  // [ng][nbaby] plaintext index (absent: the zero plaintext); per-baby flags
+  std::vector<int> gpi, bzero, bslot;     // host copies, checked before every diagonal-MAC launch
   bool dense = false;                     // every giant group holds every baby step
   double scale = 0;
   // device arrays of key / permutation pointers (baby and giant rotations), built on first use
@@ -1173,6 +1174,28 @@ std::vector<int> lt_rotations(const LinTrans& t) {
   return out;
 }
 
+// The diagonal MAC reads plaintext gpi[g][b] of its diagonal buffer (np
+// diagonals plus the all-zero one at index np) and the key / permutation of
+// baby slot bslot[b]; every index must stay inside those arrays, and a dense
+// transform (plaintext index computed as g * nbaby + b, no table) must hold
+// exactly that layout.  Checked on the host before the tables are uploaded
+// and again before every launch.
+void check_mac_tables(const LinTrans& t) {
+  const int ng = (int)t.giant.size(), nb = (int)t.rot2.size(), np = (int)t.plain_idx.size();
+  REQUIRE(t.gpi.size() == (size_t)ng * nb && t.bzero.size() == (size_t)nb && t.bslot.size() == (size_t)nb,
+          "linear transform: index tables do not match the baby / giant step counts");
+  int nbr = 0;
+  for (int b = 0; b < nb; b++) nbr += t.rot2[b] != 0;
+  for (int b = 0; b < nb; b++) {
+    REQUIRE(t.bzero[b] == (t.rot2[b] == 0 ? 1 : 0), "linear transform: baby-step zero flag out of step");
+    REQUIRE(t.bzero[b] || (t.bslot[b] >= 0 && t.bslot[b] < nbr), "linear transform: baby-step key slot out of range");
+  }
+  for (size_t i = 0; i < t.gpi.size(); i++) {
+    REQUIRE(t.gpi[i] >= 0 && t.gpi[i] <= np, "linear transform: plaintext index out of range");
+    if (t.dense) REQUIRE(t.gpi[i] == (int)i, "linear transform: dense layout broken");
+  }
+}
+
 int generate_lt(const int* idx, int nidx, const float* data, int ndata, int level, float ratio, bool load_mode) {
   Scheme& s = sch();
   const int N = s.N, slots = N / 2, K = s.K;
@@ -1195,7 +1218,6 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
     t->N1 = find_best_bsgs_ratio(t->keys, slots, logratio);
     REQUIRE(t->N1 >= 1, "invalid baby-step size");
     bsgs_index(t->keys, slots, t->N1, t->rot1, t->rot2);
-    REQUIRE(t->rot2.size() <= 64, "more than 64 baby steps are not supported");
     t->giant = t->rot1;
     t->baby.assign(t->giant.size(), {});
     for (int d : t->keys) {
@@ -1237,9 +1259,11 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
     for (size_t i = 0; i < gpi.size(); i++) if (gpi[i] != (int)i) t->dense = false;
     int slot = 0;
     for (int i = 0; i < nb; i++) { bzero[i] = t->rot2[i] == 0; bslot[i] = t->rot2[i] == 0 ? 0 : slot++; }
-    t->d_gpi = DevArray<int>(gpi.size()); upload(t->d_gpi.p, gpi.data(), gpi.size());
-    t->d_bzero = DevArray<int>(nb); upload(t->d_bzero.p, bzero.data(), nb);
-    t->d_bslot = DevArray<int>(nb); upload(t->d_bslot.p, bslot.data(), nb);
+    t->gpi = std::move(gpi); t->bzero = std::move(bzero); t->bslot = std::move(bslot);
+    check_mac_tables(*t);
+    t->d_gpi = DevArray<int>(t->gpi.size()); upload(t->d_gpi.p, t->gpi.data(), t->gpi.size());
+    t->d_bzero = DevArray<int>(nb); upload(t->d_bzero.p, t->bzero.data(), nb);
+    t->d_bslot = DevArray<int>(nb); upload(t->d_bslot.p, t->bslot.data(), nb);
   }
   sync();
   int id = s.lt_ids.take();
@@ -1301,6 +1325,8 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct, bool r
   dm.T = T.p; dm.T_gstride = 2 * qp; dm.T_pstride = qp; dm.mods = s.d_mods.p;
   dm.N = N; dm.l = l; dm.L = s.L; dm.K = K; dm.nqp = nqp; dm.lt_level = t.level; dm.ng = ng; dm.nbaby = nb;
   dm.g0 = 0; dm.g1 = ng;
+  check_mac_tables(t);
+  REQUIRE(t.diags.p && t.diags.n >= (t.plain_idx.size() + 1) * dm.diag_stride, "linear transform: diagonal storage missing");
   for (int b0 = 0; b0 < nb; b0 += 32) {
     dm.b0 = b0; dm.nb_chunk = std::min(32, nb - b0);
     timed("diag_mac", [&] { launch_diag_mac(dm, s.st); });

@@ -405,25 +405,37 @@ class LinearLayer:
         tids = tids.reshape(rows, cols)
         cts_out = []
         io = self.scheme.io_mode != "none"
-        for i in range(rows):
-            ct_out = None
-            for j in range(cols):
-                if io:
-                    self.load_transform(i, j, int(tids[i][j]))
-                res = CipherTensor(self.scheme, [b.EvaluateLinearTransform(int(tids[i][j]), x.ids[j])], x.n)
-                if io:
-                    b.RemoveRotationKeys()
-                    b.RemovePlaintextDiagonals(int(tids[i][j]))
-                if ct_out is None:
-                    ct_out = res
+        # A prerescaled transform returns Rescale(block result): summed over
+        # several column blocks that would round each block separately, not
+        # Rescale(sum) as the Lattigo flow does, so a layer with more than
+        # one column block evaluates its transforms unrescaled and rescales
+        # the sum once.
+        pre = bool(getattr(b, "lt_output_prerescaled", False))
+        if pre and cols > 1:
+            b.set_lt_output_prerescaled(False)
+        try:
+            for i in range(rows):
+                ct_out = None
+                for j in range(cols):
+                    if io:
+                        self.load_transform(i, j, int(tids[i][j]))
+                    res = CipherTensor(self.scheme, [b.EvaluateLinearTransform(int(tids[i][j]), x.ids[j])], x.n)
+                    if io:
+                        b.RemoveRotationKeys()
+                        b.RemovePlaintextDiagonals(int(tids[i][j]))
+                    if ct_out is None:
+                        ct_out = res
+                    else:
+                        ct_out = ct_out + res
+                        res.free()
+                if pre and cols == 1:
+                    cts_out.append(ct_out.ids[0])
                 else:
-                    ct_out = ct_out + res
-                    res.free()
-            if getattr(b, "lt_output_prerescaled", False):
-                cts_out.append(ct_out.ids[0])
-            else:
-                cts_out.append(b.RescaleNew(ct_out.ids[0]))
-                ct_out.free()
+                    cts_out.append(b.RescaleNew(ct_out.ids[0]))
+                    ct_out.free()
+        finally:
+            if pre and cols > 1:
+                b.set_lt_output_prerescaled(True)
         return CipherTensor(self.scheme, cts_out, self.out_features)
 
     # linear.py:99-140 (no slicing, no fold-retag on the Lattigo path)

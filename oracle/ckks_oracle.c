@@ -721,11 +721,13 @@ void orc_decode(const orc_ctx* c, const uint64_t* pt, int level, double scale, f
  * ===================================================================== */
 static void poly_from_signed(const orc_ctx* c, const i64* v, const int* mi, int nm, u64* out) {
     int N = c->N;
+    #pragma omp parallel for num_threads(g_threads) schedule(static) if (nm > 1 && g_threads > 1)
     for (int j = 0; j < nm; j++) { u64 q = c->mod[mi[j]]; for (int x = 0; x < N; x++) out[(size_t)j * N + x] = signed_mod(v[x], q); }
 }
 static void sample_cbd(u64 seed, u64 stream, int N, i64* out) { for (int x = 0; x < N; x++) out[x] = cbd21(orc_rand64(seed, stream, (u64)x)); }
 static void sample_uniform_qp(const orc_ctx* c, u64 stream, const int* mi, int nm, u64* out) {
     int N = c->N;
+    #pragma omp parallel for num_threads(g_threads) schedule(static) if (nm > 1 && g_threads > 1)
     for (int j = 0; j < nm; j++) { u64 q = c->mod[mi[j]]; for (int x = 0; x < N; x++) out[(size_t)j * N + x] = uniform_mod(orc_rand64(c->seed, stream, (u64)mi[j] * N + x), q); }
 }
 static void full_qp_list(const orc_ctx* c, int* mi) { for (int i = 0; i < c->L + c->K; i++) mi[i] = i; }
@@ -764,6 +766,7 @@ static u64* gen_eval_key(orc_ctx* c, const u64* s_in_ntt, const u64* s_out_ntt, 
         sample_uniform_qp(c, st_a(tag, (u64)d), mi, nm, a); ntt_limbs(c, a, mi, nm);
         sample_cbd(c->seed, st_e(tag, (u64)d), N, e);
         poly_from_signed(c, e, mi, nm, b); ntt_limbs(c, b, mi, nm);
+        #pragma omp parallel for num_threads(g_threads) schedule(static) if (g_threads > 1)
         for (int j = 0; j < nm; j++) {
             u64 q = c->mod[j]; u64 Pq = 0; int own = (j < c->L) && (j >= d * K) && (j < (d + 1) * K);
             if (own) { Pq = 1; for (int k = 0; k < K; k++) Pq = orc_mulmod(Pq, c->mod[c->L + k] % q, q); }
@@ -1231,6 +1234,9 @@ static orc_lt* lt_new_impl(orc_ctx* c, const int* idx, int nidx, const float* da
             for (int g = 0; g < t->ngiant; g++) if (t->giant[g] == j) { t->baby[g][t->nbaby[g]++] = b; break; }
         }
         for (int g = 0; g < t->ngiant; g++) t->nbaby[g] = uniq_sorted(t->baby[g], t->nbaby[g]);
+        /* the plaintext list (diagonal, source row, pre-rotation) in group order,
+         * then the encodings, independent of each other, in parallel */
+        int* srcs = (int*)xmalloc(sizeof(int) * (nidx + 1)); int* rotp = (int*)xmalloc(sizeof(int) * (nidx + 1));
         for (int g = 0; g < t->ngiant; g++) {
             if (max_groups >= 0 && g >= max_groups) break;
             int j = t->giant[g]; int rot = (-j) & (slots - 1);
@@ -1238,12 +1244,22 @@ static orc_lt* lt_new_impl(orc_ctx* c, const int* idx, int nidx, const float* da
                 int di = j + t->baby[g][bi], src = -1;
                 for (int i = 0; i < nidx; i++) if (keys[i] == di || keys[i] == di - slots) { src = i; break; }
                 if (src < 0) die("lintrans: diagonal missing");
-                /* utils.RotateSliceAllocFree(v, rot): buf[k] = v[(k + rot) mod slots] */
-                for (int k = 0; k < slots; k++) buf[k] = (double)data[(size_t)src * slots + ((k + rot) & (slots - 1))];
-                t->plain_idx[t->nplain] = di; t->plain[t->nplain] = (u64*)xmalloc(8 * (size_t)nqp * N);
-                orc_encode_f64(c, buf, slots, level, scale, 1, t->plain[t->nplain]); t->nplain++;
+                t->plain_idx[t->nplain] = di; srcs[t->nplain] = src; rotp[t->nplain] = rot;
+                t->plain[t->nplain] = (u64*)xmalloc(8 * (size_t)nqp * N); t->nplain++;
             }
         }
+        #pragma omp parallel num_threads(g_threads) if (g_threads > 1 && t->nplain > 1)
+        {
+            double* vb = (double*)xmalloc(sizeof(double) * slots);
+            #pragma omp for schedule(dynamic, 1)
+            for (int pi = 0; pi < t->nplain; pi++) {
+                /* utils.RotateSliceAllocFree(v, rot): buf[k] = v[(k + rot) mod slots] */
+                for (int k = 0; k < slots; k++) vb[k] = (double)data[(size_t)srcs[pi] * slots + ((k + rotp[pi]) & (slots - 1))];
+                orc_encode_f64(c, vb, slots, level, scale, 1, t->plain[pi]);
+            }
+            free(vb);
+        }
+        free(srcs); free(rotp);
     }
     free(keys); free(buf);
     return t;

@@ -405,6 +405,12 @@ class Oracle:
         self.lts.append(t)
         return t
 
+    def lt_free(self, t):
+        """Release a transform before close() (its diagonals are the bulk of the memory)."""
+        if t in self.lts:
+            self.lts.remove(t)
+            lib().orc_lt_free(t)
+
     def lt_n1(self, t):
         return lib().orc_lt_n1(t)
 

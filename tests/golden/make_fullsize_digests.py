@@ -1,0 +1,100 @@
+"""Writes tests/golden/fullsize_digests.json: SHA-256 digests, one per
+polynomial row, of the oracle's words for the two full-size linear layers at
+N=2^16 that the GPU suite cannot afford to recompute on the CPU at test time
+(the oracle needs several minutes for the keys and the 512 diagonals):
+
+  pcmm26    26-table embedding PCMM (workload seed 3, key seed 17):
+            N=2^16, Q=[60,50x23], P=[61x8], dnum 3, 512 diagonals, 16 x 32 BSGS
+  dense_lt  dense layer W 512x256 (workload seed 4, key seed 19):
+            N=2^16, Q=[60,50x15], P=[61x6], dnum 3, 512 diagonals, 16 x 32 BSGS
+
+For each: the input ciphertext (encryption index 0 at the top level), the
+first and last encoded diagonals, one giant-step Galois key, the linear
+transform output before the rescale, and the layer output after rescale,
+hybrid fold and the (zero) bias -- each as the hex SHA-256 of the
+little-endian u64 words of every row.  Run in the build container:
+
+    python tests/golden/make_fullsize_digests.py [threads]
+"""
+import hashlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from oracle import oracle as O  # noqa: E402
+from helrm_amd import orion_host as oh  # noqa: E402
+from helrm_amd.workloads import DenseLTWorkload, PCMMWorkload  # noqa: E402
+
+CASES = {
+    "pcmm26": (PCMMWorkload, 3, 17),
+    "dense_lt": (DenseLTWorkload, 4, 19),
+}
+OUT = os.path.join(HERE, "fullsize_digests.json")
+
+
+def row_digests(a):
+    """Hex SHA-256 of every row of a u64 array (last axis = coefficients)."""
+    a = np.ascontiguousarray(a, dtype="<u8")
+    rows = a.reshape(-1, a.shape[-1])
+    return [hashlib.sha256(r.tobytes()).hexdigest() for r in rows]
+
+
+def case_digests(name, cls, seed, key_seed, log=print):
+    w = cls(None, name, seed=seed, key_seed=key_seed)
+    c = w.cfg
+    q, p = O.gen_primes(c["logn"], c["logq"], c["logp"])
+    orc = O.Oracle(c["logn"], q, p, h=c["h"], seed=key_seed)
+    try:
+        S, level, scale = orc.slots, len(q) - 1, float(1 << c["logscale"])
+        d, rots = oh.diagonalize(w.matrix, S)
+        d = d[(0, 0)]
+        idx = list(d.keys())
+        t0 = time.time()
+        ct = orc.encrypt(orc.encode(w.input, level, scale), level, 0)
+        t = orc.lt_new(idx, np.stack([d[i] for i in idx]), level, 2.0)
+        n1 = orc.lt_n1(t)
+        log(f"{name}: {len(idx)} diagonals encoded, N1 {n1} ({time.time() - t0:.0f} s)")
+        giant = n1  # the first nonzero giant step
+        gk = orc.galois_key(orc.galois_element(giant))
+        lt_out, l = orc.lt_eval(t, ct, level)
+        log(f"{name}: transform done ({time.time() - t0:.0f} s)")
+        out = orc.rescale(lt_out, l)
+        sc = scale * q[level] / q[l]
+        l -= 1
+        for i in range(1, rots + 1):
+            out = orc.add(out, orc.rotate(out, l, S // (2 ** i)), l)
+        zero = orc.encode(np.zeros(1, np.float32), l, scale)
+        out[0] = orc.add(out[0][None], zero[None], l)[0]
+        log(f"{name}: layer done ({time.time() - t0:.0f} s)")
+        return {
+            "workload_seed": seed, "key_seed": key_seed, "q": [int(v) for v in q], "p": [int(v) for v in p],
+            "level": level, "diagonals": len(idx), "N1": n1, "fold_rotations": rots,
+            "ct_in": row_digests(ct),
+            "diag_first": {"index": idx[0], "rows": row_digests(orc.lt_plaintext(t, idx[0]))},
+            "diag_last": {"index": idx[-1], "rows": row_digests(orc.lt_plaintext(t, idx[-1]))},
+            "galois_key": {"rotation": giant, "galel": int(orc.galois_element(giant)), "rows": row_digests(gk)},
+            "lt_out": {"level": level, "scale": scale * q[level], "rows": row_digests(lt_out)},
+            "out": {"level": l, "scale": sc, "rows": row_digests(out)},
+        }
+    finally:
+        orc.close()
+
+
+def main():
+    threads = int(sys.argv[1]) if len(sys.argv) > 1 else (os.cpu_count() or 1)
+    O.set_threads(threads)
+    res = {name: case_digests(name, *spec, log=lambda m: print(m, flush=True)) for name, spec in CASES.items()}
+    with open(OUT, "w") as f:
+        json.dump(res, f, indent=1)
+    print(f"wrote {OUT}")
+
+
+if __name__ == "__main__":
+    main()

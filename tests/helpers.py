@@ -153,3 +153,64 @@ def from_montgomery(rows, mods):
         rinv = pow(1 << 64, -1, int(q))
         out[i] = np.array([(int(v) * rinv) % int(q) for v in rows[i]], dtype=np.uint64)
     return out
+
+
+def row_digests(a):
+    """Hex SHA-256 of every row (last axis) of a u64 array, little-endian words,
+    as tests/golden/make_fullsize_digests.py writes them."""
+    import hashlib
+    a = np.ascontiguousarray(a, dtype="<u8")
+    return [hashlib.sha256(r.tobytes()).hexdigest() for r in a.reshape(-1, a.shape[-1])]
+
+
+def fullsize_digests(name):
+    """The oracle's digests of one full-size layer (tests/golden/fullsize_digests.json)."""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "fullsize_digests.json")
+    with open(path) as f:
+        return json.load(f)[name]
+
+
+def assert_rows_match(a, want_rows, what):
+    """Row-wise SHA-256 comparison of a u64 array with the oracle's digests;
+    names the first rows that differ."""
+    got = row_digests(a)
+    assert len(got) == len(want_rows), f"{what}: {len(got)} rows, oracle has {len(want_rows)}"
+    bad = [i for i, (g, w) in enumerate(zip(got, want_rows)) if g != w]
+    assert not bad, f"{what}: {len(bad)} of {len(got)} rows differ from the oracle, first rows {bad[:8]}"
+
+
+def check_fullsize_layer(lib, w, d, what):
+    """A set-up LinearWorkload at N=2^16 against the oracle's digests d: the
+    moduli, the input ciphertext, two encoded diagonals, one giant-step key,
+    the transform output before the rescale, and the layer output with the
+    transform's rescale both separate (Lattigo's convention) and fused into
+    its final ModDown (lt_output_prerescaled).  Returns the output."""
+    assert lib.GetModuliChain() == d["q"] and lib.GetAuxModuliChain() == d["p"]
+    tid = int(list(w.layer.transform_ids.values())[0])
+    assert lib.lt_info(tid)["N1"] == d["N1"] and w.layer.output_rotations == d["fold_rotations"]
+    cid = w.ct_in.ids[0]
+    assert_rows_match(lib.export_ciphertext(cid), d["ct_in"], f"{what} input ciphertext")
+    for k in ("diag_first", "diag_last"):
+        assert_rows_match(lib.export_lt_diagonal(tid, d[k]["index"], d["level"]), d[k]["rows"],
+                          f"{what} diagonal {d[k]['index']}")
+    assert_rows_match(lib.export_galois_key(d["galois_key"]["galel"]), d["galois_key"]["rows"],
+                      f"{what} Galois key of rotation {d['galois_key']['rotation']}")
+    lib.set_lt_output_prerescaled(False)
+    lt = lib.EvaluateLinearTransform(tid, cid)
+    assert lib.GetCiphertextLevel(lt) == d["lt_out"]["level"]
+    assert lib.GetCiphertextScaleDouble(lt) == d["lt_out"]["scale"]
+    assert_rows_match(lib.export_ciphertext(lt), d["lt_out"]["rows"], f"{what} transform output")
+    lib.DeleteCiphertext(lt)
+    out = None
+    for pre in (False, True):
+        lib.set_lt_output_prerescaled(pre)
+        if out is not None:
+            out.free()
+        out = w.run()
+        oid = out.ids[0]
+        assert lib.GetCiphertextLevel(oid) == d["out"]["level"]
+        assert lib.GetCiphertextScaleDouble(oid) == d["out"]["scale"]
+        assert_rows_match(lib.export_ciphertext(oid), d["out"]["rows"], f"{what} layer output (prerescaled {pre})")
+    return out
