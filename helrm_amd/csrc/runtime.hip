@@ -30,6 +30,15 @@
 #include "kernels.h"
 #include "../../include/helrm_hip.h"
 
+// Device scratch of RotateInto, the entry point that allocates nothing: its
+// key switch takes every temporary from this array (96 MiB, enough for a
+// rotation at N = 2^16 with 24 Q and 8 P limbs).  Each GPU holds its own copy
+// from the library's load to the process end.  Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not a device
+// address): it uses the per-device address hipGetSymbolAddress returns.
+constexpr size_t SCRATCH_WORDS = (size_t)96 << 17;
+static __device__ __align__(256) uint64_t scratch[SCRATCH_WORDS];
+
 namespace {
 
 // ============================================================================
@@ -178,7 +187,9 @@ struct Pool {
   std::unordered_map<void*, size_t> size_;
   size_t live = 0, cached = 0, peak = 0;
   int cur = 0;  // the scheme's current stream
+  int forbid = 0;  // > 0 inside an entry point that allocates nothing: get() is an error
   void* get(size_t bytes) {
+    REQUIRE(!forbid, "device allocation inside an entry point that allocates nothing");
     bytes = (bytes + 255) & ~(size_t)255;
     if (bytes == 0) bytes = 256;
     auto& fl = free_[cur];
@@ -211,6 +222,35 @@ struct Pool {
   }
 };
 Pool* g_pool = nullptr;
+
+// Device address of `scratch` per device, taken once per device when a
+// scheme is built on it (with that device current).
+// A failure is kept per device and reported by RotateInto, so that the rest
+// of the library works without the scratch array.
+std::map<int, uint64_t*> g_scratch;
+std::map<int, std::string> g_scratch_err;
+void init_scratch() {
+  int dev = 0;
+  HCHECK(hipGetDevice(&dev));
+  if (g_scratch.count(dev)) return;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr) {
+    (void)hipGetLastError();
+    g_scratch_err[dev] = std::string("device scratch has no address: ") + hipGetErrorString(e);
+    return;
+  }
+  g_scratch[dev] = static_cast<uint64_t*>(ptr);
+  g_scratch_err.erase(dev);
+}
+uint64_t* scratch_ptr() {
+  int dev = 0;
+  HCHECK(hipGetDevice(&dev));
+  auto it = g_scratch.find(dev);
+  if (it != g_scratch.end()) return it->second;
+  auto er = g_scratch_err.find(dev);
+  throw Error(er != g_scratch_err.end() ? er->second : "device scratch not set up on this device: build a scheme on it first");
+}
 
 template <class T> struct DevArray {
   T* p = nullptr; size_t n = 0;
@@ -403,6 +443,23 @@ BConvHost& bconv_table(int s0, int s1) {
   return ref;
 }
 
+// The table of a source range that must already exist (built with the
+// scheme for every digit split and for P -> Q): a lookup that allocates nothing.
+BConvHost& bconv_table_cached(int s0, int s1) {
+  Scheme& s = sch();
+  auto it = s.bconv.find(std::make_pair(s0, s1));
+  REQUIRE(it != s.bconv.end(), "basis conversion table missing");
+  return *it->second;
+}
+// Every table a key switch at any level reads: each digit [dK, min(dK+K, l+1))
+// of each level l, and the P -> Q extension of ModDown.
+void prebuild_bconv_tables() {
+  Scheme& s = sch();
+  for (int l = 0; l < s.L; l++)
+    for (int st0 = 0; st0 <= l; st0 += s.K) bconv_table(st0, std::min(st0 + s.K, l + 1));
+  bconv_table(s.L, s.L + s.K);
+}
+
 const uint32_t* perm_for(u64 galel) {
   Scheme& s = sch();
   auto it = s.perms.find(galel);
@@ -436,6 +493,12 @@ const uint32_t* perm_inv_for(u64 galel) {
   const uint32_t* p = d.p;
   s.perm_invs[galel] = std::move(d);
   return p;
+}
+// the inverse gather of an automorphism whose key exists (built with the key)
+const uint32_t* perm_inv_cached(u64 galel) {
+  auto it = sch().perm_invs.find(galel);
+  REQUIRE(it != sch().perm_invs.end(), "automorphism table missing");
+  return it->second.p;
 }
 u64 galois_element(int k) { Scheme& s = sch(); u64 M = 2 * (u64)s.N; return powmod(5, (u64)(i64)k & (M - 1), M); }
 
@@ -472,45 +535,64 @@ const DigitRows& digit_rows(int l, int batch, size_t dstride) {
 }
 
 // copy_own: also copy each digit's own rows (the key-product kernels can instead read them from c1)
-void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* digits, bool copy_own = true) {
+// coef_ws: nullptr -> the coefficient-domain copy of c1 comes from the buffer
+// cache; else batch * (l+1) * N device words the call may overwrite, and the
+// forward transforms go per digit over a RowMap (nothing is allocated)
+void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* digits, bool copy_own = true,
+                     u64* coef_ws = nullptr) {
   Scheme& s = sch();
   const int N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
   const size_t dstride = (size_t)dn * nqp * N;
-  DU64 coef((size_t)batch * (l + 1) * N);
-  ntt_oop(c1, c1_bstride, coef.p, (size_t)(l + 1) * N, batch, rows_q(l), false);
+  DU64 coef_buf;
+  if (!coef_ws) coef_buf = DU64((size_t)batch * (l + 1) * N);
+  u64* coef = coef_ws ? coef_ws : coef_buf.p;
+  ntt_oop(c1, c1_bstride, coef, (size_t)(l + 1) * N, batch, rows_q(l), false);
   // every digit's extension in one launch: targets are every QP row except the digit's own [st0, en)
   REQUIRE(dn <= HCK_MAXJOBS, "too many decomposition digits");
   BConvJobs jobs{};
   jobs.n = dn;
   for (int d = 0; d < dn; d++) {
     const int st0 = d * K, en = std::min(st0 + K, l + 1), ns = en - st0;
-    jobs.j[d] = BConvJob{bconv_table(st0, en).dtab.p, st0, ns, ns == 1 ? 1 : 0, 0, RowMap{nqp, l + 1, 0, s.L, st0, en},
+    jobs.j[d] = BConvJob{bconv_table_cached(st0, en).dtab.p, st0, ns, ns == 1 ? 1 : 0, 0, RowMap{nqp, l + 1, 0, s.L, st0, en},
                          (size_t)d * nqp * N};
   }
-  launch_bconv(coef.p, (size_t)(l + 1) * N, jobs, digits, dstride, batch, s.d_mods.p, N, s.st);
+  launch_bconv(coef, (size_t)(l + 1) * N, jobs, digits, dstride, batch, s.d_mods.p, N, s.st);
   if (copy_own)
     for (int d = 0; d < dn; d++) {
       const int st0 = d * K, ns = std::min(st0 + K, l + 1) - st0;
       u64* D = digits + (size_t)d * nqp * N;
       copy_rows(D + (size_t)st0 * N, dstride, c1 + (size_t)st0 * N, c1_bstride, (size_t)ns * N, batch);
     }
+  if (coef_ws) {
+    // a digit's extended rows: every QP row but its own [st0, en)
+    for (int d = 0; d < dn; d++) {
+      const int st0 = d * K, en = std::min(st0 + K, l + 1);
+      launch_ntt(digits + (size_t)d * nqp * N, dstride, batch, RowMap{nqp, l + 1, 0, s.L, st0, en}, s.logN, true, s.tw, s.st);
+    }
+    return;
+  }
   // one forward transform over the extended rows of every digit of every batch entry
   const DigitRows& dr = digit_rows(l, batch, dstride);
   launch_ntt_list(digits, dr.list.p, dr.n, s.logN, true, s.tw, s.st);
 }
 // out[b] (Q rows, stride o_bstride) = ModDown(x[b]) (QP rows, stride x_bstride) [+ add[b<add_batches]],
 // written through perm_inv (out[perm_inv[p]] takes position p; nullptr: identity)
+// ws: nullptr -> temporaries from the buffer cache; else batch * (K + l + 1) * N
+// device words the call may overwrite (nothing is allocated)
 void mod_down(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t o_bstride, const u64* add = nullptr,
-              size_t a_bstride = 0, int add_batches = 0, const uint32_t* perm_inv = nullptr) {
+              size_t a_bstride = 0, int add_batches = 0, const uint32_t* perm_inv = nullptr, u64* ws = nullptr) {
   Scheme& s = sch();
   const int N = s.N, K = s.K;
-  DU64 pc((size_t)batch * K * N), ext((size_t)batch * (l + 1) * N);
+  DU64 pc_buf, ext_buf;
+  if (!ws) { pc_buf = DU64((size_t)batch * K * N); ext_buf = DU64((size_t)batch * (l + 1) * N); }
+  u64* pc = ws ? ws : pc_buf.p;
+  u64* ext = ws ? ws + (size_t)batch * K * N : ext_buf.p;
   // P rows of x (rows l+1.. of each batch entry) -> coefficient domain in pc
-  ntt_oop(x + (size_t)(l + 1) * N, x_bstride, pc.p, (size_t)K * N, batch, rows_p(), false);
-  BConvHost& bt = bconv_table(s.L, s.L + K);
-  launch_bconv(pc.p, (size_t)K * N, K, bt.dtab.p, ext.p, (size_t)(l + 1) * N, batch, rows_q(l), s.d_mods.p, N, false, s.st);
+  ntt_oop(x + (size_t)(l + 1) * N, x_bstride, pc, (size_t)K * N, batch, rows_p(), false);
+  BConvHost& bt = bconv_table_cached(s.L, s.L + K);
+  launch_bconv(pc, (size_t)K * N, K, bt.dtab.p, ext, (size_t)(l + 1) * N, batch, rows_q(l), s.d_mods.p, N, false, s.st);
   // forward transform of the extension fused with (x - ext) * P^-1 (+ add), gathered through perm
-  launch_ntt_moddown(ext.p, (size_t)(l + 1) * N, batch, l, s.logN, x, x_bstride, out, o_bstride, add, a_bstride,
+  launch_ntt_moddown(ext, (size_t)(l + 1) * N, batch, l, s.logN, x, x_bstride, out, o_bstride, add, a_bstride,
                      add_batches, perm_inv, s.pinv_w.p, s.pinv_wp.p, s.tw, s.st);
 }
 
@@ -613,6 +695,7 @@ void ensure_galois_key(u64 galel) {
   launch_mont_convert(soR.p, 0, 1, rows_all(), s.d_mods.p, N, true, s.st);
   s.gkeys[galel] = gen_eval_key(s.sR.p, soR.p, [galel](int d) { return ST_GK_A(galel, (u64)d); },
                                  [galel](int d) { return ST_GK_E(galel, (u64)d); });
+  perm_for(galel); perm_inv_for(galel);
   // transforms cache key addresses: a key created after a removal lives elsewhere
   for (auto& kv : s.lts) kv.second->ptrs_ready = false;
 }
@@ -883,6 +966,8 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
     up(s.prs_inv, pri); up(s.prs_invp, prip);
     s.pinv_h.assign(pin.begin(), pin.end()); s.pinv_hp.assign(pinp.begin(), pinp.end());
     init_encoder(s);
+    prebuild_bconv_tables();
+    init_scratch();
   } catch (...) {
     S = old;
     throw;
@@ -923,22 +1008,46 @@ void ct_drop_to(Cipher& c, int level) {
 // ============================================================================
 // evaluator operations
 // ============================================================================
-std::unique_ptr<Cipher> automorphism(const Cipher& ct, u64 galel, bool lt_keyset) {
+// Key-switched automorphism of ct into out (2 (l+1) N words, out != ct):
+// c1 decomposed and extended to QP, key product fused with nothing else,
+// ModDown of both parts with sigma applied in its epilogue and c0 added.
+// ws: nullptr -> temporaries from the buffer cache; else
+// automorphism_ws_words(l) device words laid out as
+//   [digits (dn nqp N), later ModDown's pc and ext | dd (2 nqp N) | coef ((l+1) N)]
+// (the digits are dead once the key product has read them).
+size_t automorphism_ws_words(int l) {
+  Scheme& s = sch();
+  const size_t N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
+  return (std::max(dn * nqp, 2 * K + 2 * (size_t)(l + 1)) + 2 * nqp + (size_t)(l + 1)) * N;
+}
+void automorphism_core(const Cipher& ct, const u64* key, const uint32_t* perm_inv, u64* out, u64* ws) {
   Scheme& s = sch();
   const int l = ct.level, N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
-  const u64* key = key_ptr(galel, lt_keyset);
-  DU64 digits((size_t)dn * nqp * N);
-  decompose_modup(l, ct.d.p + (size_t)(l + 1) * N, 0, 1, digits.p, false);
-  DU64 dd((size_t)2 * nqp * N);
+  DU64 digits_buf, dd_buf;
+  u64 *digits, *dd, *coef = nullptr, *md = nullptr;
+  if (ws) {
+    digits = ws;
+    md = ws;
+    dd = ws + std::max((size_t)dn * nqp, 2 * (size_t)K + 2 * (size_t)(l + 1)) * N;
+    coef = dd + (size_t)2 * nqp * N;
+  } else {
+    digits_buf = DU64((size_t)dn * nqp * N); dd_buf = DU64((size_t)2 * nqp * N);
+    digits = digits_buf.p; dd = dd_buf.p;
+  }
+  decompose_modup(l, ct.d.p + (size_t)(l + 1) * N, 0, 1, digits, false, coef);
   KeyMacArgs a{};
-  a.digits = digits.p; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = nullptr; a.perm = nullptr;
+  a.digits = digits; a.dig_bstride = 0; a.digits_per_batch = 0; a.key = nullptr; a.perm = nullptr;
   a.key1 = key; a.perm1 = nullptr; a.add0 = nullptr;
   a.own = ct.d.p + (size_t)(l + 1) * N; a.own_bstride = 0;
-  a.out0 = dd.p; a.out1 = dd.p + (size_t)nqp * N; a.out_bstride = 0; a.mods = s.d_mods.p;
+  a.out0 = dd; a.out1 = dd + (size_t)nqp * N; a.out_bstride = 0; a.mods = s.d_mods.p;
   a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
   launch_keymac(a, 1, s.st);
-  auto out = new_ct(l, ct.scale); out->logslots = ct.logslots;
-  mod_down(l, dd.p, (size_t)nqp * N, 2, out->d.p, (size_t)(l + 1) * N, ct.d.p, 0, 1, perm_inv_for(galel));
+  mod_down(l, dd, (size_t)nqp * N, 2, out, (size_t)(l + 1) * N, ct.d.p, 0, 1, perm_inv, md);
+}
+std::unique_ptr<Cipher> automorphism(const Cipher& ct, u64 galel, bool lt_keyset) {
+  const u64* key = key_ptr(galel, lt_keyset);
+  auto out = new_ct(ct.level, ct.scale); out->logslots = ct.logslots;
+  automorphism_core(ct, key, perm_inv_for(galel), out->d.p, nullptr);
   return out;
 }
 // ---- plaintext, scalar and ciphertext products (Lattigo ckks Evaluator
@@ -1755,6 +1864,33 @@ int RotateNew(int ctID, int amount) {
     return push_ct(automorphism(get_ct(ctID), ge, false));
   });
 }
+// RotateNew into an existing ciphertext with no allocation: the key switch's
+// temporaries live in the device scratch array, the automorphism tables and
+// basis-conversion tables were built with the key and the scheme.  The
+// rotation key must exist already.  Calls that overlap on one GPU (another
+// stream) race on the scratch array.
+int RotateInto(int ctID, int amount, int outID) {
+  return guard([&] {
+    Scheme& s = sch();
+    REQUIRE(ctID != outID, "RotateInto: the output must be another ciphertext than the input");
+    const Cipher& c = get_ct(ctID);
+    Cipher& o = get_ct(outID);
+    const u64 ge = galois_element(amount);
+    REQUIRE(s.rot_keys.count(ge) && s.gkeys.count(ge),
+            "RotateInto: no rotation key for this amount (AddRotationKey or RotateNew generates it)");
+    const size_t need = automorphism_ws_words(c.level);
+    REQUIRE(need <= SCRATCH_WORDS, "RotateInto: the key switch needs " + std::to_string(need * 8) +
+                                       " bytes of scratch at this level, more than the " +
+                                       std::to_string(SCRATCH_WORDS * 8) + " bytes available");
+    REQUIRE(o.d.n >= (size_t)2 * (c.level + 1) * s.N, "RotateInto: the output ciphertext is too small for the input's level");
+    u64* ws = scratch_ptr();
+    // the buffer cache refuses to hand out memory until the key switch is queued
+    struct NoAlloc { NoAlloc() { g_pool->forbid++; } ~NoAlloc() { g_pool->forbid--; } } guard_alloc;
+    automorphism_core(c, s.gkeys.at(ge)->p, perm_inv_cached(ge), o.d.p, ws);
+    o.level = c.level; o.scale = c.scale; o.logslots = c.logslots;
+    return outID;
+  });
+}
 int Conjugate(int ctID) {
   return guard([&] { Scheme& s = sch(); u64 ge = 2 * (u64)s.N - 1; ensure_galois_key(ge); s.rot_keys.insert(ge);
     Cipher& c = get_ct(ctID); auto r = automorphism(c, ge, false); c.d = std::move(r->d); return ctID; });
@@ -1977,6 +2113,7 @@ int LoadRotationKey(const unsigned char* data, unsigned long len, unsigned long 
     auto k = std::make_unique<DU64>(h.size());
     upload(k->p, h.data(), h.size());
     s.gkeys[(u64)galEl] = std::move(k);
+    perm_for((u64)galEl); perm_inv_for((u64)galEl);
     s.lt_keys.insert((u64)galEl);
     // transforms cache key pointers: rebuild them on next use
     for (auto& kv : s.lts) kv.second->ptrs_ready = false;

@@ -91,6 +91,15 @@ int NewEvaluator(void);                   /* evaluator.go:13-35 (+ power-of-two 
 int AddRotationKey(int rotation);         /* evaluator.go:37-52 */
 int Rotate(int ciphertextID, int amount); /* evaluator.go:80-87 */
 int RotateNew(int ciphertextID, int amount); /* evaluator.go:89-101 */
+/* [ext] No counterpart in the reference.  For callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops): RotateNew
+ * written into the existing ciphertext outID (!= ciphertextID, with room for
+ * the input's level), calling no hipMalloc / hipFree.  The key switch's
+ * temporaries live in a static 96 MiB device array per GPU (a rotation at
+ * N = 2^16 with up to 24 Q and 8 P limbs fits; larger levels are refused
+ * with an error); the rotation key must already exist.  Calls that overlap
+ * on one GPU (two streams) race on that array.  Returns outID. */
+int RotateInto(int ciphertextID, int amount, int outID);
 int Conjugate(int ciphertextID);          /* evaluator.go:103-114 */
 int ConjugateNew(int ciphertextID);       /* evaluator.go:116-128 */
 int Rescale(int ciphertextID);            /* evaluator.go:130-136 */
