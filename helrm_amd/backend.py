@@ -263,6 +263,7 @@ _SIGNATURES = {
     "NttDevice": ([_c.c_void_p, _I, _I, _I], _I),
     "MulAccDevice": ([_c.c_void_p, _c.c_void_p, _c.c_void_p, _I, _I], _I),
     "GetStream": ([], _c.c_void_p),
+    "ValuPeakProbe": ([_c.POINTER(_c.c_double), _I], _I),
     "KernelTimingEnable": ([_I], _I),
     "KernelTimingGet": ([_c.c_char_p, _c.POINTER(_c.c_long), _c.POINTER(_c.c_double)], _I),
     "GetMemoryStats": ([_PU64, _PU64, _PU64], _I),
@@ -427,6 +428,13 @@ class HipLibrary:
         tot = ctypes.c_double(0.0)
         self.KernelTimingGet(name, ctypes.byref(cnt), ctypes.byref(tot))
         return int(cnt.value), float(tot.value)
+
+    def valu_peak(self):
+        """Integer VALU issue rate measured on the device (ValuPeakProbe)."""
+        out = (ctypes.c_double * 5)()
+        self.ValuPeakProbe(out, 5)
+        return {"wave_instr_per_s": out[0], "cus": int(out[1]), "wave_instr_per_clk_per_cu": out[2],
+                "v_mad_u64_u32_per_s": out[3], "v_add3_u32_per_s": out[4]}
 
     def memory_stats(self):
         a, b, c = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()

@@ -153,3 +153,7 @@ void launch_mul_i(u64* out, const u64* in, size_t bstride, int batch, RowMap rm,
                   const u64* niu, const u64* niup, const ModC* mods, int N, hipStream_t st);
 // out[r][x] = sum_{p < npoly} a[p][r][x] * b[p][r][x] mod q_r, rows r < nrows of the modulus table
 void launch_mulacc(const u64* a, const u64* b, u64* out, int npoly, int nrows, const ModC* mods, int N, hipStream_t st);
+// Integer VALU issue-rate probe: `blocks` workgroups of 256 lanes, each lane
+// iters x 8 independent instructions (op 0: v_mad_u64_u32, op 1: v_add3_u32);
+// one word per lane written to out.
+void launch_valu_probe(int op, u64* out, int blocks, uint32_t seed, int iters, hipStream_t st);

@@ -672,3 +672,41 @@ void launch_gk_combine(u64* b, const u64* a, const u64* soR, const u64* sR, int 
   hipLaunchKernelGGL(gk_combine_kernel, dim3(N / 256, rows, 1), dim3(256), 0, st, b, a, soR, sR, own0, own1, pmod, mods, N);
 }
 
+
+// ---------------------------------------------------------------------------
+// Integer VALU issue-rate probe: every lane runs iters x 8 independent
+// instructions of one kind, so the launch is limited by VALU issue alone:
+//   op 0: v_mad_u64_u32 (the 32 x 32 + 64 multiply-add the NTT butterflies,
+//         key products and basis conversions are built from; its carry-out
+//         goes to an SGPR pair that is never read)
+//   op 1: v_add3_u32 (a plain full-rate 32-bit integer instruction)
+// The faster of the two is the integer issue peak that VALU utilisation is
+// quoted against.
+// ---------------------------------------------------------------------------
+template <int OP>
+__global__ __launch_bounds__(256) void valu_probe_kernel(u64* __restrict__ out, uint32_t seed, int iters) {
+  uint32_t a[8];
+  u64 b[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) { a[i] = seed + threadIdx.x * 7u + (uint32_t)i; b[i] = (u64)a[i] * 0x12345ull; }
+  const uint32_t c = seed | 1u;
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      if (OP == 0) {
+        u64 junk;
+        asm volatile("v_mad_u64_u32 %0, %1, %2, %3, %0" : "+v"(b[i]), "=s"(junk) : "v"(a[i]), "v"(c));
+      } else {
+        asm volatile("v_add3_u32 %0, %0, %1, %1" : "+v"(a[i]) : "v"(c));
+      }
+    }
+  }
+  u64 s = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) s += a[i] + b[i];
+  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+void launch_valu_probe(int op, u64* out, int blocks, uint32_t seed, int iters, hipStream_t st) {
+  if (op == 0) hipLaunchKernelGGL((valu_probe_kernel<0>), dim3(blocks), dim3(256), 0, st, out, seed, iters);
+  else hipLaunchKernelGGL((valu_probe_kernel<1>), dim3(blocks), dim3(256), 0, st, out, seed, iters);
+}

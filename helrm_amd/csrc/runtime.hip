@@ -1047,7 +1047,7 @@ void automorphism_core(const Cipher& ct, const u64* key, const uint32_t* perm_in
 std::unique_ptr<Cipher> automorphism(const Cipher& ct, u64 galel, bool lt_keyset) {
   const u64* key = key_ptr(galel, lt_keyset);
   auto out = new_ct(ct.level, ct.scale); out->logslots = ct.logslots;
-  automorphism_core(ct, key, perm_inv_for(galel), out->d.p, nullptr);
+  timed("rotate", [&] { automorphism_core(ct, key, perm_inv_for(galel), out->d.p, nullptr); });
   return out;
 }
 // ---- plaintext, scalar and ciphertext products (Lattigo ckks Evaluator
@@ -2389,6 +2389,42 @@ int JoinStream(int idx) {
   });
 }
 void* GetStream(void) { return S ? (void*)S->st : nullptr; }
+// [ext] integer VALU issue rate, wave-instructions per second over the
+// whole GPU: out[0] = the peak (the faster of the two probes), out[1] =
+// compute units, out[2] = the peak per compute unit and clock at the
+// device's peak clock, out[3] = v_mad_u64_u32 alone, out[4] = v_add3_u32.
+int ValuPeakProbe(double* out, int len) {
+  return guard([&] {
+    Scheme& s = sch();
+    REQUIRE(out && len >= 5, "ValuPeakProbe needs 5 outputs");
+    int dev = 0;
+    HCHECK(hipGetDevice(&dev));
+    hipDeviceProp_t prop;
+    HCHECK(hipGetDeviceProperties(&prop, dev));
+    const int cus = prop.multiProcessorCount, blocks = cus * 16, iters = 4096;
+    DU64 buf((size_t)blocks * 256);
+    hipEvent_t a, b;
+    HCHECK(hipEventCreate(&a)); HCHECK(hipEventCreate(&b));
+    double rate[2];
+    for (int op = 0; op < 2; op++) {
+      launch_valu_probe(op, buf.p, blocks, 3u, iters, s.st);  // warm-up (clocks up)
+      HCHECK(hipEventRecord(a, s.st));
+      launch_valu_probe(op, buf.p, blocks, 5u, iters, s.st);
+      HCHECK(hipEventRecord(b, s.st));
+      HCHECK(hipEventSynchronize(b));
+      float ms = 0;
+      HCHECK(hipEventElapsedTime(&ms, a, b));
+      rate[op] = (double)blocks * (256 / 64) * iters * 8 / (ms * 1e-3);
+    }
+    (void)hipEventDestroy(a); (void)hipEventDestroy(b);
+    out[0] = std::max(rate[0], rate[1]);
+    out[1] = cus;
+    out[2] = out[0] / cus / ((double)prop.clockRate * 1e3);
+    out[3] = rate[0];
+    out[4] = rate[1];
+    return 0;
+  });
+}
 int KernelTimingEnable(int on) { return guard([&] { Scheme& s = sch(); sync(); timing_collect(); s.timing.acc.clear(); s.timing.on = on != 0; return 0; }); }
 int KernelTimingGet(const char* name, long* count, double* total_ms) {
   return guard([&] {

@@ -221,6 +221,11 @@ void* GetStream(void);                                            /* hipStream_t
  * stream that last used it is current, or after joining that stream. */
 int SetStream(int idx);
 int JoinStream(int idx);
+/* [ext] integer VALU issue-rate probe (measurement only), wave-instructions
+ * per second over the GPU: out[0] = peak (the faster probe), out[1] = compute
+ * units, out[2] = the peak per compute unit per clock (peak clock), out[3] =
+ * v_mad_u64_u32 alone, out[4] = v_add3_u32 alone. */
+int ValuPeakProbe(double* out, int len);
 int KernelTimingEnable(int on);                                   /* HIP events around named launches */
 int KernelTimingGet(const char* name, long* count, double* total_ms);
 int GetMemoryStats(uint64_t* live, uint64_t* cached, uint64_t* peak);
