@@ -150,27 +150,41 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
   const int x = blockIdx.x * blockDim.x + threadIdx.x;
   const u64* inb = in + (size_t)b * in_bstride + (size_t)J.src_row * N;
   u64* outb = out + (size_t)b * out_bstride + J.out_off;
+  const RowMap rm = J.rm;
+  const int r0 = blockIdx.y * jobs.rows_per_block;
+  const int r1 = min(r0 + jobs.rows_per_block, rm.nact());
   u64 y[MAXS];
   double vf = 0.0;
   // every source word in flight at once (rows past ns re-read row 0, unused)
 #pragma unroll
   for (int i = 0; i < MAXS; i++) y[i] = inb[(size_t)(i < ns ? i : 0) * N + x];
-#pragma unroll
-  for (int i = 0; i < MAXS; i++) {
-    if (i < ns) {
-      const BConvSrc s = tab->src[i];
-      y[i] = shoup_mul(y[i], s.hinv, s.hinvp, s.q);
-      vf += (double)y[i] / s.qd;
-    } else {
-      y[i] = 0;
+  // v*S mod t of this workgroup's destination rows for every v = 0..ns,
+  // staged in LDS once: read per lane from memory inside the row loop it
+  // would put an L2 round trip on every destination row
+  __shared__ u64 svs[HCK_MAXMOD * (MAXS + 1)];
+  {
+    const u64* __restrict__ vS = tab->vS;
+    const int w = ns + 1, n = (r1 - r0) * w;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+      const int rr = e / w;
+      svs[e] = vS[(size_t)rm.mod(rm.row(r0 + rr)) * w + (e - rr * w)];
     }
   }
+  __syncthreads();
+  // the source constants are read without a branch per source (entries past
+  // ns are zero and their terms are selected away), so that their scalar
+  // loads are issued together instead of one round trip per source
+#pragma unroll
+  for (int i = 0; i < MAXS; i++) {
+    const BConvSrc s = tab->src[i];
+    const bool act = i < ns;
+    const u64 yi = shoup_mul(y[i], s.hinv, s.hinvp, s.q);
+    const double t = (double)yi / s.qd;
+    y[i] = act ? yi : 0;
+    vf += act ? t : 0.0;
+  }
   const int v = J.force_v0 ? 0 : (int)(u64)vf;
-  const RowMap rm = J.rm;
-  const int r0 = blockIdx.y * jobs.rows_per_block;
-  const int r1 = min(r0 + jobs.rows_per_block, rm.nact());
   const u64* __restrict__ hat = tab->hat;
-  const u64* __restrict__ vS = tab->vS;
   for (int r = r0; r < r1; r++) {
     const int row = rm.row(r);
     const int m = rm.mod(row);
@@ -207,7 +221,7 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
       }
       res = redc((u64)acc, fold_hi4((u64)(acc >> 64), mc.q), mc.q, mc.qinv);
     }
-    res = sub_mod(res, vS[(size_t)m * (ns + 1) + v], mc.q);
+    res = sub_mod(res, svs[(r - r0) * (ns + 1) + v], mc.q);
     outb[(size_t)row * N + x] = res;
   }
 }

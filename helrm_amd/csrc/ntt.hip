@@ -10,6 +10,8 @@
 // A sub-transform of size 2^S is computed by 2^(S-4) threads holding 16
 // words each in registers: one radix-16 round (4 butterfly stages without
 // any exchange), one LDS exchange, one round of the remaining S-4 stages.
+// Launches over few limbs use kernels with 8 words per thread instead
+// (rounds of 3 stages, twice the waves per limb).
 // Butterflies are lazy (Harvey): forward values stay in [0, 4q), inverse
 // values in [0, 2q); each pass's output is reduced to [0, q) only where the
 // transform ends, so the result equals the textbook NTT word for word.
@@ -57,9 +59,11 @@ __device__ __forceinline__ void round_tw_load_tab(RoundTw<NST>& T, const uint4* 
 #pragma unroll
   for (int sl = 0; sl < ntt_round_slots(NST); sl++) T.t[sl] = tab[(size_t)sl * P];
 }
-// NST butterfly stages on v[16] with the preloaded twiddles.
-template <bool FWD, int NST>
-__device__ __forceinline__ void ntt_round(u64 (&v)[16], const RoundTw<NST>& T, u64 q) {
+// NST butterfly stages on v[W]; tw_at(s, k, sl) gives twiddle k of stage s
+// (slot sl of the round): a preloaded RoundTw in the 16-word kernels, a load
+// per stage in the 8-word ones.
+template <bool FWD, int NST, int W = 16, class TWF>
+__device__ __forceinline__ void ntt_round_f(u64 (&v)[W], TWF tw_at, u64 q) {
   const u64 q2 = q + q, q4 = q2 + q2, nq = 0 - q;
   int sl = 0;
 #pragma unroll
@@ -67,9 +71,12 @@ __device__ __forceinline__ void ntt_round(u64 (&v)[16], const RoundTw<NST>& T, u
     const int lrd = FWD ? NST - 1 - s : s;  // log2 of the register distance
     const int rd = 1 << lrd;
     const int sh = lrd + 1;
+    uint4 ts[W >> 1];
 #pragma unroll
-    for (int k = 0; k < (16 >> sh); k++, sl++) {
-      const uint4 t4 = T.t[sl];
+    for (int k = 0; k < (W >> sh); k++) ts[k] = tw_at(s, k, sl + k);
+#pragma unroll
+    for (int k = 0; k < (W >> sh); k++, sl++) {
+      const uint4 t4 = ts[k];
       const u64 w = ((u64)t4.y << 32) | t4.x, wp = ((u64)t4.w << 32) | t4.z;
 #pragma unroll
       for (int r = 0; r < rd; r++) {
@@ -92,6 +99,11 @@ __device__ __forceinline__ void ntt_round(u64 (&v)[16], const RoundTw<NST>& T, u
       }
     }
   }
+}
+// NST butterfly stages on v[16] with the preloaded twiddles.
+template <bool FWD, int NST>
+__device__ __forceinline__ void ntt_round(u64 (&v)[16], const RoundTw<NST>& T, u64 q) {
+  ntt_round_f<FWD, NST>(v, [&](int, int, int sl) { return T.t[sl]; }, q);
 }
 
 // LDS column swizzle for the row pass: conflict-free both for the strided
@@ -317,6 +329,219 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 8 words per thread, for launches of few limbs.  A sub-transform of 2^S
+// points is computed by T = 2^(S-3) threads in rounds of at most 3 stages
+// (ceil(S/3) rounds, an LDS exchange between rounds): twice the waves of the
+// 16-word kernels per limb and half the instruction chain per wave, so a
+// launch over a few dozen limbs keeps more SIMDs busy.  Forward round k acts
+// on element bits [ls_k, ls_k + width_k) with ls_k = max(0, S - 3(k+1)),
+// width_k = min(3, S - 3k); register i of thread t holds element
+//   e = ((t >> ls_k) << (ls_k + 3)) | (i << ls_k) | (t & (2^ls_k - 1)).
+// The inverse runs the same rounds in the opposite order.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int w8_ls(int S, int k) { return S - 3 * (k + 1) > 0 ? S - 3 * (k + 1) : 0; }
+__host__ __device__ constexpr int w8_width(int S, int k) { return S - 3 * k < 3 ? S - 3 * k : 3; }
+__device__ __forceinline__ int w8_elem(int ls, int t, int i) {
+  return ((t >> ls) << (ls + 3)) | (i << ls) | (t & ((1 << ls) - 1));
+}
+// LDS position of element e inside a row (bijection on [0, 2^S), S >= 4):
+// XOR of bits 3..6 into bits 0..3 keeps all three access patterns of the
+// 256-point row pass free of bank conflicts.
+__device__ __forceinline__ int w8_swz(int e) { return e ^ ((e >> 3) & 15); }
+
+// One round k of the 8-word transform: element e of the sub-transform stands
+// for global index base + e * stride (stride = 2^lstride); twiddle pairs as
+// in round_tw_load with A the element-block base of the thread.
+template <bool FWD, int S, int K>
+__device__ __forceinline__ void w8_round(u64 (&v)[8], int t, u64 base, int lstride, u64 Nn, const uint4* __restrict__ tw,
+                                         u64 q) {
+  constexpr int ls = w8_ls(S, K), width = w8_width(S, K);
+  if constexpr (width > 0) {
+    const u64 A = base + ((u64)((t >> ls) << (ls + 3)) << lstride);
+    const int LS = ls + lstride;
+    ntt_round_f<FWD, width, 8>(v, [&](int st, int k, int) {
+      const int sh = (FWD ? width - 1 - st : st) + 1;
+      return tw[((Nn + A) >> (LS + sh)) + k];
+    }, q);
+  }
+}
+
+// Column pass, 8 words per thread: workgroup = nsub columns x R rows, T
+// threads per column (512 threads for 16 columns).
+template <bool FWD, int S>
+__global__ __launch_bounds__(512) void ntt_col8_kernel(NttArgs a) {
+  __shared__ u64 sm[4096];
+  constexpr int T = 1 << (S - 3), NR = (S + 2) / 3;
+  const int nsub = a.nsub;
+  const int tid = threadIdx.x;
+  const int c = tid & (nsub - 1);
+  const int t = tid / nsub;  // in [0, T)
+  const LimbRef lr = limb_ref(a, blockIdx.y);
+  const int m = lr.mod;
+  const u64 q = a.mods[m].q;
+  const u64 Nn = 1ull << a.logN;
+  const int SB = a.SB;
+  const size_t C = (size_t)1 << SB;
+  const int col = blockIdx.x * nsub + c;
+  u64* poly = a.data + lr.off + col;
+  const uint4* tw = a.tw + (size_t)m * Nn;
+  u64 v[8];
+  (void)T;
+  if (FWD) {
+    const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + col;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = in[(size_t)w8_elem(w8_ls(S, 0), t, i) * C];
+    w8_round<true, S, 0>(v, t, 0, SB, Nn, tw, q);
+#pragma unroll
+    for (int k = 1; k < NR; k++) {
+      const int lp = w8_ls(S, k - 1), lc = w8_ls(S, k);
+      if (k > 1) __syncthreads();  // the previous exchange has been read
+#pragma unroll
+      for (int i = 0; i < 8; i++) sm[w8_elem(lp, t, i) * nsub + c] = v[i];
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = sm[w8_elem(lc, t, i) * nsub + c];
+      if (k == 1) w8_round<true, S, 1>(v, t, 0, SB, Nn, tw, q);
+      if (k == 2) w8_round<true, S, 2>(v, t, 0, SB, Nn, tw, q);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) poly[(size_t)w8_elem(w8_ls(S, NR - 1), t, i) * C] = v[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = poly[(size_t)w8_elem(w8_ls(S, NR - 1), t, i) * C];
+#pragma unroll
+    for (int k = NR - 1; k >= 0; k--) {
+      if (k < NR - 1) {
+        const int lp = w8_ls(S, k + 1), lc = w8_ls(S, k);
+        if (k < NR - 2) __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; i++) sm[w8_elem(lp, t, i) * nsub + c] = v[i];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = sm[w8_elem(lc, t, i) * nsub + c];
+      }
+      if (k == 2) w8_round<false, S, 2>(v, t, 0, SB, Nn, tw, q);
+      if (k == 1) w8_round<false, S, 1>(v, t, 0, SB, Nn, tw, q);
+      if (k == 0) w8_round<false, S, 0>(v, t, 0, SB, Nn, tw, q);
+    }
+    const u64 ni = a.ninv[m], nip = a.ninvp[m];
+#pragma unroll
+    for (int i = 0; i < 8; i++) poly[(size_t)w8_elem(w8_ls(S, 0), t, i) * C] = csub(shoup_lazy(v[i], ni, nip, 0 - q), q);
+  }
+}
+
+// Row pass, 8 words per thread: workgroup = nsub rows x C columns, T threads
+// per row.  Global memory is read and written in the round-0 element order
+// (consecutive lanes, consecutive words); the other rounds go through LDS.
+template <bool FWD, int S, bool EPI = false>
+__global__ __launch_bounds__(256) void ntt_row8_kernel(NttArgs a) {
+  __shared__ u64 sm[2048];
+  constexpr int T = 1 << (S - 3), C = 1 << S, NR = (S + 2) / 3;
+  constexpr int L0 = w8_ls(S, 0), LL = w8_ls(S, NR - 1);
+  const int tid = threadIdx.x;
+  const int t = tid & (T - 1);
+  const int rho = tid >> (S - 3);
+  const LimbRef lr = limb_ref(a, blockIdx.y);
+  const int m = lr.mod;
+  const u64 q = a.mods[m].q;
+  const u64 Nn = 1ull << a.logN;
+  const int r = blockIdx.x * a.nsub + rho;  // row of the R x C view
+  u64* poly = a.data + lr.off + (size_t)r * C;
+  u64* srow = sm + rho * C;
+  const uint4* tw = a.tw + (size_t)m * Nn;
+  const u64 A = (u64)r * C;
+  u64 v[8];
+  if (FWD) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = __builtin_nontemporal_load(&poly[w8_elem(L0, t, i)]);
+    w8_round<true, S, 0>(v, t, A, 0, Nn, tw, q);
+#pragma unroll
+    for (int k = 1; k < NR; k++) {
+      const int lp = w8_ls(S, k - 1), lc = w8_ls(S, k);
+      if (k > 1) __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 8; i++) srow[w8_swz(w8_elem(lp, t, i))] = v[i];
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = srow[w8_swz(w8_elem(lc, t, i))];
+      if (k == 1) w8_round<true, S, 1>(v, t, A, 0, Nn, tw, q);
+      if (k == 2) w8_round<true, S, 2>(v, t, A, 0, Nn, tw, q);
+    }
+    // canonical values back in round-0 order for coalesced stores
+    const u64 q2 = q + q;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; i++) srow[w8_swz(w8_elem(LL, t, i))] = csub(csub(csub(v[i], q2 + q2), q2), q);
+    __syncthreads();
+    if (EPI) {
+      const int b = lr.pad, row = (int)((lr.off - (int64_t)b * (int64_t)a.bstride) >> a.logN);
+      const size_t rowoff = ((size_t)row << a.logN) + (size_t)r * C;
+      const u64* xr = a.e.x + (size_t)b * a.e.x_bstride + rowoff;
+      const u64* ar = (a.e.add && b < a.e.add_batches) ? a.e.add + (size_t)b * a.e.a_bstride + rowoff : nullptr;
+      u64* orow = a.e.out + (size_t)b * a.e.o_bstride + ((size_t)row << a.logN);
+      const u64 pi = a.e.pinv[m], pip = a.e.pinvp[m];
+      u64 xv[8], av[8];
+      uint32_t dst[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) xv[i] = __builtin_nontemporal_load(&xr[w8_elem(L0, t, i)]);
+      if (ar) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) av[i] = __builtin_nontemporal_load(&ar[w8_elem(L0, t, i)]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) av[i] = 0;
+      }
+      if (a.e.perm_inv) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) dst[i] = a.e.perm_inv[r * C + w8_elem(L0, t, i)];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) dst[i] = (uint32_t)(r * C + w8_elem(L0, t, i));
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int pos = w8_elem(L0, t, i);
+        const u64 o = shoup_mul(sub_mod(xv[i], srow[w8_swz(pos)], q), pi, pip, q);
+        __builtin_nontemporal_store(add_mod(o, av[i], q), &orow[dst[i]]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int pos = w8_elem(L0, t, i);
+        __builtin_nontemporal_store(srow[w8_swz(pos)], &poly[pos]);
+      }
+    }
+  } else {
+    const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + (size_t)r * C;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = __builtin_nontemporal_load(&in[w8_elem(L0, t, i)]);
+#pragma unroll
+    for (int i = 0; i < 8; i++) srow[w8_swz(w8_elem(L0, t, i))] = v[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = srow[w8_swz(w8_elem(LL, t, i))];
+#pragma unroll
+    for (int k = NR - 1; k >= 0; k--) {
+      if (k < NR - 1) {
+        const int lp = w8_ls(S, k + 1), lc = w8_ls(S, k);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; i++) srow[w8_swz(w8_elem(lp, t, i))] = v[i];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = srow[w8_swz(w8_elem(lc, t, i))];
+      }
+      if (k == 2) w8_round<false, S, 2>(v, t, A, 0, Nn, tw, q);
+      if (k == 1) w8_round<false, S, 1>(v, t, A, 0, Nn, tw, q);
+      if (k == 0) w8_round<false, S, 0>(v, t, A, 0, Nn, tw, q);
+    }
+    // the last round is round 0: its order is the coalesced one
+#pragma unroll
+    for (int i = 0; i < 8; i++) __builtin_nontemporal_store(v[i], &poly[w8_elem(L0, t, i)]);
+  }
+}
+
 template <bool FWD>
 void launch_col(int S, dim3 grid, dim3 block, const NttArgs& a, hipStream_t st) {
   switch (S) {
@@ -342,6 +567,29 @@ void launch_row(int S, dim3 grid, dim3 block, const NttArgs& a, hipStream_t st) 
   if (FWD && a.epi) launch_row_t<true, true>(S, grid, block, a, st);
   else launch_row_t<FWD, false>(S, grid, block, a, st);
 }
+template <bool FWD>
+void launch_col8(int S, dim3 grid, dim3 block, const NttArgs& a, hipStream_t st) {
+  switch (S) {
+    case 5: hipLaunchKernelGGL((ntt_col8_kernel<FWD, 5>), grid, block, 0, st, a); break;
+    case 6: hipLaunchKernelGGL((ntt_col8_kernel<FWD, 6>), grid, block, 0, st, a); break;
+    case 7: hipLaunchKernelGGL((ntt_col8_kernel<FWD, 7>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((ntt_col8_kernel<FWD, 8>), grid, block, 0, st, a); break;
+  }
+}
+template <bool FWD, bool EPI>
+void launch_row8_t(int S, dim3 grid, dim3 block, const NttArgs& a, hipStream_t st) {
+  switch (S) {
+    case 5: hipLaunchKernelGGL((ntt_row8_kernel<FWD, 5, EPI>), grid, block, 0, st, a); break;
+    case 6: hipLaunchKernelGGL((ntt_row8_kernel<FWD, 6, EPI>), grid, block, 0, st, a); break;
+    case 7: hipLaunchKernelGGL((ntt_row8_kernel<FWD, 7, EPI>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((ntt_row8_kernel<FWD, 8, EPI>), grid, block, 0, st, a); break;
+  }
+}
+template <bool FWD>
+void launch_row8(int S, dim3 grid, dim3 block, const NttArgs& a, hipStream_t st) {
+  if (FWD && a.epi) launch_row8_t<true, true>(S, grid, block, a, st);
+  else launch_row8_t<FWD, false>(S, grid, block, a, st);
+}
 
 }  // namespace
 
@@ -364,10 +612,33 @@ void launch_ntt(u64* data, size_t bstride, int batch, RowMap rm, int logN, bool 
 
 // Workgroup shape: 256-thread tiles (narrower tiles lose coalescing and
 // measured slower even for launches of a few limbs).
+// Launches over at most this many limbs use the 8-word kernels (a launch of
+// few limbs leaves most SIMDs with one or two waves of the 16-word kernels).
+#ifndef NTT_W8_MAX_LIMBS
+#define NTT_W8_MAX_LIMBS 96
+#endif
+
 static void ntt_launch(NttArgs a, int nlimbs, bool forward, hipStream_t st) {
   int SA, SB;
   ntt_split(a.logN, &SA, &SB);
   a.SA = SA; a.SB = SB;
+  if (nlimbs <= NTT_W8_MAX_LIMBS) {
+    const int TA = 1 << (SA - 3), TB = 1 << (SB - 3), C = 1 << SB, R = 1 << SA;
+    const int nsubA = std::min(512 / TA, C), nsubB = std::min(256 / TB, R);
+    NttArgs aA = a; aA.nsub = nsubA;
+    NttArgs aB = a; aB.nsub = nsubB;
+    if (forward) { aB.src = a.data; aB.sstride = a.bstride; } else { aA.src = a.data; aA.sstride = a.bstride; }
+    dim3 gridA(C / nsubA, nlimbs), blockA(TA * nsubA);
+    dim3 gridB(R / nsubB, nlimbs), blockB(TB * nsubB);
+    if (forward) {
+      launch_col8<true>(SA, gridA, blockA, aA, st);
+      launch_row8<true>(SB, gridB, blockB, aB, st);
+    } else {
+      launch_row8<false>(SB, gridB, blockB, aB, st);
+      launch_col8<false>(SA, gridA, blockA, aA, st);
+    }
+    return;
+  }
   const int PA = 1 << (SA - 4), C = 1 << SB, R = 1 << SA;
   const int PB = 1 << (SB - 4);
   const int nsubA = std::min(NTT_TPB / PA, C), nsubB = std::min(NTT_TPB / PB, R);
