@@ -164,6 +164,10 @@ _SIGNATURES = {
     "LoadRotationKey": ([_PB, _c.c_ulong, _c.c_ulong], _I),
     "SerializeDiagonal": ([_I, _I], ArrayResultByte),
     "LoadPlaintextDiagonal": ([_PB, _c.c_ulong, _I, _c.c_ulong], _I),
+    "SerializeCiphertext": ([_I], ArrayResultByte),
+    "LoadCiphertext": ([_PB, _c.c_ulong], _I),
+    "SerializePlaintext": ([_I], ArrayResultByte),
+    "LoadPlaintext": ([_PB, _c.c_ulong], _I),
     "RemovePlaintextDiagonals": ([_I], _I),
     "EncodeComplex": ([_PF, _I, _I, _c.c_ulong], _I),
     "DecodeComplex": ([_I], ArrayResultFloat),
@@ -428,6 +432,14 @@ class HipLibrary:
         tot = ctypes.c_double(0.0)
         self.KernelTimingGet(name, ctypes.byref(cnt), ctypes.byref(tot))
         return int(cnt.value), float(tot.value)
+
+    def serialize(self, fn, *args):
+        """Bytes of a Serialize* entry point as a numpy uint8 copy (the
+        library's buffer is released)."""
+        data, ptr = getattr(self, fn)(*args)
+        if ptr:
+            self.FreeCArray(ptr)
+        return data
 
     def valu_peak(self):
         """Integer VALU issue rate measured on the device (ValuPeakProbe)."""

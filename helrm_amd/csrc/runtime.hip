@@ -1648,6 +1648,14 @@ unsigned long scale_to_ulong(double sc) { if (!(sc < 18446744073709551616.0)) re
 //                dnum, then per digit: 1, 2, (b, a) as ringqp.Poly
 //   diagonal     ringqp.Poly at the transform's level
 // Everything stays in the NTT domain and in Montgomery form (x * 2^64 mod q).
+// Ciphertexts and plaintexts (no counterpart in the reference, which never
+// serializes them) follow the field order of Lattigo v6's rlwe.Element:
+// metadata, then the vector of polynomials:
+//   metadata     scale (IEEE-754 binary64 bits), log2 slots, flags
+//                (bit 0 batched, bit 1 NTT domain, bit 2 Montgomery form)
+//   vector       count (2 ciphertext, 1 plaintext), then count ring.Poly
+// with standard representatives in the NTT domain (flags 0b011).
+constexpr u64 WIRE_ELEM_FLAGS = 0x3;
 struct Wire {
   std::vector<uint8_t> b;
   void u64v(u64 x) { for (int i = 0; i < 8; i++) b.push_back((uint8_t)(x >> (8 * i))); }
@@ -1695,6 +1703,45 @@ ArrayResultByte bytes_result(const std::vector<uint8_t>& v) {
   ArrayResultByte r;
   r.Data = (char*)c_array(v); r.Length = v.size();
   return r;
+}
+std::vector<uint8_t> serialize_element(const u64* d, int npoly, int level, double scale, int logslots) {
+  Scheme& s = sch();
+  const int N = s.N;
+  std::vector<u64> h((size_t)npoly * (level + 1) * N);
+  download(h.data(), d, h.size());
+  Wire w;
+  u64 bits;
+  std::memcpy(&bits, &scale, 8);
+  w.u64v(bits); w.u64v((u64)logslots); w.u64v(WIRE_ELEM_FLAGS);
+  w.u64v((u64)npoly);
+  for (int p = 0; p < npoly; p++) w.poly(h.data() + (size_t)p * (level + 1) * N, level + 1, N);
+  return w.b;
+}
+// parses an element written by serialize_element; returns its words
+// (npoly x rows x N), level, scale and log2 slots
+std::vector<u64> parse_element(const unsigned char* data, size_t len, int npoly, int& level, double& scale, int& logslots) {
+  Scheme& s = sch();
+  const int N = s.N;
+  REQUIRE(data, "no data");
+  WireIn in{data, len};
+  const u64 bits = in.u64v();
+  std::memcpy(&scale, &bits, 8);
+  REQUIRE(std::isfinite(scale) && scale > 0, "serialized scale is not a positive number");
+  const u64 ls = in.u64v();
+  REQUIRE(ls >= 1 && ls <= (u64)(s.logN - 1), "serialized slot count does not fit the ring");
+  logslots = (int)ls;
+  REQUIRE(in.u64v() == WIRE_ELEM_FLAGS, "serialized element is not in the NTT domain with standard representatives");
+  REQUIRE(in.u64v() == (u64)npoly, npoly == 2 ? "serialized element is not a degree-1 ciphertext" : "serialized element is not a plaintext");
+  // the row count of the first polynomial fixes the level
+  REQUIRE(in.off + 8 <= in.n, "serialized data truncated");
+  u64 rows = 0;
+  for (int i = 0; i < 8; i++) rows |= (u64)in.p[in.off + i] << (8 * i);
+  REQUIRE(rows >= 1 && rows <= (u64)s.L, "serialized element has more limbs than the Q chain");
+  level = (int)rows - 1;
+  std::vector<u64> h((size_t)npoly * rows * N);
+  for (int p = 0; p < npoly; p++) in.poly(h.data() + (size_t)p * rows * N, (int)rows, N, s.mod, 0);
+  in.end();
+  return h;
 }
 std::vector<uint8_t> serialize_galois_key(u64 galel, const DU64& key) {
   Scheme& s = sch();
@@ -2166,6 +2213,50 @@ int LoadPlaintextDiagonal(const unsigned char* data, unsigned long len, int tran
     upload(t.diags.p + p * nqp * N, h.data(), h.size());
     t.resident[p] = 1;
     return 0;
+  });
+}
+// [ext] ciphertexts and plaintexts in the wire layout (no counterpart in the
+// reference: its backends never serialize them)
+ArrayResultByte SerializeCiphertext(int ciphertextID) {
+  ArrayResultByte r{nullptr, 0};
+  guard([&] {
+    const Cipher& c = get_ct(ciphertextID);
+    r = bytes_result(serialize_element(c.d.p, 2, c.level, c.scale, c.logslots));
+    return 0;
+  });
+  return r;
+}
+int LoadCiphertext(const unsigned char* data, unsigned long len) {
+  return guard([&] {
+    int level, logslots;
+    double scale;
+    std::vector<u64> h = parse_element(data, (size_t)len, 2, level, scale, logslots);
+    auto c = new_ct(level, scale);
+    c->logslots = logslots;
+    upload(c->d.p, h.data(), h.size());
+    return push_ct(std::move(c));
+  });
+}
+ArrayResultByte SerializePlaintext(int plaintextID) {
+  ArrayResultByte r{nullptr, 0};
+  guard([&] {
+    const Plain& p = get_pt(plaintextID);
+    r = bytes_result(serialize_element(p.d.p, 1, p.level, p.scale, p.logslots));
+    return 0;
+  });
+  return r;
+}
+int LoadPlaintext(const unsigned char* data, unsigned long len) {
+  return guard([&] {
+    Scheme& s = sch();
+    int level, logslots;
+    double scale;
+    std::vector<u64> h = parse_element(data, (size_t)len, 1, level, scale, logslots);
+    auto p = std::make_unique<Plain>();
+    p->level = level; p->scale = scale; p->logslots = logslots;
+    p->d = DU64((size_t)(level + 1) * s.N);
+    upload(p->d.p, h.data(), h.size());
+    return push_pt(std::move(p));
   });
 }
 int RemovePlaintextDiagonals(int transformID) {

@@ -161,6 +161,15 @@ ArrayResultByte SerializeDiagonal(int transformID, int diagIdx);  /* lineartrans
 int LoadPlaintextDiagonal(const unsigned char* data, unsigned long len, int transformID,
                           unsigned long diagIdx);                 /* lineartransform.go:179-193 */
 int RemovePlaintextDiagonals(int transformID);                    /* lineartransform.go:195-201 */
+/* [ext] ciphertexts and plaintexts in the same wire layout (the field order of
+ * Lattigo v6 rlwe.Element: scale bits, log2 slots, flags, then the vector of
+ * ring.Poly in the NTT domain with standard representatives).  No counterpart
+ * in the reference, whose backends never serialize them; they complete the
+ * objects a Lattigo cross-check needs (inputs and expected outputs). */
+ArrayResultByte SerializeCiphertext(int ciphertextID);
+int LoadCiphertext(const unsigned char* data, unsigned long len);   /* returns a new ciphertext id */
+ArrayResultByte SerializePlaintext(int plaintextID);
+int LoadPlaintext(const unsigned char* data, unsigned long len);    /* returns a new plaintext id */
 
 /* ---- tensors -------------------------------------------------------------------- */
 int DeletePlaintext(int plaintextID);                       /* tensors.go:34-37 */
