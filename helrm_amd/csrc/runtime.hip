@@ -24,6 +24,7 @@
 #include <string>
 #include <thread>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "hipckks.h"
@@ -181,10 +182,15 @@ std::vector<int8_t> ternary_hw(u64 seed, u64 stream, int N, int h) {
 // only to later work on stream i, which runs after everything stream i was
 // given before (work of the other stream that touched the buffer must have
 // been joined first -- JoinStream -- before it is freed on stream i).
+// Every pointer handed out is in live_ until it comes back; put() of any
+// other pointer (a second free, or a buffer released with its scheme) is
+// refused instead of entering a free list, where it could be handed out twice.
 struct Pool {
   static constexpr int NSTREAMS = 2;
   std::multimap<size_t, void*> free_[NSTREAMS];
   std::unordered_map<void*, size_t> size_;
+  std::unordered_set<void*> live_;
+  std::unordered_set<void*> user_;  // handed out by DeviceAlloc (released by DeleteScheme)
   size_t live = 0, cached = 0, peak = 0;
   int cur = 0;  // the scheme's current stream
   int forbid = 0;  // > 0 inside an entry point that allocates nothing: get() is an error
@@ -194,17 +200,25 @@ struct Pool {
     if (bytes == 0) bytes = 256;
     auto& fl = free_[cur];
     auto it = fl.find(bytes);
-    if (it != fl.end()) { void* p = it->second; fl.erase(it); cached -= bytes; live += bytes; peak = std::max(peak, live); return p; }
+    if (it != fl.end()) {
+      void* p = it->second; fl.erase(it); cached -= bytes; live += bytes; peak = std::max(peak, live);
+      live_.insert(p);
+      return p;
+    }
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, bytes);
     if (e != hipSuccess) { (void)hipGetLastError(); trim(); HCHECK(hipMalloc(&p, bytes)); }
     size_[p] = bytes; live += bytes; peak = std::max(peak, live);
+    live_.insert(p);
     return p;
   }
-  void put(void* p) {
-    if (!p) return;
-    size_t b = size_.at(p);
+  // returns false (and changes nothing) for a pointer that is not live
+  bool put(void* p) {
+    if (!p) return true;
+    if (!live_.erase(p)) return false;
+    const size_t b = size_.at(p);
     free_[cur].emplace(b, p); live -= b; cached += b;
+    return true;
   }
   void trim() {
     (void)hipDeviceSynchronize();
@@ -218,7 +232,7 @@ struct Pool {
     (void)hipDeviceSynchronize();
     for (auto& kv : size_) (void)hipFree(kv.first);
     for (auto& fl : free_) fl.clear();
-    size_.clear(); live = cached = 0; cur = 0;
+    size_.clear(); live_.clear(); user_.clear(); live = cached = 0; cur = 0;
   }
 };
 Pool* g_pool = nullptr;
@@ -261,7 +275,7 @@ template <class T> struct DevArray {
   DevArray(DevArray&& o) noexcept : p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
   DevArray& operator=(DevArray&& o) noexcept { if (this != &o) { reset(); p = o.p; n = o.n; o.p = nullptr; o.n = 0; } return *this; }
   ~DevArray() { reset(); }
-  void reset() { if (p && g_pool) g_pool->put(p); p = nullptr; n = 0; }
+  void reset() { if (p && g_pool) (void)g_pool->put(p); p = nullptr; n = 0; }
   size_t bytes() const { return n * sizeof(T); }
 };
 using DU64 = DevArray<u64>;
@@ -2404,15 +2418,22 @@ void* DeviceAlloc(size_t bytes) {
   guard([&] {
     if (!g_pool) g_pool = new Pool();
     p = g_pool->get(bytes);
+    g_pool->user_.insert(p);
     return 0;
   });
   return p;
 }
+// A buffer from DeviceAlloc is released by DeviceFree or by DeleteScheme
+// (which releases all device memory): freeing it twice, or after the scheme
+// was deleted, is an error.
 int DeviceFree(void* ptr) {
   return guard([&] {
     REQUIRE(g_pool, "no device pool");
+    if (!ptr) return 0;
+    REQUIRE(g_pool->user_.count(ptr), "DeviceFree: not a live buffer from DeviceAlloc (freed twice, or released by DeleteScheme)");
     if (S) sync();
-    g_pool->put(ptr);
+    g_pool->user_.erase(ptr);
+    REQUIRE(g_pool->put(ptr), "DeviceFree: buffer is not live");
     return 0;
   });
 }

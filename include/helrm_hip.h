@@ -206,7 +206,7 @@ int GetSchemeInfo(int* out, int len);  /* logN, L, K, dnum, logScale, h */
 /* ---- [ext] device buffers from the library's allocator (for callers that have
  *      no HIP runtime of their own; one process should use one HIP runtime) ---- */
 void* DeviceAlloc(size_t bytes);                           /* NULL on failure */
-int DeviceFree(void* ptr);
+int DeviceFree(void* ptr);  /* -1 for a pointer freed twice or released by DeleteScheme */
 int CopyToDevice(void* dst, const void* src, size_t bytes);  /* synchronous */
 int CopyToHost(void* dst, const void* src, size_t bytes);    /* waits for the scheme stream first */
 

@@ -14,7 +14,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "_build", "libckks_oracle.so")
+# HELRM_ORACLE_LIB selects another build of the same source (the
+# sanitizer build of `make -C oracle asan`)
+_LIB_PATH = os.environ.get("HELRM_ORACLE_LIB") or os.path.join(_HERE, "_build", "libckks_oracle.so")
 
 u64p = ctypes.POINTER(ctypes.c_uint64)
 i64p = ctypes.POINTER(ctypes.c_int64)
