@@ -437,14 +437,22 @@ __device__ __forceinline__ int mac_pidx(const DiagMacArgs& a, int g, int b) {
 }
 // Diagonals are read exactly once per transform: non-temporal loads keep them
 // from displacing reused data in L2 (measured 5 % faster on the full MAC).
-template <int NB, bool DENSE>
-__device__ __forceinline__ void mac_load(const DiagMacArgs& a, const u64* dbase, int g, u64 (&d)[NB]) {
+// A later chunk of baby steps (ACC) also reads the group's accumulators
+// written by the earlier chunks, together with its diagonals.
+template <int NB, bool DENSE, bool ACC>
+__device__ __forceinline__ void mac_load(const DiagMacArgs& a, const u64* dbase, int g, u64 (&d)[NB], u64 (&t)[2],
+                                         const u64* Tb) {
 #pragma unroll
   for (int b = 0; b < NB; b++) d[b] = __builtin_nontemporal_load(&dbase[(size_t)mac_pidx<DENSE>(a, g, b) * a.diag_stride]);
+  if (ACC) {
+    const u64* T = Tb + (size_t)g * a.T_gstride;
+    t[0] = T[0];
+    t[1] = T[a.T_pstride];
+  }
 }
-template <int NB>
-__device__ __forceinline__ void mac_group(const DiagMacArgs& a, const u64 (&d)[NB], const u64 (&s0)[NB], const u64 (&s1)[NB],
-                                          const ModC& mc, u64* T) {
+template <int NB, bool ACC>
+__device__ __forceinline__ void mac_group(const DiagMacArgs& a, const u64 (&d)[NB], const u64 (&t)[2], const u64 (&s0)[NB],
+                                          const u64 (&s1)[NB], const ModC& mc, u64* T) {
   // exact column sums of 16 products; chunks of 16 are reduced to (lo, hi < q)
   u128 tot0 = 0, tot1 = 0;
 #pragma unroll
@@ -465,7 +473,7 @@ __device__ __forceinline__ void mac_group(const DiagMacArgs& a, const u64 (&d)[N
   // one chunk: hi < 4q was already folded below q
   u64 r0 = redc((u64)tot0, NB <= 16 ? (u64)(tot0 >> 64) : fold_hi4((u64)(tot0 >> 64), mc.q), mc.q, mc.qinv);
   u64 r1 = redc((u64)tot1, NB <= 16 ? (u64)(tot1 >> 64) : fold_hi4((u64)(tot1 >> 64), mc.q), mc.q, mc.qinv);
-  if (a.b0 > 0) { r0 = add_mod(r0, T[0], mc.q); r1 = add_mod(r1, T[a.T_pstride], mc.q); }
+  if (ACC) { r0 = add_mod(r0, t[0], mc.q); r1 = add_mod(r1, t[1], mc.q); }
   __builtin_nontemporal_store(r0, &T[0]);
   __builtin_nontemporal_store(r1, &T[a.T_pstride]);
 }
@@ -498,7 +506,7 @@ __device__ __forceinline__ void baby_rotation_at(const DiagMacArgs& a, int slot,
   r1 = redc(lo1, hi1, mc.q, mc.qinv);
 }
 
-template <int NB, bool DENSE>
+template <int NB, bool DENSE, bool ACC>
 __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
   const int x = blockIdx.x * blockDim.x + threadIdx.x;
   const int k = blockIdx.y;
@@ -520,26 +528,49 @@ __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
       }
     }
   }
-  // ping-pong: the next group's NB diagonals are in flight while a group is multiplied
-  u64 dA[NB], dB[NB];
+  // ping-pong: the next group's NB diagonals are in flight while a group is
+  // multiplied.  The prefetches inside the loop are unconditional (the last
+  // one or two groups are peeled off): a prefetch under a branch makes the
+  // compiler wait for every outstanding load, the prefetch included, before
+  // the current group's products.
+  u64 dA[NB], dB[NB], tA[2], tB[2];
   u64* Tb = a.T + (size_t)k * N + x;
-  mac_load<NB, DENSE>(a, dbase, a.g0, dA);
-  for (int g = a.g0; g < a.g1; g += 2) {
-    if (g + 1 < a.g1) mac_load<NB, DENSE>(a, dbase, g + 1, dB);
-    mac_group<NB>(a, dA, s0, s1, mc, Tb + (size_t)g * a.T_gstride);
-    if (g + 1 >= a.g1) break;
-    if (g + 2 < a.g1) mac_load<NB, DENSE>(a, dbase, g + 2, dA);
-    mac_group<NB>(a, dB, s0, s1, mc, Tb + (size_t)(g + 1) * a.T_gstride);
+  int g = a.g0;
+  mac_load<NB, DENSE, ACC>(a, dbase, g, dA, tA, Tb);
+  // (the scheduling barriers keep the machine scheduler from sinking the
+  // prefetch below the products to save registers)
+  for (; g + 2 < a.g1; g += 2) {
+    mac_load<NB, DENSE, ACC>(a, dbase, g + 1, dB, tB, Tb);
+    __builtin_amdgcn_sched_barrier(0);
+    mac_group<NB, ACC>(a, dA, tA, s0, s1, mc, Tb + (size_t)g * a.T_gstride);
+    mac_load<NB, DENSE, ACC>(a, dbase, g + 2, dA, tA, Tb);
+    __builtin_amdgcn_sched_barrier(0);
+    mac_group<NB, ACC>(a, dB, tB, s0, s1, mc, Tb + (size_t)(g + 1) * a.T_gstride);
+  }
+  if (g + 1 < a.g1) {
+    mac_load<NB, DENSE, ACC>(a, dbase, g + 1, dB, tB, Tb);
+    __builtin_amdgcn_sched_barrier(0);
+    mac_group<NB, ACC>(a, dA, tA, s0, s1, mc, Tb + (size_t)g * a.T_gstride);
+    mac_group<NB, ACC>(a, dB, tB, s0, s1, mc, Tb + (size_t)(g + 1) * a.T_gstride);
+  } else {
+    mac_group<NB, ACC>(a, dA, tA, s0, s1, mc, Tb + (size_t)g * a.T_gstride);
   }
 }
 void launch_diag_mac(const DiagMacArgs& a, hipStream_t st) {
   if (a.g1 <= a.g0) return;
   dim3 grid(a.N / 256, a.nqp, 1);
   const bool dense = a.dense && a.nb_chunk == 16 && a.b0 + 16 <= a.nbaby;
-  if (dense) hipLaunchKernelGGL((diag_mac_kernel<16, true>), grid, dim3(256), 0, st, a);
-  else if (a.nb_chunk <= 8) hipLaunchKernelGGL((diag_mac_kernel<8, false>), grid, dim3(256), 0, st, a);
-  else if (a.nb_chunk <= 16) hipLaunchKernelGGL((diag_mac_kernel<16, false>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((diag_mac_kernel<32, false>), grid, dim3(256), 0, st, a);
+  if (a.b0 == 0) {
+    if (dense) hipLaunchKernelGGL((diag_mac_kernel<16, true, false>), grid, dim3(256), 0, st, a);
+    else if (a.nb_chunk <= 8) hipLaunchKernelGGL((diag_mac_kernel<8, false, false>), grid, dim3(256), 0, st, a);
+    else if (a.nb_chunk <= 16) hipLaunchKernelGGL((diag_mac_kernel<16, false, false>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((diag_mac_kernel<32, false, false>), grid, dim3(256), 0, st, a);
+  } else {
+    // later chunks of a transform with more than 32 baby steps accumulate
+    if (a.nb_chunk <= 8) hipLaunchKernelGGL((diag_mac_kernel<8, false, true>), grid, dim3(256), 0, st, a);
+    else if (a.nb_chunk <= 16) hipLaunchKernelGGL((diag_mac_kernel<16, false, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((diag_mac_kernel<32, false, true>), grid, dim3(256), 0, st, a);
+  }
 }
 
 // RNS multiply-accumulate over a batch: out[r][x] = sum_p a[p][r][x] * b[p][r][x]
