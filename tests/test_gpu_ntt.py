@@ -70,3 +70,4 @@ def test_rns_multiply_accumulate(ntt_ctx):
             want = sum(int(x[pi, r, c]) * int(b[pi, r, c]) for pi in range(NPOLY)) % qq
             assert int(got[r, c]) == want, (r, c)
     assert (got < np.array(q, dtype=np.uint64)[:, None]).all()
+
