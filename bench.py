@@ -510,10 +510,23 @@ def main():
         nqp, dn = lf + 1 + K, (lf + 1 + K - 1) // K
         rb = (dn * 2 + dn + 2) * nqp * N * 8
         r_ms = kt["rotate"]["avg_ms"]
+        # the same key switch counted pass by pass (rows of N words moved, a
+        # transform = 2 passes each reading and writing its limb): inverse
+        # NTT of the ql input rows, extension to the E = dn*nqp - ql digit
+        # rows, their forward NTT, the key product, inverse NTT of the 2K
+        # P rows, extension of both parts to Q, forward NTT of the 2 ql rows
+        # whose last pass also reads x and c0
+        ql = lf + 1
+        ext_rows = dn * nqp - ql
+        pass_rows = (4 * ql + (ql + ext_rows) + 4 * ext_rows + (dn * 2 + dn + 2) * nqp
+                     + 4 * 2 * K + (2 * K + 2 * ql) + 2 * 2 * ql + (2 * ql + 2 * ql + ql + 2 * ql))
+        pb = pass_rows * N * 8
         kernel_rooflines["keyswitch_rotation"] = {
             "level": lf, "algorithmic_bytes_per_rotation": rb, "avg_ms": r_ms,
             "rotations_per_step": kt["rotate"]["launches"] / nprof,
-            "achieved_GBs": rb / (r_ms / 1000.0) / 1e9, "frac": rb / (r_ms / 1000.0) / 1e9 / HBM_PEAK_GBS}
+            "achieved_GBs": rb / (r_ms / 1000.0) / 1e9, "frac": rb / (r_ms / 1000.0) / 1e9 / HBM_PEAK_GBS,
+            "pass_bytes_per_rotation": pb, "pass_GBs": pb / (r_ms / 1000.0) / 1e9,
+            "pass_frac": pb / (r_ms / 1000.0) / 1e9 / HBM_PEAK_GBS}
 
     cpu = None
     if not args.no_cpu_baseline and cfg["kind"] == "dlrm":
