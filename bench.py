@@ -45,6 +45,24 @@ def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=
     return pcmm, diag_mac
 
 
+def keyswitch_pass_rows(level, K):
+    """Rows of N words that one single key switch at `level` moves, pass by
+    pass (a transform is 2 passes, each reading and writing its limb)."""
+    ql = level + 1
+    nqp = ql + K
+    dn = (nqp - 1) // K
+    ext = dn * nqp - ql  # extended digit rows: every QP row but each digit's own
+    return {
+        "inverse NTT of c1": 4 * ql,
+        "extension of the digits": ql + ext,
+        "forward NTT of the extended rows": 4 * ext,
+        "key product": (dn * 2 + dn + 2) * nqp,
+        "inverse NTT of the P rows, both parts": 4 * 2 * K,
+        "extension P -> Q, both parts": 2 * K + 2 * ql,
+        "forward NTT with the ModDown epilogue": 2 * 2 * ql + (2 * ql + 2 * ql + ql + 2 * ql),
+    }
+
+
 def read_traffic(kernel="diag_mac"):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary, if present."""
     path = os.path.join(ROOT, "profiles", f"{kernel}_pcmm26_traffic.json")
@@ -510,17 +528,7 @@ def main():
         nqp, dn = lf + 1 + K, (lf + 1 + K - 1) // K
         rb = (dn * 2 + dn + 2) * nqp * N * 8
         r_ms = kt["rotate"]["avg_ms"]
-        # the same key switch counted pass by pass (rows of N words moved, a
-        # transform = 2 passes each reading and writing its limb): inverse
-        # NTT of the ql input rows, extension to the E = dn*nqp - ql digit
-        # rows, their forward NTT, the key product, inverse NTT of the 2K
-        # P rows, extension of both parts to Q, forward NTT of the 2 ql rows
-        # whose last pass also reads x and c0
-        ql = lf + 1
-        ext_rows = dn * nqp - ql
-        pass_rows = (4 * ql + (ql + ext_rows) + 4 * ext_rows + (dn * 2 + dn + 2) * nqp
-                     + 4 * 2 * K + (2 * K + 2 * ql) + 2 * 2 * ql + (2 * ql + 2 * ql + ql + 2 * ql))
-        pb = pass_rows * N * 8
+        pb = sum(keyswitch_pass_rows(lf, K).values()) * N * 8
         kernel_rooflines["keyswitch_rotation"] = {
             "level": lf, "algorithmic_bytes_per_rotation": rb, "avg_ms": r_ms,
             "rotations_per_step": kt["rotate"]["launches"] / nprof,

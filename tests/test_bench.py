@@ -51,3 +51,16 @@ def test_keyswitch_bytes_without_rotations(lq, nb, ng):
     assert baby >= 0 and giant >= 0
     if nb == 1:
         assert baby == ((lq + 7) // 8) * (lq + 8) * (1 << 13) * 8 + lq * (1 << 13) * 8
+
+
+def test_keyswitch_pass_rows():
+    """One rotation at level 22 (23 Q limbs, K=8, 3 digits of 8, 8, 7 rows):
+    inverse NTT of 23 limbs (92 rows), extension 23 -> 70 rows (93), forward
+    NTT of 70 limbs (280), key product 11 x 31 rows (341), inverse NTT of 16 P
+    limbs (64), extension 16 -> 46 rows (62), forward NTT of 46 limbs whose
+    last pass also reads x and c0 (92 + 161): 1,185 rows = 621,281,280 B."""
+    rows = bench.keyswitch_pass_rows(22, 8)
+    assert list(rows.values()) == [92, 93, 280, 341, 64, 62, 253]
+    assert sum(rows.values()) * (1 << 16) * 8 == 621_281_280
+    # the key product alone is the per-rotation figure of the key-switch roofline
+    assert rows["key product"] * (1 << 16) * 8 == 178_782_208
