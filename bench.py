@@ -75,6 +75,19 @@ def read_traffic(kernel="diag_mac"):
         return None
 
 
+def measured_step_traffic(workload, ms):
+    """HBM bytes one PCMM actually moves (every dispatch, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary) and the rate they imply at
+    this run's step time; empty for other workloads or without the summary."""
+    path = os.path.join(ROOT, "profiles", "pcmm26_traffic.json")
+    if workload != "pcmm26" or not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        b = json.load(f)["bytes_per_pcmm"]
+    return {"measured_traffic_bytes": b, "measured_traffic_GBs": b / (ms / 1000.0) / 1e9,
+            "measured_traffic_frac": b / (ms / 1000.0) / 1e9 / HBM_PEAK_GBS}
+
+
 def cpu_baseline(q, p, h, key_seed, diagonals, selector, level, logscale, threads, per_step=26, fold=6, repeats=3,
                  single_thread=True):
     """The same PCMM on the CPU restatement (oracle/), whole: encode and
@@ -573,7 +586,8 @@ def main():
                                f"L={L} (60+50x{L - 1} bit), K={K} (61 bit), dnum={(L + K - 1) // K}, scale 2^{cfg['logscale']}"},
         "end_to_end_hbm": {"algorithmic_bytes": step_bytes,
                            "achieved_GBs": step_bytes / (ms / 1000.0) / 1e9,
-                           "frac": step_bytes / (ms / 1000.0) / 1e9 / HBM_PEAK_GBS},
+                           "frac": step_bytes / (ms / 1000.0) / 1e9 / HBM_PEAK_GBS,
+                           **measured_step_traffic(args.workload, ms)},
         "kernels": kt,
         "linear_transforms": lt_shapes,
         "selector_upload": upload,

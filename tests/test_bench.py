@@ -64,3 +64,11 @@ def test_keyswitch_pass_rows():
     assert sum(rows.values()) * (1 << 16) * 8 == 621_281_280
     # the key product alone is the per-rotation figure of the key-switch roofline
     assert rows["key product"] * (1 << 16) * 8 == 178_782_208
+
+
+def test_measured_step_traffic():
+    """The whole-PCMM traffic of the committed PMC summary, as a rate at a step time."""
+    r = bench.measured_step_traffic("pcmm26", 7.0)
+    assert r["measured_traffic_bytes"] > 30e9
+    assert abs(r["measured_traffic_GBs"] - r["measured_traffic_bytes"] / 7e-3 / 1e9) < 1e-6
+    assert bench.measured_step_traffic("dlrm", 7.0) == {}
