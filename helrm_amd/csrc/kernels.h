@@ -105,7 +105,6 @@ void launch_mont_mul(u64* out, size_t obstride, const u64* a, size_t abstride, c
 void launch_mont_convert(u64* data, size_t bstride, int batch, RowMap rm, const ModC* mods, int N, bool to, hipStream_t st);
 // out = in +- c[modulus] on the rows of rm (one polynomial)
 void launch_add_scalar(u64* out, const u64* in, RowMap rm, const u64* c, const ModC* mods, int N, bool sub, hipStream_t st);
-void launch_permute(u64* out, const u64* in, size_t bstride, int batch, int rows, const uint32_t* perm, int N, hipStream_t st);
 // Basis extension of the ns source rows of `in` into the target rows rm of `out`.
 // One source group of a batched basis extension (e.g. one digit of a
 // decomposition): its table (device copy), source rows, destination rows.

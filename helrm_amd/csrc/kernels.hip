@@ -89,16 +89,6 @@ void launch_mont_convert(u64* data, size_t bstride, int batch, RowMap rm, const 
   hipLaunchKernelGGL(mont_convert_kernel, dim3(N / 256, rm.nact(), batch), dim3(256), 0, st, data, bstride, rm, mods, N, to ? 1 : 0);
 }
 
-// out[row][i] = in[row][perm[i]]
-__global__ void permute_kernel(u64* __restrict__ out, const u64* __restrict__ in, size_t bstride, int rows, const uint32_t* __restrict__ perm, int N) {
-  int i = blockIdx.x * blockDim.x + threadIdx.x;
-  size_t o = (size_t)blockIdx.z * bstride + (size_t)blockIdx.y * N;
-  out[o + i] = in[o + perm[i]];
-}
-void launch_permute(u64* out, const u64* in, size_t bstride, int batch, int rows, const uint32_t* perm, int N, hipStream_t st) {
-  if (rows <= 0 || batch <= 0) return;
-  hipLaunchKernelGGL(permute_kernel, dim3(N / 256, rows, batch), dim3(256), 0, st, out, in, bstride, rows, perm, N);
-}
 
 // Strided batched copy: dst[b][0..words) = src[b][0..words), 16 bytes per lane.
 template <bool VEC>

@@ -383,7 +383,6 @@ void copy_rows(u64* dst, size_t dstride, const u64* src, size_t sstride, size_t 
 }
 
 RowMap rows_q(int l) { return RowMap{l + 1, l + 1, 0, 0, 0, 0}; }
-RowMap rows_qp(int l) { Scheme& s = sch(); return RowMap{l + 1 + s.K, l + 1, 0, s.L, 0, 0}; }
 RowMap rows_p() { Scheme& s = sch(); return RowMap{s.K, 0, 0, s.L, 0, 0}; }
 RowMap rows_all() { Scheme& s = sch(); return RowMap{s.L + s.K, s.L + s.K, 0, 0, 0, 0}; }
 inline int qp_mod(int l, int k) { Scheme& s = sch(); return k <= l ? k : s.L + (k - l - 1); }
