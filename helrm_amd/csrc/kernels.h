@@ -2,11 +2,24 @@
 #pragma once
 #include "hipckks.h"
 
+// Per-modulus constants of the float64 transform (moduli q <= FP_QMAX,
+// fpntt.h); the other moduli leave the entry unused.
+struct FpC {
+  double q, qinv;  // q and fl(1/q)
+  double cneg;     // 2^52 + q (canonical output of a negative residue)
+  double ni, niq;  // N^-1 centred, and fl(N^-1 / q)
+  double wn, wnq;  // the inverse transform's last twiddle times N^-1, centred, and fl(wn / q)
+  double pad;
+};
 struct NttTables {
   const ModC* mods;
-  const u64 *tw, *itw;     // [mod][N][2]: (psi^brv(k), Shoup companion) and the same for psi^-1
+  // [mod][N][2]: (psi^brv(k), Shoup companion) and the same for psi^-1; for
+  // a modulus q <= FP_QMAX the pair is (w, fl(w / q)) as float64 bits with
+  // w = psi^brv(k) centred in (-q/2, q/2]
+  const u64 *tw, *itw;
   const u64 *twr, *itwr;   // [mod][R][slots][P][2]: row-pass consecutive-round twiddles, lane-interleaved
   const u64 *ninv, *ninvp; // [mod]
+  const FpC* fpc;          // [mod]
 };
 // N = R x C, R = 2^SA, C = 2^SB (the transform's column / row split)
 void ntt_split(int logN, int* SA, int* SB);

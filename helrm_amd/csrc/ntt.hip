@@ -16,8 +16,17 @@
 // values in [0, 2q); each pass's output is reduced to [0, q) only where the
 // transform ends, so the result equals the textbook NTT word for word.
 // Twiddles are (w, floor(w 2^64 / q)) pairs read as one 16-byte load.
+//
+// Limbs whose modulus is at most FP_QMAX (the 40- and 50-bit primes) run the
+// same passes on float64 words instead: exact products by the float64
+// multiply-add (fpntt.h), so a butterfly costs 8 VALU instructions on the
+// full-rate FP64 pipe instead of ~19 integer ones.  Twiddles of such a
+// modulus are (w, fl(w / q)) float64 pairs, w centred; words between the two
+// passes are integer-valued doubles, and each transform still reads and
+// writes canonical u64 residues.
 #include <algorithm>
 
+#include "fpntt.h"
 #include "hipckks.h"
 #include "kernels.h"
 
@@ -106,6 +115,110 @@ __device__ __forceinline__ void ntt_round(u64 (&v)[16], const RoundTw<NST>& T, u
   ntt_round_f<FWD, NST>(v, [&](int, int, int sl) { return T.t[sl]; }, q);
 }
 
+// ---- float64 words (moduli q <= FP_QMAX; fpntt.h gives the bounds) ----
+__device__ __forceinline__ double f_val(u64 bits) { return __longlong_as_double((long long)bits); }
+__device__ __forceinline__ u64 f_bits(double x) { return (u64)__double_as_longlong(x); }
+// a canonical residue (< 2^52) as a double: its bits under the exponent of
+// 2^52, minus 2^52
+__device__ __forceinline__ double f_in(u64 x) { return f_val(x | 0x4330000000000000ull) - 4503599627370496.0; }
+// y * w - rint(y * wq) * q, exact (|t| <= q/2 + |y|/8)
+__device__ __forceinline__ double f_mm(double y, double w, double wq, double q) {
+  const double h = y * w;
+  const double l = __fma_rn(y, w, -h);
+  const double b = __builtin_rint(y * wq);
+  const double r = __fma_rn(-b, q, h);
+  return r + l;
+}
+// x - rint(x / q) * q, in [-q/2 - 2, q/2 + 2]
+__device__ __forceinline__ double f_red(double x, double q, double qinv) {
+  return __fma_rn(-__builtin_rint(x * qinv), q, x);
+}
+// the canonical residue of x as a u64: 2^52 + (x mod q) is below 2^53, so
+// its bits under the exponent of 2^52 are the residue
+__device__ __forceinline__ u64 f_canon(double x, const FpC& c) {
+  const double r = f_red(x, c.q, c.qinv);
+  const double s = r + (r < 0.0 ? c.cneg : 4503599627370496.0);
+  return f_bits(s) - 0x4330000000000000ull;
+}
+__device__ __forceinline__ double2 f_tw(const uint4& t) {
+  return make_double2(f_val(((u64)t.y << 32) | t.x), f_val(((u64)t.w << 32) | t.z));
+}
+// NST forward (Cooley-Tukey) stages on W registers: X' = X + t, Y' = X - t,
+// t = MM(Y); RED reduces the first stage's X inputs.
+template <int NST, int W, bool RED, class TWF>
+__device__ __forceinline__ void f_round_fwd(double (&v)[W], TWF tw_at, const FpC& c) {
+  int sl = 0;
+#pragma unroll
+  for (int s = 0; s < NST; s++) {
+    const int lrd = NST - 1 - s;
+    const int rd = 1 << lrd;
+    const int sh = lrd + 1;
+    double2 ts[W >> 1];
+#pragma unroll
+    for (int k = 0; k < (W >> sh); k++) ts[k] = f_tw(tw_at(s, k, sl + k));
+#pragma unroll
+    for (int k = 0; k < (W >> sh); k++, sl++) {
+#pragma unroll
+      for (int r = 0; r < rd; r++) {
+        const int i = (k << sh) + r;
+        double X = v[i];
+        if (RED && s == 0) X = f_red(X, c.q, c.qinv);
+        const double t = f_mm(v[i + rd], ts[k].x, ts[k].y, c.q);
+        v[i] = X + t;
+        v[i + rd] = X - t;
+      }
+    }
+  }
+}
+// Which sum outputs of an inverse round are reduced (fpb::gs_red), as a
+// table the unrolled loops index with constants.
+template <int NST, int W, long BIN>
+struct GsPlan {
+  bool red[4][16];
+  constexpr GsPlan() : red() {
+    for (int s = 0; s < NST; s++)
+      for (int i = 0; i < W; i++) red[s][i] = fpb::gs_red(NST, W, BIN, s, i);
+  }
+};
+// NST inverse (Gentleman-Sande) stages on W registers from the input bound
+// BIN: X' = X + Y (reduced where the plan says), Y' = MM(X - Y); NINV makes
+// the round's last stage X' = MM(X + Y, N^-1), Y' = MM(X - Y, w N^-1).
+template <int NST, int W, long BIN, bool NINV, class TWF>
+__device__ __forceinline__ void f_round_inv(double (&v)[W], TWF tw_at, const FpC& c) {
+  static_assert(fpb::gs_out(NST, W, BIN) >= 0, "float64 inverse round out of bounds");
+  constexpr GsPlan<NST, W, BIN> plan{};
+  int sl = 0;
+#pragma unroll
+  for (int s = 0; s < NST; s++) {
+    const int rd = 1 << s;
+    const int sh = s + 1;
+    const bool last = NINV && s == NST - 1;
+    double2 ts[W >> 1];
+    if (!last) {
+#pragma unroll
+      for (int k = 0; k < (W >> sh); k++) ts[k] = f_tw(tw_at(s, k, sl + k));
+    }
+#pragma unroll
+    for (int k = 0; k < (W >> sh); k++, sl++) {
+#pragma unroll
+      for (int r = 0; r < rd; r++) {
+        const int i = (k << sh) + r;
+        const double X = v[i], Y = v[i + rd];
+        if (last) {
+          v[i] = f_mm(X + Y, c.ni, c.niq, c.q);
+          v[i + rd] = f_mm(X - Y, c.wn, c.wnq, c.q);
+        } else {
+          const double d = X - Y;
+          double sum = X + Y;
+          if (plan.red[s][i]) sum = f_red(sum, c.q, c.qinv);
+          v[i] = sum;
+          v[i + rd] = f_mm(d, ts[k].x, ts[k].y, c.q);
+        }
+      }
+    }
+  }
+}
+
 // LDS column swizzle for the row pass: conflict-free both for the strided
 // (j + P*i) and the consecutive (16*j + i) access patterns.
 __device__ __forceinline__ int swz(int col) { return col ^ ((col >> 4) & 15); }
@@ -138,6 +251,7 @@ struct NttArgs {
   const uint4* twr;  // [mod][R][slots][P] lane-interleaved twiddles of the row pass's consecutive round
   const ModC* mods;
   const u64 *ninv, *ninvp;  // [mod]
+  const FpC* fpc;           // [mod] float64 constants (moduli q <= FP_QMAX)
   int logN, SA, SB, nsub;   // nsub: sub-transforms per workgroup
   int rows;                 // rm.nact()
   int batch;
@@ -164,15 +278,13 @@ __device__ __forceinline__ int64_t limb_src_off(const NttArgs& a, int y, const L
 
 // Column pass (pass A): workgroup = nsub columns x R rows.
 template <bool FWD, int S>
-__global__ __launch_bounds__(NTT_TPB) void ntt_col_kernel(NttArgs a) {
+__device__ __forceinline__ void ntt_col_int(const NttArgs& a, u64* sm, const LimbRef& lr) {
   // forward: first pass (reads a.src); inverse: second pass (in place)
-  __shared__ u64 sm[4096];
   constexpr int P = 1 << (S - 4);
   const int nsub = a.nsub;
   const int tid = threadIdx.x;
   const int c = tid & (nsub - 1);
   const int j = tid / nsub;  // in [0, P)
-  const LimbRef lr = limb_ref(a, blockIdx.y);
   const int m = lr.mod;
   const u64 q = a.mods[m].q;
   const u64 Nn = 1ull << a.logN;
@@ -221,17 +333,130 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_col_kernel(NttArgs a) {
     for (int i = 0; i < 16; i++) poly[(size_t)(j + P * i) * C] = csub(shoup_lazy(v[i], ni, nip, 0 - q), q);
   }
 }
+// The same pass with float64 words (q <= FP_QMAX): canonical words in,
+// doubles bounded by the mid-transform bound out (forward), or doubles in and
+// canonical words out with N^-1 folded into the last stage (inverse).
+template <bool FWD, int S>
+__device__ __forceinline__ void ntt_col_fp(const NttArgs& a, u64* sm, const LimbRef& lr) {
+  constexpr int P = 1 << (S - 4);
+  const int nsub = a.nsub;
+  const int tid = threadIdx.x;
+  const int c = tid & (nsub - 1);
+  const int j = tid / nsub;
+  const int m = lr.mod;
+  const FpC fc = a.fpc[m];
+  const u64 Nn = 1ull << a.logN;
+  const int SB = a.SB;
+  const size_t C = (size_t)1 << SB;
+  const int col = blockIdx.x * nsub + c;
+  u64* poly = a.data + lr.off + col;
+  const uint4* tw = a.tw + (size_t)m * Nn;
+  double v[16];
+  if (FWD) {
+    static_assert(fpb::ct_pass_ok(false, S, true), "float64 forward column pass out of bounds");
+    constexpr bool R1 = fpb::ct_pass(false, S, true, 0, true), R2 = fpb::ct_pass(false, S, true, 1, true);
+    const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + col;
+    RoundTw<4> T1;
+    round_tw_load<true, 4>(T1, 0, S - 4 + SB, Nn, tw);
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = f_in(in[(size_t)(j + P * i) * C]);
+    f_round_fwd<4, 16, R1>(v, [&](int, int, int sl) { return T1.t[sl]; }, fc);
+    RoundTw<S - 4> T2;
+    round_tw_load<true, S - 4>(T2, (u64)(16 * j) << SB, SB, Nn, tw);
+#pragma unroll
+    for (int i = 0; i < 16; i++) sm[(j + P * i) * nsub + c] = f_bits(v[i]);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = f_val(sm[(16 * j + i) * nsub + c]);
+    f_round_fwd<S - 4, 16, R2>(v, [&](int, int, int sl) { return T2.t[sl]; }, fc);
+#pragma unroll
+    for (int i = 0; i < 16; i++) poly[(size_t)(16 * j + i) * C] = f_bits(v[i]);
+  } else {
+    static_assert(fpb::gs_pass_ok(false, S, false), "float64 inverse column pass out of bounds");
+    constexpr long B0 = fpb::gs_pass(false, S, false, 0), B1 = fpb::gs_pass(false, S, false, 1);
+    RoundTw<S - 4> T1;
+    round_tw_load<false, S - 4>(T1, (u64)(16 * j) << SB, SB, Nn, tw);
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = f_val(poly[(size_t)(16 * j + i) * C]);
+    f_round_inv<S - 4, 16, B0, false>(v, [&](int, int, int sl) { return T1.t[sl]; }, fc);
+    RoundTw<4> T2;
+    round_tw_load<false, 4>(T2, 0, S - 4 + SB, Nn, tw);
+#pragma unroll
+    for (int i = 0; i < 16; i++) sm[(16 * j + i) * nsub + c] = f_bits(v[i]);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = f_val(sm[(j + P * i) * nsub + c]);
+    f_round_inv<4, 16, B1, true>(v, [&](int, int, int sl) { return T2.t[sl]; }, fc);
+#pragma unroll
+    for (int i = 0; i < 16; i++) poly[(size_t)(j + P * i) * C] = f_canon(v[i], fc);
+  }
+}
+template <bool FWD, int S>
+__global__ __launch_bounds__(NTT_TPB) void ntt_col_kernel(NttArgs a) {
+  __shared__ u64 sm[4096];
+  const LimbRef lr = limb_ref(a, blockIdx.y);
+  // one modulus per workgroup: the branch is uniform
+  if (a.mods[lr.mod].q <= FP_QMAX) ntt_col_fp<FWD, S>(a, sm, lr);
+  else ntt_col_int<FWD, S>(a, sm, lr);
+}
+
+// Last part of the forward row pass: the canonical transform of one row is in
+// srow (consecutive positions, swizzled); store it, or apply the ModDown
+// epilogue to it.
+template <int S, bool EPI>
+__device__ __forceinline__ void row_fwd_tail(const NttArgs& a, const u64* srow, const LimbRef& lr, int r, int j, u64* poly) {
+  constexpr int P = 1 << (S - 4);
+  constexpr int C = 1 << S;
+  const int m = lr.mod;
+  const u64 q = a.mods[m].q;
+  if (EPI) {
+    // ModDown epilogue: limb (batch b, Q row) of the extension
+    const int b = lr.pad, row = (int)((lr.off - (int64_t)b * (int64_t)a.bstride) >> a.logN);
+    const size_t rowoff = ((size_t)row << a.logN) + (size_t)r * C;
+    const u64* xr = a.e.x + (size_t)b * a.e.x_bstride + rowoff;
+    const u64* ar = (a.e.add && b < a.e.add_batches) ? a.e.add + (size_t)b * a.e.a_bstride + rowoff : nullptr;
+    u64* orow = a.e.out + (size_t)b * a.e.o_bstride + ((size_t)row << a.logN);
+    const u64 pi = a.e.pinv[m], pip = a.e.pinvp[m];
+    // every load of the epilogue is issued before the first use, so the
+    // latencies overlap instead of adding up word by word
+    u64 xv[16], av[16];
+    uint32_t dst[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) xv[i] = __builtin_nontemporal_load(&xr[j + P * i]);
+    if (ar) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) av[i] = __builtin_nontemporal_load(&ar[j + P * i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; i++) av[i] = 0;
+    }
+    if (a.e.perm_inv) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) dst[i] = a.e.perm_inv[r * C + j + P * i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; i++) dst[i] = (uint32_t)(r * C + j + P * i);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int pos = j + P * i;
+      const u64 o = shoup_mul(sub_mod(xv[i], srow[swz(pos)], q), pi, pip, q);
+      __builtin_nontemporal_store(add_mod(o, av[i], q), &orow[dst[i]]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; i++) __builtin_nontemporal_store(srow[swz(j + P * i)], &poly[j + P * i]);
+  }
+}
 
 // Row pass (pass B): workgroup = nsub rows x C columns.
-template <bool FWD, int S, bool EPI = false>
-__global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
-  __shared__ u64 sm[4096];
+template <bool FWD, int S, bool EPI>
+__device__ __forceinline__ void ntt_row_int(const NttArgs& a, u64* sm, const LimbRef& lr) {
   constexpr int P = 1 << (S - 4);
   constexpr int C = 1 << S;
   const int tid = threadIdx.x;
   const int j = tid & (P - 1);
   const int rho = tid >> (S - 4);
-  const LimbRef lr = limb_ref(a, blockIdx.y);
   const int m = lr.mod;
   const u64 q = a.mods[m].q;
   const u64 Nn = 1ull << a.logN;
@@ -264,44 +489,7 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = csub(csub(csub(v[i], q2 + q2), q2), q);
     __syncthreads();
-    if (EPI) {
-      // ModDown epilogue: limb (batch b, Q row) of the extension
-      const int b = lr.pad, row = (int)((lr.off - (int64_t)b * (int64_t)a.bstride) >> a.logN);
-      const size_t rowoff = ((size_t)row << a.logN) + (size_t)r * C;
-      const u64* xr = a.e.x + (size_t)b * a.e.x_bstride + rowoff;
-      const u64* ar = (a.e.add && b < a.e.add_batches) ? a.e.add + (size_t)b * a.e.a_bstride + rowoff : nullptr;
-      u64* orow = a.e.out + (size_t)b * a.e.o_bstride + ((size_t)row << a.logN);
-      const u64 pi = a.e.pinv[m], pip = a.e.pinvp[m];
-      // every load of the epilogue is issued before the first use, so the
-      // latencies overlap instead of adding up word by word
-      u64 xv[16], av[16];
-      uint32_t dst[16];
-#pragma unroll
-      for (int i = 0; i < 16; i++) xv[i] = __builtin_nontemporal_load(&xr[j + P * i]);
-      if (ar) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) av[i] = __builtin_nontemporal_load(&ar[j + P * i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; i++) av[i] = 0;
-      }
-      if (a.e.perm_inv) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) dst[i] = a.e.perm_inv[r * C + j + P * i];
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; i++) dst[i] = (uint32_t)(r * C + j + P * i);
-      }
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const int pos = j + P * i;
-        const u64 o = shoup_mul(sub_mod(xv[i], srow[swz(pos)], q), pi, pip, q);
-        __builtin_nontemporal_store(add_mod(o, av[i], q), &orow[dst[i]]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; i++) __builtin_nontemporal_store(srow[swz(j + P * i)], &poly[j + P * i]);
-    }
+    row_fwd_tail<S, EPI>(a, srow, lr, r, j, poly);
   } else {
     const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + (size_t)r * C;
     // all 16 loads in flight before the LDS writes; the first round's
@@ -327,6 +515,78 @@ __global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) __builtin_nontemporal_store(v[i], &poly[j + P * i]);
   }
+}
+template <bool FWD, int S, bool EPI>
+__device__ __forceinline__ void ntt_row_fp(const NttArgs& a, u64* sm, const LimbRef& lr) {
+  constexpr int P = 1 << (S - 4);
+  constexpr int C = 1 << S;
+  const int tid = threadIdx.x;
+  const int j = tid & (P - 1);
+  const int rho = tid >> (S - 4);
+  const int m = lr.mod;
+  const FpC fc = a.fpc[m];
+  const u64 Nn = 1ull << a.logN;
+  const int r = blockIdx.x * a.nsub + rho;
+  u64* poly = a.data + lr.off + (size_t)r * C;
+  u64* srow = sm + rho * C;
+  const uint4* tw = a.tw + (size_t)m * Nn;
+  constexpr int NSL = ntt_round_slots(S - 4);
+  const uint4* twr = a.twr + (((size_t)m * (Nn >> S) + r) * NSL) * P + j;
+  const u64 A = (u64)r * C;
+  double v[16];
+  if (FWD) {
+    static_assert(fpb::ct_pass_ok(false, S, false), "float64 forward row pass out of bounds");
+    constexpr bool R1 = fpb::ct_pass(false, S, false, 0, true), R2 = fpb::ct_pass(false, S, false, 1, true);
+    RoundTw<4> T1;
+    round_tw_load<true, 4>(T1, A, S - 4, Nn, tw);
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = f_val(__builtin_nontemporal_load(&poly[j + P * i]));
+    f_round_fwd<4, 16, R1>(v, [&](int, int, int sl) { return T1.t[sl]; }, fc);
+#pragma unroll
+    for (int i = 0; i < 16; i++) srow[swz(j + P * i)] = f_bits(v[i]);
+    __syncthreads();
+    RoundTw<S - 4> T2;
+    round_tw_load_tab<S - 4>(T2, twr, P);
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = f_val(srow[swz(16 * j + i)]);
+    f_round_fwd<S - 4, 16, R2>(v, [&](int, int, int sl) { return T2.t[sl]; }, fc);
+#pragma unroll
+    for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = f_canon(v[i], fc);
+    __syncthreads();
+    row_fwd_tail<S, EPI>(a, srow, lr, r, j, poly);
+  } else {
+    static_assert(fpb::gs_pass_ok(false, S, true), "float64 inverse row pass out of bounds");
+    constexpr long B0 = fpb::gs_pass(false, S, true, 0), B1 = fpb::gs_pass(false, S, true, 1);
+    const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + (size_t)r * C;
+    u64 w[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) w[i] = __builtin_nontemporal_load(&in[j + P * i]);
+#pragma unroll
+    for (int i = 0; i < 16; i++) srow[swz(j + P * i)] = w[i];
+    RoundTw<S - 4> T1;
+    round_tw_load_tab<S - 4>(T1, twr, P);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = f_in(srow[swz(16 * j + i)]);
+    f_round_inv<S - 4, 16, B0, false>(v, [&](int, int, int sl) { return T1.t[sl]; }, fc);
+    RoundTw<4> T2;
+    round_tw_load<false, 4>(T2, A, S - 4, Nn, tw);
+#pragma unroll
+    for (int i = 0; i < 16; i++) srow[swz(16 * j + i)] = f_bits(v[i]);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = f_val(srow[swz(j + P * i)]);
+    f_round_inv<4, 16, B1, false>(v, [&](int, int, int sl) { return T2.t[sl]; }, fc);
+#pragma unroll
+    for (int i = 0; i < 16; i++) __builtin_nontemporal_store(f_bits(v[i]), &poly[j + P * i]);
+  }
+}
+template <bool FWD, int S, bool EPI = false>
+__global__ __launch_bounds__(NTT_TPB) void ntt_row_kernel(NttArgs a) {
+  __shared__ u64 sm[4096];
+  const LimbRef lr = limb_ref(a, blockIdx.y);
+  if (a.mods[lr.mod].q <= FP_QMAX) ntt_row_fp<FWD, S, EPI>(a, sm, lr);
+  else ntt_row_int<FWD, S, EPI>(a, sm, lr);
 }
 
 // ---------------------------------------------------------------------------
@@ -366,18 +626,39 @@ __device__ __forceinline__ void w8_round(u64 (&v)[8], int t, u64 base, int lstri
     }, q);
   }
 }
+// The same round on float64 words.  Forward: FIRST selects the pass (the
+// first reads canonical words); inverse: NINV folds N^-1 into the round's
+// last stage (the transform's last).  The round's place in its pass (r, in
+// execution order) fixes its bound schedule.
+template <bool FWD, int S, int K, bool FIRST, bool NINV = false>
+__device__ __forceinline__ void w8_round_fp(double (&v)[8], int t, u64 base, int lstride, u64 Nn,
+                                            const uint4* __restrict__ tw, const FpC& fc) {
+  constexpr int ls = w8_ls(S, K), width = w8_width(S, K);
+  constexpr int r = FWD ? K : fpb::w8_nr(S) - 1 - K;
+  if constexpr (width > 0) {
+    const u64 A = base + ((u64)((t >> ls) << (ls + 3)) << lstride);
+    const int LS = ls + lstride;
+    auto tw_at = [&](int st, int k, int) {
+      const int sh = (FWD ? width - 1 - st : st) + 1;
+      return tw[((Nn + A) >> (LS + sh)) + k];
+    };
+    if constexpr (FWD) {
+      f_round_fwd<width, 8, fpb::ct_pass(true, S, FIRST, r, true) != 0>(v, tw_at, fc);
+    } else {
+      f_round_inv<width, 8, fpb::gs_pass(true, S, FIRST, r), NINV>(v, tw_at, fc);
+    }
+  }
+}
 
 // Column pass, 8 words per thread: workgroup = nsub columns x R rows, T
 // threads per column (512 threads for 16 columns).
 template <bool FWD, int S>
-__global__ __launch_bounds__(512) void ntt_col8_kernel(NttArgs a) {
-  __shared__ u64 sm[4096];
-  constexpr int T = 1 << (S - 3), NR = (S + 2) / 3;
+__device__ __forceinline__ void ntt_col8_int(const NttArgs& a, u64* sm, const LimbRef& lr) {
+  constexpr int NR = (S + 2) / 3;
   const int nsub = a.nsub;
   const int tid = threadIdx.x;
   const int c = tid & (nsub - 1);
   const int t = tid / nsub;  // in [0, T)
-  const LimbRef lr = limb_ref(a, blockIdx.y);
   const int m = lr.mod;
   const u64 q = a.mods[m].q;
   const u64 Nn = 1ull << a.logN;
@@ -387,7 +668,6 @@ __global__ __launch_bounds__(512) void ntt_col8_kernel(NttArgs a) {
   u64* poly = a.data + lr.off + col;
   const uint4* tw = a.tw + (size_t)m * Nn;
   u64 v[8];
-  (void)T;
   if (FWD) {
     const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + col;
 #pragma unroll
@@ -430,19 +710,131 @@ __global__ __launch_bounds__(512) void ntt_col8_kernel(NttArgs a) {
     for (int i = 0; i < 8; i++) poly[(size_t)w8_elem(w8_ls(S, 0), t, i) * C] = csub(shoup_lazy(v[i], ni, nip, 0 - q), q);
   }
 }
+template <bool FWD, int S>
+__device__ __forceinline__ void ntt_col8_fp(const NttArgs& a, u64* sm, const LimbRef& lr) {
+  constexpr int NR = (S + 2) / 3;
+  static_assert(FWD ? fpb::ct_pass_ok(true, S, true) : fpb::gs_pass_ok(true, S, false),
+                "float64 8-word column pass out of bounds");
+  const int nsub = a.nsub;
+  const int tid = threadIdx.x;
+  const int c = tid & (nsub - 1);
+  const int t = tid / nsub;
+  const int m = lr.mod;
+  const FpC fc = a.fpc[m];
+  const u64 Nn = 1ull << a.logN;
+  const int SB = a.SB;
+  const size_t C = (size_t)1 << SB;
+  const int col = blockIdx.x * nsub + c;
+  u64* poly = a.data + lr.off + col;
+  const uint4* tw = a.tw + (size_t)m * Nn;
+  double v[8];
+  if (FWD) {
+    const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + col;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = f_in(in[(size_t)w8_elem(w8_ls(S, 0), t, i) * C]);
+    w8_round_fp<true, S, 0, true>(v, t, 0, SB, Nn, tw, fc);
+#pragma unroll
+    for (int k = 1; k < NR; k++) {
+      const int lp = w8_ls(S, k - 1), lc = w8_ls(S, k);
+      if (k > 1) __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 8; i++) sm[w8_elem(lp, t, i) * nsub + c] = f_bits(v[i]);
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = f_val(sm[w8_elem(lc, t, i) * nsub + c]);
+      if (k == 1) w8_round_fp<true, S, 1, true>(v, t, 0, SB, Nn, tw, fc);
+      if (k == 2) w8_round_fp<true, S, 2, true>(v, t, 0, SB, Nn, tw, fc);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) poly[(size_t)w8_elem(w8_ls(S, NR - 1), t, i) * C] = f_bits(v[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = f_val(poly[(size_t)w8_elem(w8_ls(S, NR - 1), t, i) * C]);
+#pragma unroll
+    for (int k = NR - 1; k >= 0; k--) {
+      if (k < NR - 1) {
+        const int lp = w8_ls(S, k + 1), lc = w8_ls(S, k);
+        if (k < NR - 2) __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; i++) sm[w8_elem(lp, t, i) * nsub + c] = f_bits(v[i]);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = f_val(sm[w8_elem(lc, t, i) * nsub + c]);
+      }
+      if (k == 2) w8_round_fp<false, S, 2, false>(v, t, 0, SB, Nn, tw, fc);
+      if (k == 1) w8_round_fp<false, S, 1, false>(v, t, 0, SB, Nn, tw, fc);
+      if (k == 0) w8_round_fp<false, S, 0, false, true>(v, t, 0, SB, Nn, tw, fc);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) poly[(size_t)w8_elem(w8_ls(S, 0), t, i) * C] = f_canon(v[i], fc);
+  }
+}
+template <bool FWD, int S>
+__global__ __launch_bounds__(512) void ntt_col8_kernel(NttArgs a) {
+  __shared__ u64 sm[4096];
+  const LimbRef lr = limb_ref(a, blockIdx.y);
+  if (a.mods[lr.mod].q <= FP_QMAX) ntt_col8_fp<FWD, S>(a, sm, lr);
+  else ntt_col8_int<FWD, S>(a, sm, lr);
+}
+
+// Last part of the 8-word forward row pass: the canonical row is in srow
+// (swizzled by w8_swz); store it, or apply the ModDown epilogue to it.
+template <int S, bool EPI>
+__device__ __forceinline__ void row8_fwd_tail(const NttArgs& a, const u64* srow, const LimbRef& lr, int r, int t, u64* poly) {
+  constexpr int C = 1 << S;
+  constexpr int L0 = w8_ls(S, 0);
+  const int m = lr.mod;
+  const u64 q = a.mods[m].q;
+  if (EPI) {
+    const int b = lr.pad, row = (int)((lr.off - (int64_t)b * (int64_t)a.bstride) >> a.logN);
+    const size_t rowoff = ((size_t)row << a.logN) + (size_t)r * C;
+    const u64* xr = a.e.x + (size_t)b * a.e.x_bstride + rowoff;
+    const u64* ar = (a.e.add && b < a.e.add_batches) ? a.e.add + (size_t)b * a.e.a_bstride + rowoff : nullptr;
+    u64* orow = a.e.out + (size_t)b * a.e.o_bstride + ((size_t)row << a.logN);
+    const u64 pi = a.e.pinv[m], pip = a.e.pinvp[m];
+    u64 xv[8], av[8];
+    uint32_t dst[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) xv[i] = __builtin_nontemporal_load(&xr[w8_elem(L0, t, i)]);
+    if (ar) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) av[i] = __builtin_nontemporal_load(&ar[w8_elem(L0, t, i)]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) av[i] = 0;
+    }
+    if (a.e.perm_inv) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) dst[i] = a.e.perm_inv[r * C + w8_elem(L0, t, i)];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) dst[i] = (uint32_t)(r * C + w8_elem(L0, t, i));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int pos = w8_elem(L0, t, i);
+      const u64 o = shoup_mul(sub_mod(xv[i], srow[w8_swz(pos)], q), pi, pip, q);
+      __builtin_nontemporal_store(add_mod(o, av[i], q), &orow[dst[i]]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int pos = w8_elem(L0, t, i);
+      __builtin_nontemporal_store(srow[w8_swz(pos)], &poly[pos]);
+    }
+  }
+}
 
 // Row pass, 8 words per thread: workgroup = nsub rows x C columns, T threads
 // per row.  Global memory is read and written in the round-0 element order
 // (consecutive lanes, consecutive words); the other rounds go through LDS.
-template <bool FWD, int S, bool EPI = false>
-__global__ __launch_bounds__(256) void ntt_row8_kernel(NttArgs a) {
-  __shared__ u64 sm[2048];
+template <bool FWD, int S, bool EPI>
+__device__ __forceinline__ void ntt_row8_int(const NttArgs& a, u64* sm, const LimbRef& lr) {
   constexpr int T = 1 << (S - 3), C = 1 << S, NR = (S + 2) / 3;
   constexpr int L0 = w8_ls(S, 0), LL = w8_ls(S, NR - 1);
   const int tid = threadIdx.x;
   const int t = tid & (T - 1);
   const int rho = tid >> (S - 3);
-  const LimbRef lr = limb_ref(a, blockIdx.y);
   const int m = lr.mod;
   const u64 q = a.mods[m].q;
   const u64 Nn = 1ull << a.logN;
@@ -474,44 +866,7 @@ __global__ __launch_bounds__(256) void ntt_row8_kernel(NttArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; i++) srow[w8_swz(w8_elem(LL, t, i))] = csub(csub(csub(v[i], q2 + q2), q2), q);
     __syncthreads();
-    if (EPI) {
-      const int b = lr.pad, row = (int)((lr.off - (int64_t)b * (int64_t)a.bstride) >> a.logN);
-      const size_t rowoff = ((size_t)row << a.logN) + (size_t)r * C;
-      const u64* xr = a.e.x + (size_t)b * a.e.x_bstride + rowoff;
-      const u64* ar = (a.e.add && b < a.e.add_batches) ? a.e.add + (size_t)b * a.e.a_bstride + rowoff : nullptr;
-      u64* orow = a.e.out + (size_t)b * a.e.o_bstride + ((size_t)row << a.logN);
-      const u64 pi = a.e.pinv[m], pip = a.e.pinvp[m];
-      u64 xv[8], av[8];
-      uint32_t dst[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) xv[i] = __builtin_nontemporal_load(&xr[w8_elem(L0, t, i)]);
-      if (ar) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) av[i] = __builtin_nontemporal_load(&ar[w8_elem(L0, t, i)]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; i++) av[i] = 0;
-      }
-      if (a.e.perm_inv) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) dst[i] = a.e.perm_inv[r * C + w8_elem(L0, t, i)];
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; i++) dst[i] = (uint32_t)(r * C + w8_elem(L0, t, i));
-      }
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const int pos = w8_elem(L0, t, i);
-        const u64 o = shoup_mul(sub_mod(xv[i], srow[w8_swz(pos)], q), pi, pip, q);
-        __builtin_nontemporal_store(add_mod(o, av[i], q), &orow[dst[i]]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const int pos = w8_elem(L0, t, i);
-        __builtin_nontemporal_store(srow[w8_swz(pos)], &poly[pos]);
-      }
-    }
+    row8_fwd_tail<S, EPI>(a, srow, lr, r, t, poly);
   } else {
     const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + (size_t)r * C;
 #pragma unroll
@@ -540,6 +895,81 @@ __global__ __launch_bounds__(256) void ntt_row8_kernel(NttArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; i++) __builtin_nontemporal_store(v[i], &poly[w8_elem(L0, t, i)]);
   }
+}
+template <bool FWD, int S, bool EPI>
+__device__ __forceinline__ void ntt_row8_fp(const NttArgs& a, u64* sm, const LimbRef& lr) {
+  constexpr int T = 1 << (S - 3), C = 1 << S, NR = (S + 2) / 3;
+  constexpr int L0 = w8_ls(S, 0), LL = w8_ls(S, NR - 1);
+  static_assert(FWD ? fpb::ct_pass_ok(true, S, false) : fpb::gs_pass_ok(true, S, true),
+                "float64 8-word row pass out of bounds");
+  const int tid = threadIdx.x;
+  const int t = tid & (T - 1);
+  const int rho = tid >> (S - 3);
+  const int m = lr.mod;
+  const FpC fc = a.fpc[m];
+  const u64 Nn = 1ull << a.logN;
+  const int r = blockIdx.x * a.nsub + rho;
+  u64* poly = a.data + lr.off + (size_t)r * C;
+  u64* srow = sm + rho * C;
+  const uint4* tw = a.tw + (size_t)m * Nn;
+  const u64 A = (u64)r * C;
+  double v[8];
+  if (FWD) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = f_val(__builtin_nontemporal_load(&poly[w8_elem(L0, t, i)]));
+    w8_round_fp<true, S, 0, false>(v, t, A, 0, Nn, tw, fc);
+#pragma unroll
+    for (int k = 1; k < NR; k++) {
+      const int lp = w8_ls(S, k - 1), lc = w8_ls(S, k);
+      if (k > 1) __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 8; i++) srow[w8_swz(w8_elem(lp, t, i))] = f_bits(v[i]);
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = f_val(srow[w8_swz(w8_elem(lc, t, i))]);
+      if (k == 1) w8_round_fp<true, S, 1, false>(v, t, A, 0, Nn, tw, fc);
+      if (k == 2) w8_round_fp<true, S, 2, false>(v, t, A, 0, Nn, tw, fc);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; i++) srow[w8_swz(w8_elem(LL, t, i))] = f_canon(v[i], fc);
+    __syncthreads();
+    row8_fwd_tail<S, EPI>(a, srow, lr, r, t, poly);
+  } else {
+    const u64* in = a.src + limb_src_off(a, blockIdx.y, lr) + (size_t)r * C;
+    u64 w[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i] = __builtin_nontemporal_load(&in[w8_elem(L0, t, i)]);
+#pragma unroll
+    for (int i = 0; i < 8; i++) srow[w8_swz(w8_elem(L0, t, i))] = w[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = f_in(srow[w8_swz(w8_elem(LL, t, i))]);
+#pragma unroll
+    for (int k = NR - 1; k >= 0; k--) {
+      if (k < NR - 1) {
+        const int lp = w8_ls(S, k + 1), lc = w8_ls(S, k);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; i++) srow[w8_swz(w8_elem(lp, t, i))] = f_bits(v[i]);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = f_val(srow[w8_swz(w8_elem(lc, t, i))]);
+      }
+      if (k == 2) w8_round_fp<false, S, 2, true>(v, t, A, 0, Nn, tw, fc);
+      if (k == 1) w8_round_fp<false, S, 1, true>(v, t, A, 0, Nn, tw, fc);
+      if (k == 0) w8_round_fp<false, S, 0, true>(v, t, A, 0, Nn, tw, fc);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) __builtin_nontemporal_store(f_bits(v[i]), &poly[w8_elem(L0, t, i)]);
+  }
+}
+template <bool FWD, int S, bool EPI = false>
+__global__ __launch_bounds__(256) void ntt_row8_kernel(NttArgs a) {
+  __shared__ u64 sm[2048];
+  const LimbRef lr = limb_ref(a, blockIdx.y);
+  if (a.mods[lr.mod].q <= FP_QMAX) ntt_row8_fp<FWD, S, EPI>(a, sm, lr);
+  else ntt_row8_int<FWD, S, EPI>(a, sm, lr);
 }
 
 template <bool FWD>
@@ -665,7 +1095,7 @@ void launch_ntt(const u64* src, size_t sstride, u64* data, size_t bstride, int b
   a.list = nullptr;
   a.src = src; a.sstride = sstride; a.data = data; a.bstride = bstride; a.rm = rm; a.rows = rows; a.batch = batch;
   a.mods = tw.mods;
-  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN;
+  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.fpc = tw.fpc; a.logN = logN;
   a.tw = reinterpret_cast<const uint4*>(forward ? tw.tw : tw.itw);
   a.twr = reinterpret_cast<const uint4*>(forward ? tw.twr : tw.itwr);
   ntt_launch(a, rows * batch, forward, st);
@@ -679,7 +1109,7 @@ void launch_ntt_moddown(u64* ext, size_t ext_bstride, int batch, int l, int logN
   a.list = nullptr;
   a.src = ext; a.sstride = ext_bstride; a.data = ext; a.bstride = ext_bstride; a.rm = rm; a.rows = l + 1; a.batch = batch;
   a.mods = tw.mods;
-  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN;
+  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.fpc = tw.fpc; a.logN = logN;
   a.tw = reinterpret_cast<const uint4*>(tw.tw);
   a.twr = reinterpret_cast<const uint4*>(tw.twr);
   a.epi = 1;
@@ -692,7 +1122,7 @@ void launch_ntt_list(u64* data, const void* list, int nlimbs, int logN, bool for
   NttArgs a{};
   a.list = reinterpret_cast<const LimbRef*>(list);
   a.src = data; a.data = data; a.mods = tw.mods; a.rows = 1; a.batch = 1;
-  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.logN = logN;
+  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.fpc = tw.fpc; a.logN = logN;
   a.tw = reinterpret_cast<const uint4*>(forward ? tw.tw : tw.itw);
   a.twr = reinterpret_cast<const uint4*>(forward ? tw.twr : tw.itwr);
   ntt_launch(a, nlimbs, forward, st);

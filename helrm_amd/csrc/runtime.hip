@@ -27,6 +27,7 @@
 #include <unordered_set>
 #include <vector>
 
+#include "fpntt.h"
 #include "hipckks.h"
 #include "kernels.h"
 #include "../../include/helrm_hip.h"
@@ -326,6 +327,7 @@ struct Scheme {
   DevArray<ModC> d_mods;
   DU64 tw2, itw2, ninv, ninvp;  // interleaved (w, w') twiddle pairs [mod][N][2]
   DU64 twr2, itwr2;             // row-pass consecutive-round twiddles, lane-interleaved
+  DevArray<FpC> fpc;            // float64 transform constants (moduli <= FP_QMAX)
   NttTables tw{};
   std::vector<ModC> hmods;
   // per-modulus constants (Shoup pairs indexed by modulus)
@@ -910,6 +912,7 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
     s.d_mods = DevArray<ModC>(nm); upload(s.d_mods.p, s.hmods.data(), nm);
     std::vector<u64> htw((size_t)nm * N * 2), hitw((size_t)nm * N * 2), hn(nm), hnp(nm);
     std::vector<u64> hiu(nm), hiup(nm), hniu(nm), hniup(nm);
+    std::vector<FpC> hfpc(nm, FpC{});
     for (int m = 0; m < nm; m++) {
       u64 qq = s.mod[m];
       u64 g = smallest_generator(qq);
@@ -926,6 +929,20 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
       hn[m] = invmod((u64)N, qq); hnp[m] = shoup(hn[m], qq);
       hiu[m] = pw[N / 2]; hiup[m] = shoup(hiu[m], qq);
       hniu[m] = qq - pw[N / 2]; hniup[m] = shoup(hniu[m], qq);
+      if (qq <= FP_QMAX) {
+        // float64 transform: (w, fl(w / q)) with w centred in (-q/2, q/2]
+        const double qd = (double)qq;
+        auto cen = [&](u64 w) { return w > qq / 2 ? (double)w - qd : (double)w; };
+        auto bits = [](double x) { u64 b; std::memcpy(&b, &x, 8); return b; };
+        for (size_t k = 0; k < (size_t)N; k++) {
+          const size_t o = ((size_t)m * N + k) * 2;
+          const double w = cen(htw[o]), iw = cen(hitw[o]);
+          htw[o] = bits(w); htw[o + 1] = bits(w / qd);
+          hitw[o] = bits(iw); hitw[o + 1] = bits(iw / qd);
+        }
+        const double ni = cen(hn[m]), wn = cen(mulmod(ipw[brv(1, logN)], hn[m], qq));
+        hfpc[m] = FpC{qd, 1.0 / qd, 4503599627370496.0 + qd, ni, ni / qd, wn, wn / qd, 0.0};
+      }
     }
     auto up = [&](DU64& d, const std::vector<u64>& h) { d = DU64(h.size()); upload(d.p, h.data(), h.size()); };
     up(s.iu, hiu); up(s.iup, hiup); up(s.niu, hniu); up(s.niup, hniup);
@@ -955,7 +972,8 @@ void build_scheme(int logN, const std::vector<u64>& q, const std::vector<u64>& p
           }
         }
     up(s.tw2, htw); up(s.itw2, hitw); up(s.twr2, htwr); up(s.itwr2, hitwr); up(s.ninv, hn); up(s.ninvp, hnp);
-    s.tw = NttTables{s.d_mods.p, s.tw2.p, s.itw2.p, s.twr2.p, s.itwr2.p, s.ninv.p, s.ninvp.p};
+    s.fpc = DevArray<FpC>(nm); upload(s.fpc.p, hfpc.data(), nm);
+    s.tw = NttTables{s.d_mods.p, s.tw2.p, s.itw2.p, s.twr2.p, s.itwr2.p, s.ninv.p, s.ninvp.p, s.fpc.p};
     std::vector<u64> pm(nm), pmp(nm), pin(nm), pinp(nm), p0i(nm), p0ip(nm), pmr(nm);
     for (int m = 0; m < nm; m++) {
       u64 qq = s.mod[m], P = 1;
