@@ -187,6 +187,7 @@ _SIGNATURES = {
     "AddRotationKey": ([_I], _I),
     "Rotate": ([_I, _I], _I),
     "RotateNew": ([_I, _I], _I),
+    "RotateAdd": ([_I, _I], _I),
     "RotateInto": ([_I, _I, _I], _I),
     "Conjugate": ([_I], _I),
     "ConjugateNew": ([_I], _I),

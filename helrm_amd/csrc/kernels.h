@@ -106,10 +106,12 @@ void launch_ntt_list(u64* data, const void* list, int nlimbs, int logN, bool for
 // Forward NTT of the Q rows 0..l of ext (the extension of [x]_P to Q) fused
 // with the ModDown combine: out[b][i][perm_inv^-1...] -- for every position p,
 // out[b][i][perm_inv[p]] = (x[b][i][p] - NTT(ext)[b][i][p]) * P^-1 (+ add[b][i][p]
-// for b < add_batches); ext itself is left in an intermediate state.
+// for b < add_batches) (+ acc[b][i][perm_inv[p]] if acc, a buffer other than
+// out); ext itself is left in an intermediate state.
 void launch_ntt_moddown(u64* ext, size_t ext_bstride, int batch, int l, int logN, const u64* x, size_t x_bstride,
                         u64* out, size_t o_bstride, const u64* add, size_t a_bstride, int add_batches,
-                        const uint32_t* perm_inv, const u64* pinv, const u64* pinvp, const NttTables& tw, hipStream_t st);
+                        const uint32_t* perm_inv, const u64* pinv, const u64* pinvp, const NttTables& tw, hipStream_t st,
+                        const u64* acc = nullptr, size_t c_bstride = 0);
 // dst[b][0..words) = src[b][0..words) for b < batch.
 void launch_copy(u64* dst, size_t dstride, const u64* src, size_t sstride, size_t words, int batch, hipStream_t st);
 void launch_add(u64* out, const u64* a, const u64* b, size_t bstride, int batch, RowMap rm, const ModC* mods, int N, bool sub, hipStream_t st);

@@ -215,6 +215,80 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
     outb[(size_t)row * N + x] = res;
   }
 }
+// The same extension for launches too small to fill the GPU one coefficient
+// per thread (a single key switch: a few thousand waves, each running every
+// destination row).  A workgroup takes 64 coefficients of one (batch entry,
+// job): its four waves load the sources and compute y_i and y_i / s_i once
+// (two sources each), share them through LDS, and each wave then produces
+// every fourth destination row -- four times the waves for the same work.
+// The overflow count sums y_i / s_i in source order, as the one-thread form.
+constexpr int BCL_X = 64;
+__global__ __launch_bounds__(256) void bconv_lds_kernel(const u64* __restrict__ in, size_t in_bstride, BConvJobs jobs,
+                                                       u64* __restrict__ out, size_t out_bstride,
+                                                       const ModC* __restrict__ mods, int N) {
+  constexpr int MAXS = 8;
+  const int b = blockIdx.z / jobs.n, d = blockIdx.z - b * jobs.n;
+  const BConvJob& J = jobs.j[d];
+  const BConvTable* __restrict__ tab = J.tab;
+  const int ns = J.ns;
+  const int lane = threadIdx.x & (BCL_X - 1), w = threadIdx.x / BCL_X;
+  const int x = blockIdx.x * BCL_X + lane;
+  const u64* inb = in + (size_t)b * in_bstride + (size_t)J.src_row * N;
+  u64* outb = out + (size_t)b * out_bstride + J.out_off;
+  const RowMap rm = J.rm;
+  const int nrows = rm.nact();
+  __shared__ u64 sy[MAXS][BCL_X];
+  __shared__ double st[MAXS][BCL_X];
+  __shared__ u64 svs[HCK_MAXMOD * (MAXS + 1)];
+  // sources w and w + 4 of this coefficient
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int i = w + 4 * k;
+    const BConvSrc s = tab->src[i];
+    const bool act = i < ns;
+    const u64 xi = inb[(size_t)(act ? i : 0) * N + x];
+    const u64 yi = shoup_mul(xi, s.hinv, s.hinvp, s.q);
+    const double t = (double)yi / s.qd;
+    sy[i][lane] = act ? yi : 0;
+    st[i][lane] = act ? t : 0.0;
+  }
+  {
+    const u64* __restrict__ vS = tab->vS;
+    const int wd = ns + 1, n = nrows * wd;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+      const int rr = e / wd;
+      svs[e] = vS[(size_t)rm.mod(rm.row(rr)) * wd + (e - rr * wd)];
+    }
+  }
+  __syncthreads();
+  u64 y[MAXS];
+  double vf = 0.0;
+#pragma unroll
+  for (int i = 0; i < MAXS; i++) {
+    y[i] = sy[i][lane];
+    vf += st[i][lane];
+  }
+  const int v = J.force_v0 ? 0 : (int)(u64)vf;
+  const u64* __restrict__ hat = tab->hat;
+  for (int r = w; r < nrows; r += 4) {
+    const int row = rm.row(r);
+    const int m = rm.mod(row);
+    const ModC mc = mods[m];
+    const u64* __restrict__ h = hat + (size_t)m * ns;
+    Acc61 A;
+#pragma unroll
+    for (int i = 0; i < MAXS; i++) {  // y[i] = 0 past ns
+      if (i == 0) acc61_first_s(A, y[i], h[i]);
+      else if (i < 4) acc61_mac_s<0>(A, y[i], h[i]);
+      else if (i == 4) acc61_first_half_s(A, y[i], h[i]);
+      else acc61_mac_s<1>(A, y[i], h[i]);
+    }
+    u64 lo, hi;
+    acc61_value(A, lo, hi);
+    const u64 res = redc(lo, hi, mc.q, mc.qinv);
+    outb[(size_t)row * N + x] = sub_mod(res, svs[r * (ns + 1) + v], mc.q);
+  }
+}
 void launch_bconv(const u64* in, size_t in_bstride, BConvJobs jobs, u64* out, size_t out_bstride, int batch,
                   const ModC* mods, int N, hipStream_t st) {
   if (jobs.n <= 0 || batch <= 0) return;
@@ -226,6 +300,12 @@ void launch_bconv(const u64* in, size_t in_bstride, BConvJobs jobs, u64* out, si
   if (nrows <= 0) return;
   // all destination rows in one thread unless that leaves too few workgroups
   const int cols = N / 256;
+  // a launch of at most a few waves per SIMD: the shared-source form
+  if (nsmax <= 8 && N % BCL_X == 0 && (long)cols * batch * jobs.n < 2048) {
+    hipLaunchKernelGGL(bconv_lds_kernel, dim3(N / BCL_X, 1, batch * jobs.n), dim3(256), 0, st, in, in_bstride, jobs, out,
+                       out_bstride, mods, N);
+    return;
+  }
   int ny = 1;
   while (ny < nrows && (long)cols * batch * jobs.n * ny < 768) ny *= 2;
   jobs.rows_per_block = (nrows + ny - 1) / ny;

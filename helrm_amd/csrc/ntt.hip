@@ -230,14 +230,15 @@ struct LimbRef { int64_t off; int mod; int pad; };  // pad: batch entry (RowMap 
 
 // ModDown epilogue of a forward transform (the transform of the extension of
 // [x]_P to Q): instead of the transform v, the row pass writes
-//   out[b][row][perm^-1(pos)] = (x[b][row][pos] - v) * P^-1 (+ add[b][row][pos])
-// so the extension never goes back to memory.
+//   out[b][row][d] = (x[b][row][pos] - v) * P^-1 (+ add[b][row][pos]) (+ acc[b][row][d]),
+// d = perm^-1(pos), so the extension never goes back to memory.
 struct ModDownEpi {
   const u64* x; size_t x_bstride;       // Q rows of the QP polynomial
   u64* out; size_t o_bstride;
   const u64* add; size_t a_bstride; int add_batches;
   const uint32_t* perm_inv;             // nullptr: identity
   const u64 *pinv, *pinvp;              // [mod] P^-1 mod q and its Shoup companion
+  const u64* acc; size_t c_bstride;     // nullptr, or added at the output position (out != acc)
 };
 
 struct NttArgs {
@@ -436,6 +437,13 @@ __device__ __forceinline__ void row_fwd_tail(const NttArgs& a, const u64* srow, 
     } else {
 #pragma unroll
       for (int i = 0; i < 16; i++) dst[i] = (uint32_t)(r * C + j + P * i);
+    }
+    if (a.e.acc) {
+      // a sum of the result and acc: acc at the output position, gathered
+      // through the same permutation as the stores
+      const u64* crow = a.e.acc + (size_t)b * a.e.c_bstride + ((size_t)row << a.logN);
+#pragma unroll
+      for (int i = 0; i < 16; i++) av[i] = add_mod(av[i], crow[dst[i]], q);
     }
 #pragma unroll
     for (int i = 0; i < 16; i++) {
@@ -810,6 +818,11 @@ __device__ __forceinline__ void row8_fwd_tail(const NttArgs& a, const u64* srow,
 #pragma unroll
       for (int i = 0; i < 8; i++) dst[i] = (uint32_t)(r * C + w8_elem(L0, t, i));
     }
+    if (a.e.acc) {
+      const u64* crow = a.e.acc + (size_t)b * a.e.c_bstride + ((size_t)row << a.logN);
+#pragma unroll
+      for (int i = 0; i < 8; i++) av[i] = add_mod(av[i], crow[dst[i]], q);
+    }
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const int pos = w8_elem(L0, t, i);
@@ -1103,7 +1116,8 @@ void launch_ntt(const u64* src, size_t sstride, u64* data, size_t bstride, int b
 
 void launch_ntt_moddown(u64* ext, size_t ext_bstride, int batch, int l, int logN, const u64* x, size_t x_bstride,
                         u64* out, size_t o_bstride, const u64* add, size_t a_bstride, int add_batches,
-                        const uint32_t* perm_inv, const u64* pinv, const u64* pinvp, const NttTables& tw, hipStream_t st) {
+                        const uint32_t* perm_inv, const u64* pinv, const u64* pinvp, const NttTables& tw, hipStream_t st,
+                        const u64* acc, size_t c_bstride) {
   const RowMap rm{l + 1, l + 1, 0, 0, 0, 0};
   NttArgs a{};
   a.list = nullptr;
@@ -1113,7 +1127,7 @@ void launch_ntt_moddown(u64* ext, size_t ext_bstride, int batch, int l, int logN
   a.tw = reinterpret_cast<const uint4*>(tw.tw);
   a.twr = reinterpret_cast<const uint4*>(tw.twr);
   a.epi = 1;
-  a.e = ModDownEpi{x, x_bstride, out, o_bstride, add, a_bstride, add_batches, perm_inv, pinv, pinvp};
+  a.e = ModDownEpi{x, x_bstride, out, o_bstride, add, a_bstride, add_batches, perm_inv, pinv, pinvp, acc, c_bstride};
   ntt_launch(a, (l + 1) * batch, true, st);
 }
 

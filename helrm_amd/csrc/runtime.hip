@@ -594,8 +594,11 @@ void decompose_modup(int l, const u64* c1, size_t c1_bstride, int batch, u64* di
 // written through perm_inv (out[perm_inv[p]] takes position p; nullptr: identity)
 // ws: nullptr -> temporaries from the buffer cache; else batch * (K + l + 1) * N
 // device words the call may overwrite (nothing is allocated)
+// acc: nullptr, or a buffer other than out whose words (at the output
+// positions, batch stride o_bstride) are added to the result
 void mod_down(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t o_bstride, const u64* add = nullptr,
-              size_t a_bstride = 0, int add_batches = 0, const uint32_t* perm_inv = nullptr, u64* ws = nullptr) {
+              size_t a_bstride = 0, int add_batches = 0, const uint32_t* perm_inv = nullptr, u64* ws = nullptr,
+              const u64* acc = nullptr) {
   Scheme& s = sch();
   const int N = s.N, K = s.K;
   DU64 pc_buf, ext_buf;
@@ -608,7 +611,7 @@ void mod_down(int l, const u64* x, size_t x_bstride, int batch, u64* out, size_t
   launch_bconv(pc, (size_t)K * N, K, bt.dtab.p, ext, (size_t)(l + 1) * N, batch, rows_q(l), s.d_mods.p, N, false, s.st);
   // forward transform of the extension fused with (x - ext) * P^-1 (+ add), gathered through perm
   launch_ntt_moddown(ext, (size_t)(l + 1) * N, batch, l, s.logN, x, x_bstride, out, o_bstride, add, a_bstride,
-                     add_batches, perm_inv, s.pinv_w.p, s.pinv_wp.p, s.tw, s.st);
+                     add_batches, perm_inv, s.pinv_w.p, s.pinv_wp.p, s.tw, s.st, acc, o_bstride);
 }
 
 // out[b] (Q rows 0..l-1, stride o_bstride) = Rescale(ModDown(x[b])) for the
@@ -1051,7 +1054,9 @@ size_t automorphism_ws_words(int l) {
   const size_t N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
   return (std::max(dn * nqp, 2 * K + 2 * (size_t)(l + 1)) + 2 * nqp + (size_t)(l + 1)) * N;
 }
-void automorphism_core(const Cipher& ct, const u64* key, const uint32_t* perm_inv, u64* out, u64* ws) {
+// acc: nullptr, or a ciphertext at ct's level (not out) added to the result
+void automorphism_core(const Cipher& ct, const u64* key, const uint32_t* perm_inv, u64* out, u64* ws,
+                       const u64* acc = nullptr) {
   Scheme& s = sch();
   const int l = ct.level, N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
   DU64 digits_buf, dd_buf;
@@ -1073,7 +1078,7 @@ void automorphism_core(const Cipher& ct, const u64* key, const uint32_t* perm_in
   a.out0 = dd; a.out1 = dd + (size_t)nqp * N; a.out_bstride = 0; a.mods = s.d_mods.p;
   a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
   launch_keymac(a, 1, s.st);
-  mod_down(l, dd, (size_t)nqp * N, 2, out, (size_t)(l + 1) * N, ct.d.p, 0, 1, perm_inv, md);
+  mod_down(l, dd, (size_t)nqp * N, 2, out, (size_t)(l + 1) * N, ct.d.p, 0, 1, perm_inv, md, acc);
 }
 std::unique_ptr<Cipher> automorphism(const Cipher& ct, u64 galel, bool lt_keyset) {
   const u64* key = key_ptr(galel, lt_keyset);
@@ -1940,6 +1945,23 @@ int RotateNew(int ctID, int amount) {
   return guard([&] {
     u64 ge = galois_element(amount); ensure_galois_key(ge); sch().rot_keys.insert(ge);
     return push_ct(automorphism(get_ct(ctID), ge, false));
+  });
+}
+// [ext] ct <- ct + Rotate(ct, amount): one step of a Linear's output fold
+// (linear.py:115-117, `out += out.roll(k)`), the add done in the key
+// switch's ModDown epilogue instead of a separate pass.  The sum is formed in
+// a new buffer (the epilogue's scattered stores cannot overwrite the words
+// they read) that then replaces the ciphertext's own.  Same words as
+// RotateNew + AddCiphertext.
+int RotateAdd(int ctID, int amount) {
+  return guard([&] {
+    u64 ge = galois_element(amount); ensure_galois_key(ge); sch().rot_keys.insert(ge);
+    Cipher& ct = get_ct(ctID);
+    const u64* key = key_ptr(ge, false);
+    auto out = new_ct(ct.level, ct.scale);
+    timed("rotate", [&] { automorphism_core(ct, key, perm_inv_for(ge), out->d.p, nullptr, ct.d.p); });
+    std::swap(ct.d, out->d);
+    return ctID;
   });
 }
 // RotateNew into an existing ciphertext with no allocation: the key switch's

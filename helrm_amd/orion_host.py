@@ -321,6 +321,20 @@ class CipherTensor:
         f = b.Rotate if in_place else b.RotateNew
         return CipherTensor(self.scheme, [f(c, int(amount)) for c in self.ids], self.n)
 
+    def add_rolled(self, amount):
+        """self += self.roll(amount), in place: the fold step of linear.py:115-117.
+        One backend call per ciphertext (RotateAdd, the add inside the key
+        switch's last pass) when the backend has it; else roll + add."""
+        b = self.scheme.backend
+        if hasattr(b, "RotateAdd"):
+            for c in self.ids:
+                b.RotateAdd(c, int(amount))
+            return self
+        rolled = self.roll(amount)
+        self.add(rolled, True)
+        rolled.free()
+        return self
+
     def free(self):
         for c in self.ids:
             self.scheme.backend.DeleteCiphertext(c)
@@ -443,9 +457,7 @@ class LinearLayer:
         out = self.evaluate_lt(x)
         slots = self.scheme.params.get_slots()
         for i in range(1, self.output_rotations + 1):
-            rolled = out.roll(slots // (2 ** i))
-            out += rolled
-            rolled.free()
+            out.add_rolled(slots // (2 ** i))
         out += self.on_bias_ptxt
         return out
 

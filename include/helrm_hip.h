@@ -91,6 +91,12 @@ int NewEvaluator(void);                   /* evaluator.go:13-35 (+ power-of-two 
 int AddRotationKey(int rotation);         /* evaluator.go:37-52 */
 int Rotate(int ciphertextID, int amount); /* evaluator.go:80-87 */
 int RotateNew(int ciphertextID, int amount); /* evaluator.go:89-101 */
+/* [ext] ciphertextID <- ciphertextID + Rotate(ciphertextID, amount), one step
+ * of a Linear's output fold (`out += out.roll(k)`, linear.py:115-117 ->
+ * RotateNew evaluator.go:89-101 + AddCiphertext evaluator.go:297-304) with
+ * the add done in the key switch's last pass.  Same words as RotateNew +
+ * AddCiphertext.  Returns ciphertextID. */
+int RotateAdd(int ciphertextID, int amount);
 /* [ext] No counterpart in the reference.  For callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops): RotateNew
  * written into the existing ciphertext outID (!= ciphertextID, with room for

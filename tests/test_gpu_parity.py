@@ -264,6 +264,22 @@ def test_rotate(ctx, rot):
     assert np.abs(dec - np.roll(vals, -k)).max() < 1e-2
 
 
+@pytest.mark.parametrize("rot", [1, 5, -1, "half"])
+def test_rotate_add(ctx, rot):
+    """RotateAdd (the fold step with the add inside the key switch) against
+    the oracle's rotate + add, at the top level and one below."""
+    k = ctx.slots // 2 if rot == "half" else rot
+    for level in (ctx.L - 1, ctx.L - 2):
+        ct, ref, vals = ctx.fresh_ct(level, 40 + (k % 7))
+        before = ctx.lib.export_ciphertext(ct)
+        assert ctx.lib.RotateAdd(ct, k) == ct
+        want = ctx.orc.add(ref, ctx.orc.rotate(ref, level, k), level)
+        assert_equal_u64(ctx.lib.export_ciphertext(ct), want, f"rotate_add {k} level {level}")
+        assert not np.array_equal(before, want)
+        dec = np.asarray(ctx.lib.Decode(ctx.lib.Decrypt(ct)))
+        assert np.abs(dec - (vals + np.roll(vals, -k))).max() < 1e-2
+
+
 def test_rescale(ctx):
     level = ctx.L - 1
     ct, ref, _ = ctx.fresh_ct(level, 21)
