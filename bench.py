@@ -25,16 +25,26 @@ METRIC = "encrypted embedding lookups/sec (26-table PCMM, N=2^16)"
 HBM_PEAK_GBS = 8000.0
 
 
+def mac_unit_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, w=8):
+    """Algorithmic bytes of the fused diagonal MAC by its per-unit definition:
+    every QP diagonal read once, 2*n1 baby-step and 2*n2 giant-step QP
+    polynomials (the rotated inputs read, the accumulators written):
+    D*(L+K)*N*w + 2*n1*(L+K)*N*w + 2*n2*(L+K)*N*w."""
+    return (D + 2 * n1 + 2 * n2) * (L + K) * N * w
+
+
 def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=8, chunks=1, fused_babies=True):
     """Per-PCMM and per-diag-MAC-launch algorithmic HBM bytes (every word once).
 
     PCMM: the diagonals, each of the R rotation keys, the input and the output
-    ciphertext.  Diagonal MAC launch (the giant groups split evenly over
-    `chunks` launches): its share of the diagonals and P*c (2 Q polys, baby
-    step 0) read, one QP accumulator pair per giant group of the launch
-    written, and the n1-1 hoisted baby rotations -- computed in the kernel's
-    prologue from their keys (dnum*2 QP polys each) and the decomposed input
-    (dnum QP polys, once) when fused_babies, else read (2 QP polys each)."""
+    ciphertext.  Diagonal MAC launch, counted as this kernel works (the giant
+    groups split evenly over `chunks` launches): its share of the diagonals
+    and P*c (2 Q polys, baby step 0) read, one QP accumulator pair per giant
+    group of the launch written, and the n1-1 hoisted baby rotations --
+    computed in the kernel's prologue from their keys (dnum*2 QP polys each)
+    and the decomposed input (dnum QP polys, once) when fused_babies, else
+    read (2 QP polys each).  mac_unit_bytes is the per-unit definition the
+    roofline is quoted on."""
     R = (n1 - 1) + (n2 - 1) + f
     pcmm = D * (L + K) * N * w + R * dnum * 2 * (L + K) * N * w + 2 * L * N * w + 2 * (L - 1) * N * w
     if fused_babies:
@@ -45,14 +55,16 @@ def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=
     return pcmm, diag_mac
 
 
-def keyswitch_pass_rows(level, K):
+def keyswitch_pass_rows(level, K, fold_add=False):
     """Rows of N words that one single key switch at `level` moves, pass by
-    pass (a transform is 2 passes, each reading and writing its limb)."""
+    pass (a transform is 2 passes, each reading and writing its limb);
+    fold_add: the fold step ct + Rotate(ct) (RotateAdd), whose last pass also
+    reads both parts of ct at the output positions."""
     ql = level + 1
     nqp = ql + K
     dn = (nqp - 1) // K
     ext = dn * nqp - ql  # extended digit rows: every QP row but each digit's own
-    return {
+    rows = {
         "inverse NTT of c1": 4 * ql,
         "extension of the digits": ql + ext,
         "forward NTT of the extended rows": 4 * ext,
@@ -61,6 +73,9 @@ def keyswitch_pass_rows(level, K):
         "extension P -> Q, both parts": 2 * K + 2 * ql,
         "forward NTT with the ModDown epilogue": 2 * 2 * ql + (2 * ql + 2 * ql + ql + 2 * ql),
     }
+    if fold_add:
+        rows["the fold's addend, read in the epilogue"] = 2 * ql
+    return rows
 
 
 def read_traffic(kernel="diag_mac"):
@@ -95,12 +110,9 @@ def cpu_baseline(q, p, h, key_seed, diagonals, selector, level, logscale, thread
     fold and bias, with keys and diagonals prepared before the timed region;
     1 warm-up + `repeats` timed runs at `threads` OpenMP threads, the mean
     reported and every trial kept (the reference's protocol,
-    examples/criteo/README.md:95-96).  On one thread (the reference times
-    Lattigo with GOMAXPROCS=1, table2.py:48) a whole PCMM takes tens of
-    seconds, so that figure is extrapolated: the decomposition, the baby
-    rotations, giant groups 0 and 1, the final ModDown and the epilogue are
-    measured and the other giant groups scaled from group 1.
-    Returns a dict of the figures."""
+    examples/criteo/README.md:95-96); then the same on one thread (the
+    reference times Lattigo with GOMAXPROCS=1, table2.py:48), whole PCMMs as
+    well (about 20 s each).  Returns a dict of the figures."""
     from oracle import oracle as O
     O.set_threads(threads)
     orc = O.Oracle(16, q, p, h=h, seed=key_seed)
@@ -142,29 +154,17 @@ def cpu_baseline(q, p, h, key_seed, diagonals, selector, level, logscale, thread
                           f"({t_prep:.1f} s)")}
         if single_thread:
             O.set_threads(1)
-            ct = orc.encrypt(orc.encode(selector, level, scale), level, 0)
-            tm = {}
-            t0 = time.perf_counter(); orc.lt_eval_partial(t, ct, level, 0, 0); tm["common"] = time.perf_counter() - t0
-            t0 = time.perf_counter(); orc.lt_eval_partial(t, ct, level, 0, 1); tm["g0"] = time.perf_counter() - t0 - tm["common"]
-            t0 = time.perf_counter(); acc = orc.lt_eval_partial(t, ct, level, 1, 2); tm["gks"] = time.perf_counter() - t0 - tm["common"]
-            t0 = time.perf_counter()
-            out = np.stack([orc.mod_down(acc[0], level), orc.mod_down(acc[1], level)])
-            tm["moddown"] = time.perf_counter() - t0
-            t0 = time.perf_counter()
-            l = level
-            out = orc.rescale(out, l); l -= 1
-            for i in range(1, fold + 1):
-                out = orc.add(out, orc.rotate(out, l, slots >> i), l)
-            out[0] = orc.add(out[0][None], orc.encode(np.zeros(1, np.float32), l, scale)[None], l)[0]
-            tm["epilogue"] = time.perf_counter() - t0
-            t1 = tm["common"] + tm["g0"] + (ng - 1) * tm["gks"] + tm["moddown"] + tm["epilogue"]
+            pcmm()
+            trials1 = []
+            for _ in range(repeats):
+                t0 = time.perf_counter()
+                pcmm()
+                trials1.append(time.perf_counter() - t0)
+            t1 = float(np.mean(trials1))
             res["single_thread"] = {
-                "value": per_step / t1, "seconds_per_pcmm": t1, "extrapolated": True,
-                "sample": (f"CPU restatement (oracle/), 1 thread, extrapolated: measured the decomposition + "
-                           f"{len([r for r in rots if 0 < r < orc.lt_n1(t)])} hoisted baby rotations, giant groups "
-                           f"0 and 1 of {ng}, final ModDown, rescale, {fold}-rotation fold and bias; the other "
-                           f"{ng - 2} key-switched giant groups scaled from group 1 ({tm['gks']:.3f} s); "
-                           f"estimated {t1:.2f} s per PCMM")}
+                "value": per_step / t1, "seconds_per_pcmm": t1, "trials_s": trials1, "extrapolated": False,
+                "sample": (f"CPU restatement (oracle/), 1 thread: whole PCMMs as above, 1 warm-up + {repeats} timed, "
+                           f"mean {t1:.2f} s")}
         return res
     finally:
         orc.close()
@@ -350,6 +350,46 @@ def ntt_microbench(lib, reps=5):
     return res
 
 
+def inflight_bench(lib, w, depth=2, queries=12):
+    """Throughput with `depth` different queries in flight on one GPU: query i
+    goes to the library's stream i % 2 and the queries are issued back to
+    back, so one query's fold and small key switches share the chip with the
+    next one's diagonal MAC.  Every output is compared word for word with the
+    same query run alone.  Reported beside the batch-1 latency, not instead
+    of it."""
+    cts = [w.ct_in] + [w.make_query(1000 + k)[0] for k in range(depth - 1)]
+    ref = []
+    for ct in cts:
+        o = w.forward(ct)
+        ref.append(lib.export_ciphertext(o.ids[0]))
+        o.free()
+
+    def burst(n):
+        outs = []
+        for i in range(n):
+            lib.SetStream(i % 2)
+            outs.append(w.forward(cts[i % depth]))
+        lib.SetStream(0)
+        lib.JoinStream(1)
+        return outs
+    for o in burst(2 * depth):
+        o.free()
+    lib.Synchronize()
+    t0 = time.perf_counter()
+    outs = burst(queries)
+    lib.Synchronize()
+    t1 = time.perf_counter()
+    exact = all(np.array_equal(lib.export_ciphertext(o.ids[0]), ref[i % depth]) for i, o in enumerate(outs))
+    for o in outs:
+        o.free()
+    for ct in cts[1:]:
+        ct.free()
+    ms = (t1 - t0) * 1000.0 / queries
+    return {"depth": depth, "queries": queries, "ms_per_query": ms, "queries_per_s": 1000.0 / ms,
+            "outputs_bit_exact_with_serial": bool(exact),
+            "note": f"{queries} queries issued back to back, query i on HIP stream i % 2, wall time / queries"}
+
+
 def read_valu_counts():
     """VALU wave-instructions per limb and pass of the NTT kernels, from the
     committed rocprofv3 PMC summary, if present."""
@@ -400,6 +440,9 @@ def main():
                     help="transforms return the un-rescaled result and the host rescales (Lattigo's convention); "
                          "by default they return the rescaled one (lt_output_prerescaled: the first rescale fused "
                          "into the final ModDown, the same residues)")
+    ap.add_argument("--inflight", type=int, default=2, metavar="D",
+                    help="also measure throughput with D different queries in flight on two HIP streams "
+                         "(embedding PCMM workloads; 0: skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (PMC counter calibration) and exit")
     args = ap.parse_args()
@@ -496,12 +539,13 @@ def main():
     # diagonal-MAC launches per step (one per 32 baby steps of every Linear)
     launches = max(1, round(kt["diag_mac"]["launches"] / nprof)) if kt["diag_mac"]["launches"] else 1
     layers = w.linear_layers()
-    step_bytes, mac_bytes, lt_shapes = 0, 0, []
+    step_bytes, mac_bytes, mac_unit, lt_shapes = 0, 0, 0, []
     ks_bytes = {"giant_acc": 0}
     for layer in layers:
         (b_layer, b_mac), lti = lt_roofline_bytes(lib, layer, N, K)
         step_bytes += b_layer
         mac_bytes += b_mac
+        mac_unit += mac_unit_bytes(N=N, L=layer.level + 1, K=K, D=lti["plaintexts"], n1=lti["baby"], n2=lti["giant"])
         _, kg = keyswitch_bytes(N, layer.level + 1, K, lti["baby"], lti["giant"])
         ks_bytes["giant_acc"] += kg if lti["giant"] > 1 else 0
         lt_shapes.append({"level": layer.level, "diagonals": lti["plaintexts"], "baby": lti["baby"],
@@ -511,19 +555,33 @@ def main():
         for name, _ in w.activations():
             lq = w.levels[name] + 1
             step_bytes += 2 * ((lq + K - 1) // K) * 2 * (lq + K) * N * 8
-    # average algorithmic bytes per diagonal-MAC launch over one step
+    # algorithmic bytes per diagonal-MAC launch over one step: the per-unit
+    # definition (diagonals + 2*n1 baby-step + 2*n2 giant-step QP polynomials)
+    # is the roofline; the kernel's own count (it computes the baby rotations
+    # in its prologue from their keys and the decomposed input, so it reads
+    # those instead of rotated polynomials) is reported beside it
+    unit_per_launch = mac_unit / launches
     mac_per_launch = mac_bytes / launches
     mac_ms = kt["diag_mac"]["avg_ms"]
-    achieved = mac_per_launch / (mac_ms / 1000.0) / 1e9 if mac_ms else None
+    achieved = unit_per_launch / (mac_ms / 1000.0) / 1e9 if mac_ms else None
+    achieved_k = mac_per_launch / (mac_ms / 1000.0) / 1e9 if mac_ms else None
     roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": (achieved / HBM_PEAK_GBS) if achieved else None,
                 "traffic": read_traffic("diag_mac") if args.workload == "pcmm26" else None,
-                "kernel": "diag_mac_kernel", "algorithmic_bytes_per_launch": mac_per_launch,
-                "launches_per_step": launches}
+                "kernel": "diag_mac_kernel", "algorithmic_bytes_per_launch": unit_per_launch,
+                "launches_per_step": launches,
+                "definition": "D*(L+K)*N*w diagonals + 2*n1*(L+K)*N*w + 2*n2*(L+K)*N*w baby- and giant-step QP polynomials",
+                "kernel_count": {"algorithmic_bytes_per_launch": mac_per_launch, "achieved": achieved_k,
+                                 "frac": (achieved_k / HBM_PEAK_GBS) if achieved_k else None,
+                                 "definition": ("diagonals, the hoisted baby rotations' keys and the decomposed input "
+                                                "(the rotations computed in the prologue), P*c, one QP accumulator "
+                                                "pair per giant group")}}
     lti = lib.lt_info(list(layers[0].transform_ids.values())[0])
     # the key-switch kernels of the transforms against the same peak
-    kernel_rooflines = {"diag_mac": {"algorithmic_bytes_per_launch": mac_per_launch, "avg_ms": mac_ms,
-                                     "achieved_GBs": achieved, "frac": roofline["frac"]}}
+    kernel_rooflines = {"diag_mac": {"algorithmic_bytes_per_launch": unit_per_launch, "avg_ms": mac_ms,
+                                     "achieved_GBs": achieved, "frac": roofline["frac"],
+                                     "kernel_count_bytes_per_launch": mac_per_launch,
+                                     "kernel_count_frac": roofline["kernel_count"]["frac"]}}
     for name, total in ks_bytes.items():
         n_l = kt[name]["launches"] / nprof if kt[name]["launches"] else 0
         if not n_l or not kt[name]["avg_ms"]:
@@ -534,14 +592,15 @@ def main():
                                   "achieved_GBs": gbs, "frac": gbs / HBM_PEAK_GBS}
 
     # the single-ciphertext key switch: the fold's rotations (one key switch
-    # each at the transform's output level) against the per-rotation bytes
+    # each at the transform's output level, the fold's add inside its last
+    # pass) against the per-rotation bytes
     # key dnum*2*(l+1+K)*N*w + digits dnum*(l+1+K)*N*w + output 2*(l+1+K)*N*w
     if kt["rotate"]["launches"] and len(layers) == 1:
         lf = layers[0].level - 1  # the fold runs on the rescaled transform output
         nqp, dn = lf + 1 + K, (lf + 1 + K - 1) // K
         rb = (dn * 2 + dn + 2) * nqp * N * 8
         r_ms = kt["rotate"]["avg_ms"]
-        pb = sum(keyswitch_pass_rows(lf, K).values()) * N * 8
+        pb = sum(keyswitch_pass_rows(lf, K, fold_add=True).values()) * N * 8
         kernel_rooflines["keyswitch_rotation"] = {
             "level": lf, "algorithmic_bytes_per_rotation": rb, "avg_ms": r_ms,
             "rotations_per_step": kt["rotate"]["launches"] / nprof,
@@ -567,6 +626,10 @@ def main():
         if "single_thread" in r:
             cpu["single_thread"] = r["single_thread"]
 
+    inflight = None
+    if args.inflight > 1 and cfg["kind"] == "pcmm" and not args.seeded_upload:
+        inflight = inflight_bench(lib, w, args.inflight)
+        inflight["lookups_per_s"] = inflight["queries_per_s"] * per_step
     ntt = None if args.no_ntt_microbench else ntt_microbench(lib)
 
     line = {
@@ -596,6 +659,7 @@ def main():
         "kernel_rooflines": kernel_rooflines,
         "cpu_baseline": cpu,
         "max_abs_err_vs_plaintext": err,
+        "inflight": inflight,
         "ntt_microbench": ntt,
         "setup_s": t_setup,
     }

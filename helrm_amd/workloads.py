@@ -113,7 +113,11 @@ class LinearWorkload:
     def run(self):
         """One forward of the layer. Returns the output CipherTensor."""
         self.expand_upload()
-        return self.layer.forward(self.ct_in)
+        return self.forward(self.ct_in)
+
+    def forward(self, ct):
+        """The layer's forward on the encrypted input ct."""
+        return self.layer.forward(ct)
 
     def decrypt_output(self, out):
         vals = self.scheme.decode(self.scheme.decrypt(out))
@@ -163,9 +167,26 @@ class PCMMWorkload(LinearWorkload):
         self.selector = oh.expanded_sparse(self.indices, sizes, threshold, base)
         self.input = self.selector
         self.matrix = oh.block_diag_matrix(self.tables)
-        self.expected = np.concatenate([
-            t[0][int(i)] if s <= threshold else oh.radix_lookup(t, int(i), base)
-            for t, i, s in zip(self.tables, self.indices, sizes)])
+        self.expected = self.lookup_of(self.indices)
+
+    def lookup_of(self, indices):
+        """The plaintext embedding lookup of one query (one index per table)."""
+        base = self.cfg["base"]
+        return np.concatenate([
+            t[0][int(i)] if s <= self.threshold else oh.radix_lookup(t, int(i), base)
+            for t, i, s in zip(self.tables, indices, self.sizes)])
+
+    def make_query(self, seed):
+        """Another query on the same tables: indices drawn from `seed`, its
+        selector encoded and encrypted at the layer's level.  Returns
+        (CipherTensor, plaintext lookup)."""
+        rng = np.random.default_rng(seed)
+        idx = np.array([rng.integers(0, s) for s in self.sizes])
+        pt = self.scheme.encode(oh.expanded_sparse(idx, self.sizes, self.threshold, self.cfg["base"]), self.layer.level)
+        ct = self.scheme.encrypt(pt)
+        for i in pt.ids:
+            self.backend.DeletePlaintext(i)
+        return ct, self.lookup_of(idx)
 
 
 class SparseToTopWorkload(PCMMWorkload):
@@ -189,9 +210,8 @@ class SparseToTopWorkload(PCMMWorkload):
                                      name="sparse_to_top").compile()
         return self
 
-    def run(self):
-        self.expand_upload()
-        emb = self.layer.forward(self.ct_in)
+    def forward(self, ct):
+        emb = self.layer.forward(ct)
         out = self.repack.forward(emb)
         emb.free()
         return out

@@ -1422,6 +1422,3 @@ void orc_lt_eval(orc_ctx* c, const orc_lt* t, const uint64_t* ct, int ct_level, 
     lt_eval_bsgs(c, t, ct, ct_level, 0, t->ngiant, acc, 1, out);
     free(acc);
 }
-void orc_lt_eval_partial(orc_ctx* c, const orc_lt* t, const uint64_t* ct, int ct_level, int g0, int g1, uint64_t* acc_qp) {
-    lt_eval_bsgs(c, t, ct, ct_level, g0, g1, acc_qp, 0, NULL);
-}

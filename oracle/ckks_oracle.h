@@ -126,10 +126,6 @@ const uint64_t* orc_lt_plaintext(const orc_lt* t, int diag_index);
 int     orc_lt_rotations(const orc_lt* t, int* out);
 void    orc_lt_eval(orc_ctx* c, const orc_lt* t, const uint64_t* ct,
                     int ct_level, uint64_t* out);
-/* Evaluate only giant groups [g0, g1) of the BSGS sum; used by the bounded
- * CPU-baseline sample.  out is the QP accumulator before the final ModDown. */
-void    orc_lt_eval_partial(orc_ctx* c, const orc_lt* t, const uint64_t* ct,
-                            int ct_level, int g0, int g1, uint64_t* acc_qp);
 int     orc_lt_num_giant(const orc_lt* t);
 void    orc_set_threads(int n);
 

@@ -85,7 +85,6 @@ def lib():
             "orc_lt_plaintext": ([vp, ctypes.c_int], u64p),
             "orc_lt_rotations": ([vp, intp], ctypes.c_int),
             "orc_lt_eval": ([vp, vp, u64p, ctypes.c_int, u64p], None),
-            "orc_lt_eval_partial": ([vp, vp, u64p, ctypes.c_int, ctypes.c_int, ctypes.c_int, u64p], None),
             "orc_lt_num_giant": ([vp], ctypes.c_int),
             "orc_set_threads": ([ctypes.c_int], None),
             "orc_relin_key": ([vp], u64p),
@@ -441,13 +440,6 @@ class Oracle:
         out = np.zeros((2, l + 1, self.N), dtype=np.uint64)
         lib().orc_lt_eval(self.ctx, t, _p(ct), ct_level, _p(out))
         return out, l
-
-    def lt_eval_partial(self, t, ct, ct_level, g0, g1):
-        ct = np.ascontiguousarray(ct, dtype=np.uint64)
-        l = min(ct_level, lib().orc_lt_level(t))
-        acc = np.zeros((2, l + 1 + self.K, self.N), dtype=np.uint64)
-        lib().orc_lt_eval_partial(self.ctx, t, _p(ct), ct_level, g0, g1, _p(acc))
-        return acc
 
     def lt_num_giant(self, t):
         return lib().orc_lt_num_giant(t)

@@ -35,6 +35,15 @@ def test_pcmm26_algorithmic_bytes():
     assert unfused == 512 * nqp * N * w + 15 * 2 * nqp * N * w + 2 * 24 * N * w + 32 * 2 * nqp * N * w
 
 
+def test_mac_unit_bytes():
+    """The fused MAC by its per-unit definition: 512 QP diagonals, 2 x 16
+    baby-step and 2 x 32 giant-step QP polynomials of 32 rows of 2^16 words."""
+    assert bench.mac_unit_bytes() == 10_200_547_328
+    assert bench.mac_unit_bytes() == (512 + 2 * 16 + 2 * 32) * 32 * (1 << 16) * 8
+    # the dense 512x256 layer at 16 limbs (K=6): same split, 22 QP rows
+    assert bench.mac_unit_bytes(L=16, K=6) == (512 + 32 + 64) * 22 * (1 << 16) * 8
+
+
 def test_keyswitch_kernel_bytes():
     """keymac_baby: 15 keys of 3 digits x 2 parts x 32 QP rows, the 3 digits
     once, P*c0 (24 rows) once, 15 rotated QP pairs; giant_acc: 31 keys, their
@@ -64,6 +73,9 @@ def test_keyswitch_pass_rows():
     assert sum(rows.values()) * (1 << 16) * 8 == 621_281_280
     # the key product alone is the per-rotation figure of the key-switch roofline
     assert rows["key product"] * (1 << 16) * 8 == 178_782_208
+    # the fold step ct + Rotate(ct): its last pass also reads both parts of ct
+    folded = bench.keyswitch_pass_rows(22, 8, fold_add=True)
+    assert sum(folded.values()) == 1185 + 2 * 23
 
 
 def test_measured_step_traffic():
