@@ -242,8 +242,13 @@ Pool* g_pool = nullptr;
 // scheme is built on it (with that device current).
 // A failure is kept per device and reported by RotateInto, so that the rest
 // of the library works without the scratch array.
+// Calls on different streams are ordered on the array: `ev` is recorded on
+// the stream of the last call after its key switch, and a call on another
+// stream waits for it first (hipStreamWaitEvent allocates nothing).
 std::map<int, uint64_t*> g_scratch;
 std::map<int, std::string> g_scratch_err;
+struct ScratchUse { hipEvent_t ev = nullptr; hipStream_t last = nullptr; };
+std::map<int, ScratchUse> g_scratch_use;
 void init_scratch() {
   int dev = 0;
   HCHECK(hipGetDevice(&dev));
@@ -255,8 +260,14 @@ void init_scratch() {
     g_scratch_err[dev] = std::string("device scratch has no address: ") + hipGetErrorString(e);
     return;
   }
+  HCHECK(hipEventCreateWithFlags(&g_scratch_use[dev].ev, hipEventDisableTiming));
   g_scratch[dev] = static_cast<uint64_t*>(ptr);
   g_scratch_err.erase(dev);
+}
+ScratchUse& scratch_use() {
+  int dev = 0;
+  HCHECK(hipGetDevice(&dev));
+  return g_scratch_use.at(dev);
 }
 uint64_t* scratch_ptr() {
   int dev = 0;
@@ -1826,6 +1837,7 @@ int NewSchemeWithModuli(int logN, const uint64_t* q, int lenQ, const uint64_t* p
 int DeleteScheme(void) {
   return guard([&] {
     if (S) { delete S; S = nullptr; }
+    for (auto& kv : g_scratch_use) kv.second.last = nullptr;  // its streams are gone
     if (g_pool) g_pool->release_all();
     return 0;
   });
@@ -1967,8 +1979,9 @@ int RotateAdd(int ctID, int amount) {
 // RotateNew into an existing ciphertext with no allocation: the key switch's
 // temporaries live in the device scratch array, the automorphism tables and
 // basis-conversion tables were built with the key and the scheme.  The
-// rotation key must exist already.  Calls that overlap on one GPU (another
-// stream) race on the scratch array.
+// rotation key must exist already.  A call on the other stream of the
+// scheme waits for the previous call's key switch; calls from several host
+// threads or processes sharing the GPU race on the array.
 int RotateInto(int ctID, int amount, int outID) {
   return guard([&] {
     Scheme& s = sch();
@@ -1984,9 +1997,17 @@ int RotateInto(int ctID, int amount, int outID) {
                                        std::to_string(SCRATCH_WORDS * 8) + " bytes available");
     REQUIRE(o.d.n >= (size_t)2 * (c.level + 1) * s.N, "RotateInto: the output ciphertext is too small for the input's level");
     u64* ws = scratch_ptr();
-    // the buffer cache refuses to hand out memory until the key switch is queued
-    struct NoAlloc { NoAlloc() { g_pool->forbid++; } ~NoAlloc() { g_pool->forbid--; } } guard_alloc;
-    automorphism_core(c, s.gkeys.at(ge)->p, perm_inv_cached(ge), o.d.p, ws);
+    ScratchUse& use = scratch_use();
+    // the previous call's key switch, if queued on another stream, is done
+    // with the array before this one starts
+    if (use.last && use.last != s.st) HCHECK(hipStreamWaitEvent(s.st, use.ev, 0));
+    {
+      // the buffer cache refuses to hand out memory until the key switch is queued
+      struct NoAlloc { NoAlloc() { g_pool->forbid++; } ~NoAlloc() { g_pool->forbid--; } } guard_alloc;
+      automorphism_core(c, s.gkeys.at(ge)->p, perm_inv_cached(ge), o.d.p, ws);
+    }
+    HCHECK(hipEventRecord(use.ev, s.st));
+    use.last = s.st;
     o.level = c.level; o.scale = c.scale; o.logslots = c.logslots;
     return outID;
   });

@@ -57,8 +57,11 @@ int GeneratePublicKey(void);          /* keygenerator.go:22 */
 int GenerateRelinearizationKey(void); /* keygenerator.go:27-30 (evaluation key s^2 -> s) */
 int GenerateEvaluationKeys(void);     /* keygenerator.go:32 */
 /* Serialization for Orion's io_mode save/load (key_generator.py:17-31).  Byte
- * layout: Lattigo v6 WriteTo structure, little-endian u64 (see runtime.hip
- * "binary wire format"); results are released with FreeCArray. */
+ * layout: this library's own, modelled on the structure of Lattigo v6's
+ * WriteTo (row counts, lengths, then little-endian u64 words; see runtime.hip
+ * "binary wire format").  Byte equality with Lattigo's MarshalBinary is not
+ * established (no Lattigo here to compare with).  Results are released with
+ * FreeCArray. */
 ArrayResultByte SerializeSecretKey(void);                        /* keygenerator.go:38-47 */
 int LoadSecretKey(const unsigned char* data, unsigned long len); /* keygenerator.go:49-58 */
 
@@ -103,8 +106,10 @@ int RotateAdd(int ciphertextID, int amount);
  * the input's level), calling no hipMalloc / hipFree.  The key switch's
  * temporaries live in a static 96 MiB device array per GPU (a rotation at
  * N = 2^16 with up to 24 Q and 8 P limbs fits; larger levels are refused
- * with an error); the rotation key must already exist.  Calls that overlap
- * on one GPU (two streams) race on that array.  Returns outID. */
+ * with an error); the rotation key must already exist.  A call on the
+ * scheme's other stream waits for the previous call's key switch before it
+ * uses the array; calls from several host threads or processes on one GPU
+ * race on it.  Returns outID. */
 int RotateInto(int ciphertextID, int amount, int outID);
 int Conjugate(int ciphertextID);          /* evaluator.go:103-114 */
 int ConjugateNew(int ciphertextID);       /* evaluator.go:116-128 */
@@ -167,11 +172,13 @@ ArrayResultByte SerializeDiagonal(int transformID, int diagIdx);  /* lineartrans
 int LoadPlaintextDiagonal(const unsigned char* data, unsigned long len, int transformID,
                           unsigned long diagIdx);                 /* lineartransform.go:179-193 */
 int RemovePlaintextDiagonals(int transformID);                    /* lineartransform.go:195-201 */
-/* [ext] ciphertexts and plaintexts in the same wire layout (the field order of
- * Lattigo v6 rlwe.Element: scale bits, log2 slots, flags, then the vector of
- * ring.Poly in the NTT domain with standard representatives).  No counterpart
- * in the reference, whose backends never serialize them; they complete the
- * objects a Lattigo cross-check needs (inputs and expected outputs). */
+/* [ext] ciphertexts and plaintexts in this library's wire layout: a header of
+ * its own (scale as float64 bits, log2 slots, flags, count), then the vector
+ * of ring.Poly in the NTT domain with standard representatives.  The header
+ * is not Lattigo's MetaData encoding and byte parity with Lattigo is
+ * unpinned.  No counterpart in the reference, whose backends never serialize
+ * them; they carry the objects of a cross-check bundle (inputs and expected
+ * outputs) that a machine with Lattigo would convert. */
 ArrayResultByte SerializeCiphertext(int ciphertextID);
 int LoadCiphertext(const unsigned char* data, unsigned long len);   /* returns a new ciphertext id */
 ArrayResultByte SerializePlaintext(int plaintextID);
@@ -212,7 +219,10 @@ int GetSchemeInfo(int* out, int len);  /* logN, L, K, dnum, logScale, h */
 /* ---- [ext] device buffers from the library's allocator (for callers that have
  *      no HIP runtime of their own; one process should use one HIP runtime) ---- */
 void* DeviceAlloc(size_t bytes);                           /* NULL on failure */
-int DeviceFree(void* ptr);  /* -1 for a pointer freed twice or released by DeleteScheme */
+/* -1 for a pointer freed twice or released by DeleteScheme.  Pointers carry
+ * no owner: a stale pointer whose address a later DeviceAlloc returned again
+ * frees that newer buffer. */
+int DeviceFree(void* ptr);
 int CopyToDevice(void* dst, const void* src, size_t bytes);  /* synchronous */
 int CopyToHost(void* dst, const void* src, size_t bytes);    /* waits for the scheme stream first */
 

@@ -110,21 +110,3 @@ def test_device_buffer_double_free_refused(lib):
     assert a.ptr != b.ptr
     np.testing.assert_array_equal(a.download(), np.arange(8))
     a.free(); b.free()
-
-
-def test_device_buffer_after_delete_scheme_refused(hip_lib):
-    """DeleteScheme releases every device buffer, DeviceAlloc ones included:
-    freeing one afterwards is refused, even when a new scheme's allocation
-    reuses the address."""
-    q, p = make_params(11, [40, 30, 30, 30], [41, 41])
-    new_hip_scheme(hip_lib, 11, q, p, 30, 64, 9)
-    stale = hip_lib.device_empty((2, 1 << 11))
-    ptr = stale.ptr
-    hip_lib.DeleteScheme()
-    new_hip_scheme(hip_lib, 11, q, p, 30, 64, 9)
-    with pytest.raises(HipError, match="DeviceAlloc"):
-        hip_lib.DeviceFree(ptr)
-    ct = fresh(hip_lib)
-    dec = np.asarray(hip_lib.Decode(hip_lib.Decrypt(ct)))
-    np.testing.assert_allclose(dec[:16], np.linspace(-1, 1, 16), atol=1e-4)
-    hip_lib.DeleteScheme()

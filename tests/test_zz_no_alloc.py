@@ -46,6 +46,42 @@ def test_rotate_into_matches_rotate_new(hip_lib):
     lib.DeleteScheme()
 
 
+def test_rotate_into_two_streams(hip_lib):
+    """Calls on the scheme's two streams queued back to back: the second
+    waits for the first one's key switch before it uses the scratch array,
+    so both outputs are RotateNew's words."""
+    lib = hip_lib
+    logq, logp, logscale = [60] + [50] * 23, [61] * 8, 50
+    q, p = make_params(16, logq, logp)
+    print("[no-alloc] two streams, N=2^16, 24 Q + 8 P limbs", flush=True)
+    new_hip_scheme(lib, 16, q, p, logscale, 192, 47)
+    rng = np.random.default_rng(4)
+    k = 1 << 9
+    a = encrypt_at(lib, rng, 22, logscale, 0)
+    b = encrypt_at(lib, rng, 20, logscale, 1)
+    ref_a, ref_b = lib.RotateNew(a, k), lib.RotateNew(b, k)
+    out_a, out_b = lib.AddCiphertextNew(a, a), lib.AddCiphertextNew(a, a)
+    lib.Synchronize()
+    for rep in range(3):
+        lib.SetStream(0)
+        assert lib.RotateInto(a, k, out_a) == out_a
+        lib.SetStream(1)
+        assert lib.RotateInto(b, k, out_b) == out_b
+        lib.SetStream(0)
+        assert lib.RotateInto(b, k, out_a) == out_a
+        lib.JoinStream(1)
+        lib.Synchronize()
+        assert_equal_u64(lib.export_ciphertext(out_b), lib.export_ciphertext(ref_b), f"stream 1 RotateInto, round {rep}")
+        assert_equal_u64(lib.export_ciphertext(out_a), lib.export_ciphertext(ref_b), f"stream 0 RotateInto, round {rep}")
+        lib.SetStream(1)
+        assert lib.RotateInto(a, k, out_b) == out_b
+        lib.SetStream(0)
+        lib.JoinStream(1)
+        lib.Synchronize()
+        assert_equal_u64(lib.export_ciphertext(out_b), lib.export_ciphertext(ref_a), f"stream 1 RotateInto of a, round {rep}")
+    lib.DeleteScheme()
+
+
 def test_rotate_into_refuses_oversize(hip_lib):
     lib = hip_lib
     logq, logp, logscale = [60] + [50] * 29, [61] * 8, 50
