@@ -375,21 +375,33 @@ class DLRMWorkload:
         return self.clear_trace()[self.top_names[-1][1]]
 
     # ---- encrypted model ----
-    def setup(self):
-        s = self.scheme = oh.Scheme(self.params, self.backend)
+    def layer_specs(self):
+        """Every module of the network: (name, "linear", weight, bias, level,
+        last) or (name, "activation", coefficients)."""
         L = self.levels
-        mods = {}
+        specs = []
         for k, (w, b) in enumerate(self.bottom_w):
-            mods[f"bottom.{2 * k}"] = oh.LinearLayer(s, w, b, level=L[f"bottom.{2 * k}"], name=f"bottom.{2 * k}")
-            mods[f"bottom.{2 * k + 1}"] = oh.Activation(s, self.coeffs)
-        mods["bottom_to_top"] = oh.LinearLayer(s, self.bottom_to_top_w, level=L["bottom_to_top"], name="bottom_to_top")
-        mods["sparse"] = oh.LinearLayer(s, self.emb.matrix, level=L["sparse"], name="sparse")
-        mods["sparse_to_top"] = oh.LinearLayer(s, self.sparse_to_top_w, level=L["sparse_to_top"], name="sparse_to_top")
+            specs.append((f"bottom.{2 * k}", "linear", w, b, L[f"bottom.{2 * k}"], False))
+            specs.append((f"bottom.{2 * k + 1}", "activation", self.coeffs))
+        specs.append(("bottom_to_top", "linear", self.bottom_to_top_w, None, L["bottom_to_top"], False))
+        specs.append(("sparse", "linear", self.emb.matrix, None, L["sparse"], False))
+        specs.append(("sparse_to_top", "linear", self.sparse_to_top_w, None, L["sparse_to_top"], False))
         for k, (w, b) in enumerate(self.top_w):
             last = k == len(self.top_w) - 1
-            mods[f"top.{2 * k}"] = oh.LinearLayer(s, w, b, level=L[f"top.{2 * k}"], last=last, name=f"top.{2 * k}")
+            specs.append((f"top.{2 * k}", "linear", w, b, L[f"top.{2 * k}"], last))
             if not last:
-                mods[f"top.{2 * k + 1}"] = oh.Activation(s, self.coeffs)
+                specs.append((f"top.{2 * k + 1}", "activation", self.coeffs))
+        return specs
+
+    def setup(self):
+        s = self.scheme = oh.Scheme(self.params, self.backend)
+        mods = {}
+        for spec in self.layer_specs():
+            if spec[1] == "linear":
+                name, _, w, b, level, last = spec
+                mods[name] = oh.LinearLayer(s, w, b, level=level, last=last, name=name)
+            else:
+                mods[spec[0]] = oh.Activation(s, spec[2])
         for m in mods.values():
             m.compile()
         self.modules = mods

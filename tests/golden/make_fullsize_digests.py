@@ -12,9 +12,17 @@ For each: the input ciphertext (encryption index 0 at the top level), the
 first and last encoded diagonals, one giant-step Galois key, the linear
 transform output before the rescale, and the layer output after rescale,
 hybrid fold and the (zero) bias -- each as the hex SHA-256 of the
-little-endian u64 words of every row.  Run in the build container:
+little-endian u64 words of every row.
 
-    python tests/golden/make_fullsize_digests.py [threads]
+  dlrm      the encrypted HE-LRM forward (workload seed 3, key seed 17):
+            N=2^16, Q=[60,50x29], P=[61x8]; both inputs encrypted at the
+            input level (encryption indices 0 and 1), then every layer's
+            output ciphertext (10 Linears, 6 degree-3 activations, the Add),
+            and the relinearised product of the two inputs at that level.
+
+Run in the build container:
+
+    python tests/golden/make_fullsize_digests.py [threads] [case ...]
 """
 import hashlib
 import json
@@ -30,7 +38,9 @@ sys.path.insert(0, ROOT)
 
 from oracle import oracle as O  # noqa: E402
 from helrm_amd import orion_host as oh  # noqa: E402
-from helrm_amd.workloads import DenseLTWorkload, PCMMWorkload  # noqa: E402
+from helrm_amd.workloads import DenseLTWorkload, DLRMWorkload, PCMMWorkload  # noqa: E402
+sys.path.insert(0, os.path.dirname(HERE))
+from helpers import oracle_dlrm  # noqa: E402
 
 CASES = {
     "pcmm26": (PCMMWorkload, 3, 17),
@@ -87,10 +97,63 @@ def case_digests(name, cls, seed, key_seed, log=print):
         orc.close()
 
 
+class _Module:
+    """What oracle_dlrm reads of a compiled module, built on the host alone."""
+
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def dlrm_digests(seed=3, key_seed=17, log=print):
+    w = DLRMWorkload(None, "dlrm", seed=seed, key_seed=key_seed)
+    c = w.cfg
+    q, p = O.gen_primes(c["logn"], c["logq"], c["logp"])
+    slots = w.params.get_slots()
+    method = w.params.get_embedding_method()
+    for spec in w.layer_specs():
+        if spec[1] == "linear":
+            name, _, weight, bias, level, last = spec
+            weight = np.asarray(weight, np.float32)
+            d, rots = oh.diagonalize(weight, slots, method, last)
+            b = np.zeros(weight.shape[0], np.float32) if bias is None else np.asarray(bias, np.float32)
+            w.modules[name] = _Module(diagonals=d, output_rotations=rots, bias=b)
+        else:
+            w.modules[spec[0]] = _Module(coeffs=list(spec[2]))
+    orc = O.Oracle(c["logn"], q, p, h=c["h"], seed=key_seed)
+    try:
+        t0 = time.time()
+        (out, l, sc), trace = oracle_dlrm(orc, w, keep=True)
+        log(f"dlrm: forward done ({time.time() - t0:.0f} s)")
+        L = w.input_level
+        scale = float(1 << c["logscale"])
+        xd = orc.encrypt(orc.encode(np.asarray(w.dense, np.float32), L, scale), L, 0)
+        xs = orc.encrypt(orc.encode(np.asarray(w.emb.selector, np.float32), L, scale), L, 1)
+        prod = orc.mul_relin(xd, xs, L)
+        log(f"dlrm: relinearised product done ({time.time() - t0:.0f} s)")
+        logit = float(orc.decode_f64(orc.decrypt(out, l), l, sc)[0])
+        return {
+            "workload_seed": seed, "key_seed": key_seed, "q": [int(v) for v in q], "p": [int(v) for v in p],
+            "input_level": L, "logit": logit,
+            "ct_dense": row_digests(xd), "ct_sparse": row_digests(xs),
+            "mul_relin": {"level": L, "rows": row_digests(prod)},
+            "layers": {name: {"level": int(lv), "scale": float(s), "rows": row_digests(ct)}
+                       for name, (ct, lv, s) in trace.items()},
+        }
+    finally:
+        orc.close()
+
+
 def main():
     threads = int(sys.argv[1]) if len(sys.argv) > 1 else (os.cpu_count() or 1)
+    names = sys.argv[2:] or list(CASES) + ["dlrm"]
     O.set_threads(threads)
-    res = {name: case_digests(name, *spec, log=lambda m: print(m, flush=True)) for name, spec in CASES.items()}
+    log = lambda m: print(m, flush=True)  # noqa: E731
+    res = {}
+    if os.path.exists(OUT):
+        with open(OUT) as f:
+            res = json.load(f)
+    for name in names:
+        res[name] = dlrm_digests(log=log) if name == "dlrm" else case_digests(name, *CASES[name], log=log)
     with open(OUT, "w") as f:
         json.dump(res, f, indent=1)
     print(f"wrote {OUT}")

@@ -5,13 +5,17 @@ degree-3 activations, on a 30-limb chain without bootstrapping.
 * dlrm_n13: every layer's output ciphertext is bit-exact with the same flow
   on the CPU restatement (oracle/), which itself decrypts to the cleartext
   model.
-* dlrm (N=2^16): the decrypted logit is within 2^-20 of the float64 cleartext
-  forward on the same fp32 weights.
+* dlrm (N=2^16): every layer's output ciphertext, both inputs and a
+  relinearised product match the oracle's per-row SHA-256 digests
+  (tests/golden/make_fullsize_digests.py: the same flow on the CPU
+  restatement), with the transforms' rescale separate and fused; the
+  decrypted logit is within 2^-20 of the float64 cleartext forward on the
+  same fp32 weights.
 """
 import numpy as np
 import pytest
 
-from helpers import assert_equal_u64, oracle_dlrm
+from helpers import assert_equal_u64, assert_rows_match, fullsize_digests, oracle_dlrm
 from oracle import oracle as O
 from helrm_amd.workloads import DLRMWorkload
 
@@ -68,24 +72,51 @@ def test_dlrm_n13_bitexact_vs_oracle(hip_lib, prerescale):
     hip_lib.DeleteScheme()
 
 
-def test_dlrm_full_size_decrypts(hip_lib):
+def test_dlrm_full_size_bitexact(hip_lib):
+    d = fullsize_digests("dlrm")
     print("[dlrm] dlrm (N=2^16): building", flush=True)
-    w = DLRMWorkload(hip_lib, "dlrm", seed=3, key_seed=17).setup()
+    w = DLRMWorkload(hip_lib, "dlrm", seed=d["workload_seed"], key_seed=d["key_seed"]).setup()
     info = w.shape_info()
     print(f"[dlrm] dlrm: {info}", flush=True)
     assert info["bottom.0"]["diagonals"] == 512 and info["sparse"]["diagonals"] == 512
     assert info["top.4"]["output_rotations"] == 0
+    assert hip_lib.GetModuliChain() == d["q"] and hip_lib.GetAuxModuliChain() == d["p"]
+    assert w.input_level == d["input_level"]
+    assert_rows_match(hip_lib.export_ciphertext(w.ct_dense.ids[0]), d["ct_dense"], "dense input")
+    assert_rows_match(hip_lib.export_ciphertext(w.ct_sparse.ids[0]), d["ct_sparse"], "selector input")
+    # a relinearised product at the input level (evaluator.go:343-364)
+    prod = hip_lib.MulRelinCiphertextNew(w.ct_dense.ids[0], w.ct_sparse.ids[0])
+    assert hip_lib.GetCiphertextLevel(prod) == d["mul_relin"]["level"]
+    assert_rows_match(hip_lib.export_ciphertext(prod), d["mul_relin"]["rows"], "relinearised product")
+    hip_lib.DeleteCiphertext(prod)
+    for pre in (True, False):
+        hip_lib.set_lt_output_prerescaled(pre)
+        print(f"[dlrm] dlrm: layer by layer, prerescale={pre}", flush=True)
+        out, kept = w.run_stages(keep=True)
+        assert set(kept) == set(d["layers"])
+        for n, t in kept.items():
+            want = d["layers"][n]
+            cid = t.ids[0]
+            assert hip_lib.GetCiphertextLevel(cid) == want["level"], n
+            assert hip_lib.GetCiphertextScaleDouble(cid) == want["scale"], n
+            assert_rows_match(hip_lib.export_ciphertext(cid), want["rows"], f"{n} output (prerescale {pre})")
+        for t in kept.values():
+            t.free()
+    print(f"[dlrm] dlrm: {len(d['layers'])} layer outputs match the oracle", flush=True)
     assert w.concurrent  # run(): the lookup path on the second stream
-    first = w.run()
-    ref = hip_lib.export_ciphertext(first.ids[0])
-    first.free()
-    out = w.run()  # reuses the buffers both streams freed: the same words
-    assert_equal_u64(hip_lib.export_ciphertext(out.ids[0]), ref, "second concurrent forward")
+    hip_lib.set_lt_output_prerescaled(True)
+    final = d["layers"][w.top_names[-1][1]]
+    for rep in range(2):  # the second reuses the buffers both streams freed
+        out = w.run()
+        assert_rows_match(hip_lib.export_ciphertext(out.ids[0]), final["rows"], f"concurrent forward {rep}")
+        if rep == 0:
+            out.free()
     assert hip_lib.GetCiphertextLevel(out.ids[0]) == 0
     y = w.decrypt_output(out)
     err = np.abs(y - w.expected).max()
     print(f"[dlrm] dlrm: logit {y[0]:.9f} vs {w.expected[0]:.9f} (|err| {err:.3e})", flush=True)
     assert err < TOL
+    assert abs(float(y[0]) - d["logit"]) < TOL
     # the square-packed last layer leaves no partial sums in the other slots
     full = np.asarray(w.scheme.decode(w.scheme.decrypt(out.__class__(w.scheme, out.ids, 4096))))
     assert np.abs(full[1:]).max() < TOL
