@@ -365,6 +365,21 @@ void launch_moddown_combine(u64* out, size_t o_bstride, const u64* x, size_t x_b
                      e_bstride, add, a_bstride, add_batches, perm, pinv, pinvp, mods, N);
 }
 
+// The counter PRNG of the key generator (see rand64 below).
+__device__ __forceinline__ u64 mix64(u64 z) {
+  z ^= z >> 30; z *= 0xbf58476d1ce4e5b9ULL;
+  z ^= z >> 27; z *= 0x94d049bb133111ebULL;
+  z ^= z >> 31; return z;
+}
+// Word (modulus index m, position x) of the a half of digit d of an
+// evaluation key this library generated: a is sampled uniformly in the NTT
+// domain, a[m][x] = floor(rand64(seed, stream_d, m*N + x) * q / 2^64), and
+// kd = mix64(seed + G*(stream_d + 1)) is rand64's per-stream key, so the word
+// is regenerated here instead of read (plain, not Montgomery form).
+__device__ __forceinline__ u64 key_a_word(u64 kd, u64 ctr, u64 q) {
+  return __umul64hi(mix64(kd ^ (ctr * 0xd1b54a32d192ed03ULL + 0x8cb92ba72f3d8dd7ULL)), q);
+}
+
 // ---------------------------------------------------------------------------
 // Key inner product (gadget product) in QP, fused with the automorphism
 // gather.  For output position i the thread reads every operand at
@@ -373,6 +388,9 @@ void launch_moddown_combine(u64* out, size_t o_bstride, const u64* x, size_t x_b
 //   mode 0: out = (sum_d dg_d*k0_d, sum_d dg_d*k1_d)                 (no perm)
 //   mode 1: out = perm(sum dg*k0 + add0[Q rows], sum dg*k1)         (hoisted)
 // Keys are in Montgomery form; the sum is accumulated lazily in 128 bits.
+// With a.seeded the a halves (k1) are regenerated (key_a_word) instead of
+// read: their products carry no factor R, so part 1 is multiplied by R
+// after its REDC.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void keymac_kernel(KeyMacArgs a) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -391,11 +409,12 @@ __global__ __launch_bounds__(256) void keymac_kernel(KeyMacArgs a) {
   const size_t kstride = (size_t)(a.L + a.K) * N;
   Acc128 A0, A1;
   acc_zero(A0); acc_zero(A1);
+  const bool seeded = a.seeded && !a.key;
   for (int d = 0; d < a.dn; d++) {
     const u64 x = d == own_d ? own[src] : dg[((size_t)d * a.nqp + k) * N + src];
     const u64* kb = key + (size_t)d * 2 * kstride + (size_t)kl * N + src;
     acc_mac(A0, x, __builtin_nontemporal_load(&kb[0]));
-    acc_mac(A1, x, __builtin_nontemporal_load(&kb[kstride]));
+    acc_mac(A1, x, seeded ? key_a_word(a.ka[d], (u64)kl * N + src, mc.q) : __builtin_nontemporal_load(&kb[kstride]));
   }
   u64 lo0, hi0, lo1, hi1;
   acc_value(A0, lo0, hi0);
@@ -406,7 +425,8 @@ __global__ __launch_bounds__(256) void keymac_kernel(KeyMacArgs a) {
   if (a.add0 && k <= a.l) hi0 = add_mod(hi0, a.add0[(size_t)k * N + src], mc.q);
   const size_t o = (size_t)b * a.out_bstride + (size_t)k * N + i;
   a.out0[o] = redc(lo0, hi0, mc.q, mc.qinv);
-  a.out1[o] = redc(lo1, hi1, mc.q, mc.qinv);
+  const u64 r1 = redc(lo1, hi1, mc.q, mc.qinv);
+  a.out1[o] = seeded ? mont_mul(r1, mc.r2, mc.q, mc.qinv) : r1;
 }
 void launch_keymac(const KeyMacArgs& a, int batch, hipStream_t st) {
   if (batch <= 0) return;
@@ -453,11 +473,12 @@ __global__ __launch_bounds__(256) void giant_acc_kernel(GiantAccArgs a) {
     const int src = (int)perm[i];
     const u64* dg = a.digits + (size_t)g * a.dig_bstride;
     const u64* own = a.own ? a.own + (size_t)g * a.own_bstride + (size_t)k * N : nullptr;
+    const u64* ka = a.ka ? a.ka + (size_t)g * a.dn : nullptr;
     for (int d = 0; d < a.dn; d++) {
       const u64 x = d == own_d ? own[src] : dg[((size_t)d * a.nqp + k) * N + src];
       const u64* kb = key + (size_t)d * 2 * kstride + (size_t)kl * N + src;
       acc_mac(A0, x, __builtin_nontemporal_load(&kb[0]));
-      acc_mac(A1, x, __builtin_nontemporal_load(&kb[kstride]));
+      acc_mac(A1, x, ka ? key_a_word(ka[d], (u64)kl * N + src, mc.q) : __builtin_nontemporal_load(&kb[kstride]));
     }
     cnt += a.dn;
     const u64* T0 = a.T + (size_t)a.tg[g] * a.T_gstride;
@@ -467,14 +488,20 @@ __global__ __launch_bounds__(256) void giant_acc_kernel(GiantAccArgs a) {
   acc_flush(A1, tlo1, thi1, mc.q);
   // T0 terms enter the high word (v*2^64 == v*R mod q)
   thi0 = add_mod(thi0, t0, mc.q);
+  u64 tz1 = 0;
   if (a.t_zero >= 0) {
     const u64* Tz = a.T + (size_t)a.t_zero * a.T_gstride;
     thi0 = add_mod(thi0, Tz[(size_t)k * N + i], mc.q);
-    thi1 = add_mod(thi1, Tz[a.T_pstride + (size_t)k * N + i], mc.q);
+    tz1 = Tz[a.T_pstride + (size_t)k * N + i];
   }
   const size_t o = (size_t)k * N + i;
   a.out0[o] = redc(tlo0, thi0, mc.q, mc.qinv);
-  a.out1[o] = redc(tlo1, thi1, mc.q, mc.qinv);
+  if (a.ka) {
+    // regenerated a halves: the products' REDC lacks the factor R
+    a.out1[o] = add_mod(mont_mul(redc(tlo1, thi1, mc.q, mc.qinv), mc.r2, mc.q, mc.qinv), tz1, mc.q);
+  } else {
+    a.out1[o] = redc(tlo1, add_mod(thi1, tz1, mc.q), mc.q, mc.qinv);
+  }
 }
 void launch_giant_acc(const GiantAccArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(giant_acc_kernel, dim3(a.N / 256, a.nqp, 1), dim3(256), 0, st, a);
@@ -556,6 +583,7 @@ __device__ __forceinline__ void baby_rotation_at(const DiagMacArgs& a, int slot,
   const int N = a.N;
   const int src = (int)a.bperm[slot][x];
   const u64* key = a.bkey[slot];
+  const u64* ka = a.bka ? a.bka + (size_t)slot * a.dn : nullptr;
   const int own_d = k <= a.l ? k / a.K : -1;
   const size_t kstride = (size_t)(a.L + a.K) * N;
   Acc128 A0, A1;
@@ -564,7 +592,7 @@ __device__ __forceinline__ void baby_rotation_at(const DiagMacArgs& a, int slot,
     const u64 v = d == own_d ? a.own[(size_t)k * N + src] : a.digits[((size_t)d * a.nqp + k) * N + src];
     const u64* kb = key + (size_t)d * 2 * kstride + (size_t)kl * N + src;
     acc_mac(A0, v, __builtin_nontemporal_load(&kb[0]));
-    acc_mac(A1, v, __builtin_nontemporal_load(&kb[kstride]));
+    acc_mac(A1, v, ka ? key_a_word(ka[d], (u64)kl * N + src, mc.q) : __builtin_nontemporal_load(&kb[kstride]));
   }
   u64 lo0, hi0, lo1, hi1;
   acc_value(A0, lo0, hi0);
@@ -574,6 +602,7 @@ __device__ __forceinline__ void baby_rotation_at(const DiagMacArgs& a, int slot,
   if (k <= a.l) hi0 = add_mod(hi0, a.pc[(size_t)k * N + src], mc.q);
   r0 = redc(lo0, hi0, mc.q, mc.qinv);
   r1 = redc(lo1, hi1, mc.q, mc.qinv);
+  if (ka) r1 = mont_mul(r1, mc.r2, mc.q, mc.qinv);  // regenerated a halves carry no R
 }
 
 template <int NB, bool DENSE, bool ACC>
@@ -724,11 +753,6 @@ void launch_moddown_rescale_spread(u64* ext, size_t e_bstride, const u64* xl, si
 // Sampling (counter PRNG shared with the key/encryption specification):
 //   rand64(seed, stream, ctr) = mix(mix(seed + G*(stream+1)) ^ (ctr*M1 + M2))
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ u64 mix64(u64 z) {
-  z ^= z >> 30; z *= 0xbf58476d1ce4e5b9ULL;
-  z ^= z >> 27; z *= 0x94d049bb133111ebULL;
-  z ^= z >> 31; return z;
-}
 __device__ __forceinline__ u64 rand64(u64 seed, u64 stream, u64 ctr) {
   u64 k = mix64(seed + 0x9e3779b97f4a7c15ULL * (stream + 1));
   return mix64(k ^ (ctr * 0xd1b54a32d192ed03ULL + 0x8cb92ba72f3d8dd7ULL));

@@ -319,6 +319,7 @@ struct LinTrans {
   double scale = 0;
   // device arrays of key / permutation pointers (baby and giant rotations), built on first use
   DevArray<const u64*> d_bkey, d_gkey; DevArray<const uint32_t*> d_bperm, d_gperm; DevArray<int> d_tg;
+  DevArray<u64> d_bka, d_gka;  // [key][dnum] stream keys of the keys' a halves (used when every key was generated here)
   bool ptrs_ready = false;
 };
 
@@ -353,6 +354,11 @@ struct Scheme {
   std::map<std::pair<int, int>, std::unique_ptr<BConvHost>> bconv;
   std::map<u64, DevArray<uint32_t>> perms, perm_invs;
   std::map<std::tuple<int, int, size_t>, std::unique_ptr<struct DigitRows>> digit_rows;
+  // Galois keys this library generated (a halves a function of the seed, the
+  // key's stream and the word's position, regenerated by the kernels); a
+  // loaded key is read whole
+  std::set<u64> seeded_gk;
+  bool rlk_seeded = false;
   // keys
   bool has_sk = false, has_pk = false;
   std::vector<int8_t> s;
@@ -697,8 +703,10 @@ std::unique_ptr<DU64> gen_eval_key(const u64* s_inR, const u64* s_outR, FA st_a,
   for (int d = 0; d < s.dnum; d++) {
     u64* b = key->p + (size_t)d * 2 * nm * N;
     u64* a = b + (size_t)nm * N;
+    // a is sampled uniformly in the NTT domain (a uniform polynomial is
+    // uniform in either domain; Lattigo's key generator samples it there too),
+    // so any word of it is a function of (seed, stream, modulus, position)
     launch_sample_uniform(a, rows_all(), s.seed, st_a(d), s.d_mods.p, N, s.st);
-    ntt(a, 0, 1, rows_all(), true);
     launch_sample_cbd(b, rows_all(), s.seed, st_e(d), s.d_mods.p, N, false, s.st);
     ntt(b, 0, 1, rows_all(), true);
     launch_gk_combine(b, a, s_outR, s_inR, d * K, std::min((d + 1) * K, s.L), s.pmod_plain.p, nm, s.d_mods.p, N, s.st);
@@ -724,6 +732,7 @@ void ensure_galois_key(u64 galel) {
   launch_mont_convert(soR.p, 0, 1, rows_all(), s.d_mods.p, N, true, s.st);
   s.gkeys[galel] = gen_eval_key(s.sR.p, soR.p, [galel](int d) { return ST_GK_A(galel, (u64)d); },
                                  [galel](int d) { return ST_GK_E(galel, (u64)d); });
+  s.seeded_gk.insert(galel);
   perm_for(galel); perm_inv_for(galel);
   // transforms cache key addresses: a key created after a removal lives elsewhere
   for (auto& kv : s.lts) kv.second->ptrs_ready = false;
@@ -739,7 +748,12 @@ void ensure_relin_key() {
   DU64 s2R((size_t)nm * N);  // s^2 in Montgomery form: mont_mul(sR, sR) = s^2 R
   launch_mont_mul(s2R.p, 0, s.sR.p, 0, s.sR.p, 0, 1, rows_all(), s.d_mods.p, N, false, s.st);
   s.rlk = gen_eval_key(s2R.p, s.sR.p, [](int d) { return ST_RLK_A((u64)d); }, [](int d) { return ST_RLK_E((u64)d); });
+  s.rlk_seeded = true;
 }
+// rand64's per-stream key: the kernels regenerate word (m, x) of a key's a
+// half of digit d as floor(mix64(kd ^ (ctr*M1 + M2)) * q / 2^64), ctr = m*N + x
+u64 stream_key(u64 stream) { return mix64(sch().seed + 0x9e3779b97f4a7c15ULL * (stream + 1)); }
+
 
 // ============================================================================
 // encoder: root and rotation-group tables (Lattigo ckks.Encoder); the special
@@ -1066,7 +1080,7 @@ size_t automorphism_ws_words(int l) {
   return (std::max(dn * nqp, 2 * K + 2 * (size_t)(l + 1)) + 2 * nqp + (size_t)(l + 1)) * N;
 }
 // acc: nullptr, or a ciphertext at ct's level (not out) added to the result
-void automorphism_core(const Cipher& ct, const u64* key, const uint32_t* perm_inv, u64* out, u64* ws,
+void automorphism_core(const Cipher& ct, u64 galel, const u64* key, const uint32_t* perm_inv, u64* out, u64* ws,
                        const u64* acc = nullptr) {
   Scheme& s = sch();
   const int l = ct.level, N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
@@ -1088,13 +1102,17 @@ void automorphism_core(const Cipher& ct, const u64* key, const uint32_t* perm_in
   a.own = ct.d.p + (size_t)(l + 1) * N; a.own_bstride = 0;
   a.out0 = dd; a.out1 = dd + (size_t)nqp * N; a.out_bstride = 0; a.mods = s.d_mods.p;
   a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
+  if (s.seeded_gk.count(galel)) {
+    a.seeded = 1;
+    for (int d = 0; d < dn; d++) a.ka[d] = stream_key(ST_GK_A(galel, (u64)d));
+  }
   launch_keymac(a, 1, s.st);
   mod_down(l, dd, (size_t)nqp * N, 2, out, (size_t)(l + 1) * N, ct.d.p, 0, 1, perm_inv, md, acc);
 }
 std::unique_ptr<Cipher> automorphism(const Cipher& ct, u64 galel, bool lt_keyset) {
   const u64* key = key_ptr(galel, lt_keyset);
   auto out = new_ct(ct.level, ct.scale); out->logslots = ct.logslots;
-  timed("rotate", [&] { automorphism_core(ct, key, perm_inv_for(galel), out->d.p, nullptr); });
+  timed("rotate", [&] { automorphism_core(ct, galel, key, perm_inv_for(galel), out->d.p, nullptr); });
   return out;
 }
 // ---- plaintext, scalar and ciphertext products (Lattigo ckks Evaluator
@@ -1190,6 +1208,10 @@ std::unique_ptr<Cipher> mul_relin_ct(const Cipher& a, const Cipher& b) {
   k.own = d2.p; k.own_bstride = 0;
   k.out0 = dd.p; k.out1 = dd.p + (size_t)nqp * N; k.out_bstride = 0; k.mods = s.d_mods.p;
   k.N = N; k.l = l; k.L = s.L; k.K = K; k.nqp = nqp; k.dn = dn;
+  if (s.rlk_seeded) {
+    k.seeded = 1;
+    for (int d = 0; d < dn; d++) k.ka[d] = stream_key(ST_RLK_A((u64)d));
+  }
   launch_keymac(k, 1, s.st);
   // out = ModDown(dd) + (d0, d1): the epilogue reads and writes each word in one thread
   mod_down(l, dd.p, (size_t)nqp * N, 2, out->d.p, ps, out->d.p, ps, 2, nullptr);
@@ -1464,9 +1486,22 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct, bool r
       tm.d_tg = DevArray<int>(std::max(ngk, 1));
       if (nbr) { upload(tm.d_bkey.p, bk.data(), nbr); upload(tm.d_bperm.p, bp.data(), nbr); }
       if (ngk) { upload(tm.d_gkey.p, gk.data(), ngk); upload(tm.d_gperm.p, gp.data(), ngk); upload(tm.d_tg.p, tg.data(), ngk); }
+      // the stream keys depend on the Galois element alone
+      std::vector<u64> bka((size_t)std::max(nbr, 1) * dn), gka((size_t)std::max(ngk, 1) * dn);
+      for (int i = 0; i < nbr; i++)
+        for (int d = 0; d < dn; d++) bka[(size_t)i * dn + d] = stream_key(ST_GK_A(galois_element(babies[i]), (u64)d));
+      for (int g = 0; g < ngk; g++)
+        for (int d = 0; d < dn; d++) gka[(size_t)g * dn + d] = stream_key(ST_GK_A(galois_element(t.giant[gs + g]), (u64)d));
+      tm.d_bka = DevArray<u64>(bka.size()); upload(tm.d_bka.p, bka.data(), bka.size());
+      tm.d_gka = DevArray<u64>(gka.size()); upload(tm.d_gka.p, gka.data(), gka.size());
       tm.ptrs_ready = true;
     }
   }
+  // the a halves are regenerated in the kernels when every key of the group
+  // of launches was generated here (a loaded key is read whole)
+  bool babies_seeded = true, giants_seeded = true;
+  for (int i = 0; i < nbr; i++) babies_seeded = babies_seeded && s.seeded_gk.count(galois_element(babies[i]));
+  for (int g = 0; g < ngk; g++) giants_seeded = giants_seeded && s.seeded_gk.count(galois_element(t.giant[gs + g]));
   // 2. the hoisted baby rotations (sigma(d0 + P c0), sigma(d1)) are computed by
   // the diagonal MAC in its prologue (keymac_kernel's arithmetic per word), so
   // they never go through memory
@@ -1475,6 +1510,7 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct, bool r
   DiagMacArgs dm{};
   dm.diag = t.diags.p; dm.diag_stride = (size_t)(t.level + 1 + K) * N;
   dm.digits = digits.p; dm.bkey = t.d_bkey.p; dm.bperm = t.d_bperm.p; dm.own = c1; dm.dn = dn;
+  dm.bka = babies_seeded ? t.d_bka.p : nullptr;
   dm.pc = pc.p; dm.pc_pstride = (size_t)(l + 1) * N;
   dm.baby_is_zero = t.d_bzero.p; dm.baby_slot = t.d_bslot.p; dm.gpi = t.d_gpi.p; dm.dense = t.dense ? 1 : 0;
   dm.zero_pidx = (int)t.plain_idx.size();
@@ -1500,6 +1536,7 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct, bool r
     a.T = T.p; a.T_gstride = 2 * qp; a.T_pstride = qp; a.t_zero = gs ? 0 : -1;
     a.out0 = acc.p; a.out1 = acc.p + qp; a.mods = s.d_mods.p;
     a.N = N; a.l = l; a.L = s.L; a.K = K; a.nqp = nqp; a.dn = dn;
+    a.ka = giants_seeded ? t.d_gka.p : nullptr;
     timed("giant_acc", [&] { launch_giant_acc(a, s.st); });
   } else {
     d2d(acc.p, T.p, 2 * qp * 8);
@@ -1971,7 +2008,7 @@ int RotateAdd(int ctID, int amount) {
     Cipher& ct = get_ct(ctID);
     const u64* key = key_ptr(ge, false);
     auto out = new_ct(ct.level, ct.scale);
-    timed("rotate", [&] { automorphism_core(ct, key, perm_inv_for(ge), out->d.p, nullptr, ct.d.p); });
+    timed("rotate", [&] { automorphism_core(ct, ge, key, perm_inv_for(ge), out->d.p, nullptr, ct.d.p); });
     std::swap(ct.d, out->d);
     return ctID;
   });
@@ -2004,7 +2041,7 @@ int RotateInto(int ctID, int amount, int outID) {
     {
       // the buffer cache refuses to hand out memory until the key switch is queued
       struct NoAlloc { NoAlloc() { g_pool->forbid++; } ~NoAlloc() { g_pool->forbid--; } } guard_alloc;
-      automorphism_core(c, s.gkeys.at(ge)->p, perm_inv_cached(ge), o.d.p, ws);
+      automorphism_core(c, ge, s.gkeys.at(ge)->p, perm_inv_cached(ge), o.d.p, ws);
     }
     HCHECK(hipEventRecord(use.ev, s.st));
     use.last = s.st;
@@ -2197,7 +2234,7 @@ int LoadSecretKey(const unsigned char* data, unsigned long len) {
     sync();
     s.s = sv; s.sR = std::move(sR); s.has_sk = true;
     // keys derived from a previous secret are stale
-    s.gkeys.clear(); s.rlk.reset();
+    s.gkeys.clear(); s.rlk.reset(); s.seeded_gk.clear(); s.rlk_seeded = false;
     for (auto& kv : s.lts) kv.second->ptrs_ready = false;
     return 0;
   });
@@ -2234,6 +2271,7 @@ int LoadRotationKey(const unsigned char* data, unsigned long len, unsigned long 
     auto k = std::make_unique<DU64>(h.size());
     upload(k->p, h.data(), h.size());
     s.gkeys[(u64)galEl] = std::move(k);
+    s.seeded_gk.erase((u64)galEl);  // its a halves are read, not regenerated
     perm_for((u64)galEl); perm_inv_for((u64)galEl);
     s.lt_keys.insert((u64)galEl);
     // transforms cache key pointers: rebuild them on next use

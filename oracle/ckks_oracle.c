@@ -755,7 +755,9 @@ void orc_public_key(const orc_ctx* c, uint64_t* out) { memcpy(out, c->pk, 8 * (s
  * (Lattigo KeyGenerator.GenGaloisKey: encrypts s under pi_{k^-1}(s)). */
 /* Evaluation key from s_in to s_out (both NTT over QP): dnum digits of
  * (b_d, a_d), b_d = -a_d*s_out + e_d + [P*s_in on the limbs of digit d]
- * (Lattigo KeyGenerator.GenEvaluationKey). */
+ * (Lattigo KeyGenerator.GenEvaluationKey).  a_d is sampled uniformly in the
+ * NTT domain, as Lattigo samples it (a uniform polynomial is uniform in
+ * either domain), word (m, x) = uniform_mod(rand64(seed, stream, m*N + x)). */
 static u64* gen_eval_key(orc_ctx* c, const u64* s_in_ntt, const u64* s_out_ntt, u64 (*st_a)(u64, u64),
                          u64 (*st_e)(u64, u64), u64 tag) {
     int N = c->N, nm = c->L + c->K, K = c->K; int mi[MAXMOD]; full_qp_list(c, mi);
@@ -763,7 +765,7 @@ static u64* gen_eval_key(orc_ctx* c, const u64* s_in_ntt, const u64* s_out_ntt, 
     i64* e = (i64*)xmalloc(sizeof(i64) * N);
     for (int d = 0; d < c->dnum; d++) {
         u64* b = key + (size_t)d * 2 * nm * N; u64* a = b + (size_t)nm * N;
-        sample_uniform_qp(c, st_a(tag, (u64)d), mi, nm, a); ntt_limbs(c, a, mi, nm);
+        sample_uniform_qp(c, st_a(tag, (u64)d), mi, nm, a);
         sample_cbd(c->seed, st_e(tag, (u64)d), N, e);
         poly_from_signed(c, e, mi, nm, b); ntt_limbs(c, b, mi, nm);
         #pragma omp parallel for num_threads(g_threads) schedule(static) if (g_threads > 1)
