@@ -33,29 +33,36 @@ def mac_unit_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, w=8):
     return (D + 2 * n1 + 2 * n2) * (L + K) * N * w
 
 
-def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=8, chunks=1, fused_babies=True):
+# Parts of each key-switching key read from HBM: the library samples the a
+# half of every key it generates from a seed and regenerates it inside the
+# key product, so only the b half is read (2 for keys loaded whole)
+KEY_PARTS = 1
+
+
+def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=8, chunks=1, fused_babies=True,
+                      key_parts=KEY_PARTS):
     """Per-PCMM and per-diag-MAC-launch algorithmic HBM bytes (every word once).
 
-    PCMM: the diagonals, each of the R rotation keys, the input and the output
-    ciphertext.  Diagonal MAC launch, counted as this kernel works (the giant
+    PCMM: the diagonals, the read parts of each of the R rotation keys, the
+    input and the output ciphertext.  Diagonal MAC launch, counted as this kernel works (the giant
     groups split evenly over `chunks` launches): its share of the diagonals
     and P*c (2 Q polys, baby step 0) read, one QP accumulator pair per giant
     group of the launch written, and the n1-1 hoisted baby rotations --
-    computed in the kernel's prologue from their keys (dnum*2 QP polys each)
+    computed in the kernel's prologue from their keys (dnum*key_parts QP polys each)
     and the decomposed input (dnum QP polys, once) when fused_babies, else
     read (2 QP polys each).  mac_unit_bytes is the per-unit definition the
     roofline is quoted on."""
     R = (n1 - 1) + (n2 - 1) + f
-    pcmm = D * (L + K) * N * w + R * dnum * 2 * (L + K) * N * w + 2 * L * N * w + 2 * (L - 1) * N * w
+    pcmm = D * (L + K) * N * w + R * dnum * key_parts * (L + K) * N * w + 2 * L * N * w + 2 * (L - 1) * N * w
     if fused_babies:
-        babies = (n1 - 1) * dnum * 2 * (L + K) * N * w + (dnum * (L + K) * N * w if n1 > 1 else 0)
+        babies = (n1 - 1) * dnum * key_parts * (L + K) * N * w + (dnum * (L + K) * N * w if n1 > 1 else 0)
     else:
         babies = (n1 - 1) * 2 * (L + K) * N * w
     diag_mac = (D * (L + K) * N * w + n2 * 2 * (L + K) * N * w) // chunks + babies + 2 * L * N * w
     return pcmm, diag_mac
 
 
-def keyswitch_pass_rows(level, K, fold_add=False):
+def keyswitch_pass_rows(level, K, fold_add=False, key_parts=KEY_PARTS):
     """Rows of N words that one single key switch at `level` moves, pass by
     pass (a transform is 2 passes, each reading and writing its limb);
     fold_add: the fold step ct + Rotate(ct) (RotateAdd), whose last pass also
@@ -68,7 +75,7 @@ def keyswitch_pass_rows(level, K, fold_add=False):
         "inverse NTT of c1": 4 * ql,
         "extension of the digits": ql + ext,
         "forward NTT of the extended rows": 4 * ext,
-        "key product": (dn * 2 + dn + 2) * nqp,
+        "key product": (dn * key_parts + dn + 2) * nqp,
         "inverse NTT of the P rows, both parts": 4 * 2 * K,
         "extension P -> Q, both parts": 2 * K + 2 * ql,
         "forward NTT with the ModDown epilogue": 2 * 2 * ql + (2 * ql + 2 * ql + ql + 2 * ql),
@@ -234,7 +241,7 @@ def cpu_baseline_dlrm(q, p, w, threads):
         orc.close()
 
 
-def keyswitch_bytes(N, Lq, K, nb, ng, w=8):
+def keyswitch_bytes(N, Lq, K, nb, ng, w=8, key_parts=KEY_PARTS):
     """Algorithmic bytes of one launch of the BSGS key-switch kernels of a
     Linear with Lq active Q limbs: keymac_baby (the nb-1 hoisted baby
     rotations: their keys, the decomposed input once, P*c0 once, the rotated
@@ -242,8 +249,8 @@ def keyswitch_bytes(N, Lq, K, nb, ng, w=8):
     c1 parts and c0 accumulators read, one QP pair written)."""
     nqp, dn = Lq + K, (Lq + K - 1) // K
     nbr, ngk = max(nb - 1, 0), max(ng - 1, 0)
-    baby = nbr * dn * 2 * nqp * N * w + dn * nqp * N * w + Lq * N * w + nbr * 2 * nqp * N * w
-    giant = ngk * (dn * 2 + dn + 1) * nqp * N * w + 2 * nqp * N * w
+    baby = nbr * dn * key_parts * nqp * N * w + dn * nqp * N * w + Lq * N * w + nbr * 2 * nqp * N * w
+    giant = ngk * (dn * key_parts + dn + 1) * nqp * N * w + 2 * nqp * N * w
     return baby, giant
 
 
@@ -554,7 +561,7 @@ def main():
         # each degree-3 activation reads the relinearisation key twice at its level
         for name, _ in w.activations():
             lq = w.levels[name] + 1
-            step_bytes += 2 * ((lq + K - 1) // K) * 2 * (lq + K) * N * 8
+            step_bytes += 2 * ((lq + K - 1) // K) * KEY_PARTS * (lq + K) * N * 8
     # algorithmic bytes per diagonal-MAC launch over one step: the per-unit
     # definition (diagonals + 2*n1 baby-step + 2*n2 giant-step QP polynomials)
     # is the roofline; the kernel's own count (it computes the baby rotations
@@ -573,8 +580,9 @@ def main():
                 "definition": "D*(L+K)*N*w diagonals + 2*n1*(L+K)*N*w + 2*n2*(L+K)*N*w baby- and giant-step QP polynomials",
                 "kernel_count": {"algorithmic_bytes_per_launch": mac_per_launch, "achieved": achieved_k,
                                  "frac": (achieved_k / HBM_PEAK_GBS) if achieved_k else None,
-                                 "definition": ("diagonals, the hoisted baby rotations' keys and the decomposed input "
-                                                "(the rotations computed in the prologue), P*c, one QP accumulator "
+                                 "definition": ("diagonals, the b halves of the hoisted baby rotations' keys (the a halves "
+                                                "regenerated from their seed) and the decomposed input (the "
+                                                "rotations computed in the prologue), P*c, one QP accumulator "
                                                 "pair per giant group")}}
     lti = lib.lt_info(list(layers[0].transform_ids.values())[0])
     # the key-switch kernels of the transforms against the same peak
@@ -594,11 +602,11 @@ def main():
     # the single-ciphertext key switch: the fold's rotations (one key switch
     # each at the transform's output level, the fold's add inside its last
     # pass) against the per-rotation bytes
-    # key dnum*2*(l+1+K)*N*w + digits dnum*(l+1+K)*N*w + output 2*(l+1+K)*N*w
+    # key dnum*KEY_PARTS*(l+1+K)*N*w + digits dnum*(l+1+K)*N*w + output 2*(l+1+K)*N*w
     if kt["rotate"]["launches"] and len(layers) == 1:
         lf = layers[0].level - 1  # the fold runs on the rescaled transform output
         nqp, dn = lf + 1 + K, (lf + 1 + K - 1) // K
-        rb = (dn * 2 + dn + 2) * nqp * N * 8
+        rb = (dn * KEY_PARTS + dn + 2) * nqp * N * 8
         r_ms = kt["rotate"]["avg_ms"]
         pb = sum(keyswitch_pass_rows(lf, K, fold_add=True).values()) * N * 8
         kernel_rooflines["keyswitch_rotation"] = {

@@ -20,16 +20,22 @@ def test_more_than_one_gpu_is_refused():
 
 def test_pcmm26_algorithmic_bytes():
     """N=2^16, L=24, K=8, D=512, 16 baby x 32 giant steps, 6 fold rotations,
-    dnum=3: diagonals + 52 rotation keys + input + output ciphertexts, and the
-    diagonal-MAC launch: diagonals, the keys of the 15 hoisted baby rotations
-    and the 3 decomposed digits (the rotations are computed in its prologue),
-    P*c, 32 QP accumulator pairs; with the rotations read instead, 15 rotated
-    QP pairs take the place of keys and digits."""
+    dnum=3: diagonals + the b halves of 52 rotation keys (the a halves are
+    regenerated from their seed) + input + output ciphertexts, and the
+    diagonal-MAC launch: diagonals, the key halves of the 15 hoisted baby
+    rotations and the 3 decomposed digits (the rotations are computed in its
+    prologue), P*c, 32 QP accumulator pairs; with the rotations read instead,
+    15 rotated QP pairs take the place of keys and digits."""
     pcmm, mac = bench.algorithmic_bytes()
-    assert pcmm == 13_873_709_056
-    assert mac == 11_249_123_328
+    assert pcmm == 11_256_463_360
+    assert mac == 10_494_148_608
     N, w, nqp = 1 << 16, 8, 32
-    assert mac == (512 * nqp + 15 * 3 * 2 * nqp + 3 * nqp + 32 * 2 * nqp) * N * w + 2 * 24 * N * w
+    assert pcmm == (512 * nqp + 52 * 3 * nqp) * N * w + 2 * 24 * N * w + 2 * 23 * N * w
+    assert mac == (512 * nqp + 15 * 3 * nqp + 3 * nqp + 32 * 2 * nqp) * N * w + 2 * 24 * N * w
+    # keys read whole (both halves), as for keys loaded from outside
+    pcmm2, mac2 = bench.algorithmic_bytes(key_parts=2)
+    assert pcmm2 - pcmm == 52 * 3 * nqp * N * w
+    assert mac2 == 11_249_123_328
     _, unfused = bench.algorithmic_bytes(fused_babies=False)
     assert unfused == 10_192_158_720
     assert unfused == 512 * nqp * N * w + 15 * 2 * nqp * N * w + 2 * 24 * N * w + 32 * 2 * nqp * N * w
@@ -45,13 +51,15 @@ def test_mac_unit_bytes():
 
 
 def test_keyswitch_kernel_bytes():
-    """keymac_baby: 15 keys of 3 digits x 2 parts x 32 QP rows, the 3 digits
-    once, P*c0 (24 rows) once, 15 rotated QP pairs; giant_acc: 31 keys, their
-    digits and c0 accumulators, one QP pair out."""
+    """keymac_baby: 15 key b halves of 3 digits x 32 QP rows, the 3 digits
+    once, P*c0 (24 rows) once, 15 rotated QP pairs; giant_acc: 31 key b
+    halves, their digits and c0 accumulators, one QP pair out."""
     baby, giant = bench.keyswitch_bytes(1 << 16, 24, 8, 16, 32)
     row = (1 << 16) * 8
-    assert baby == (15 * 3 * 2 * 32 + 3 * 32 + 24 + 15 * 2 * 32) * row
-    assert giant == (31 * (3 * 2 + 3 + 1) * 32 + 2 * 32) * row
+    assert baby == (15 * 3 * 32 + 3 * 32 + 24 + 15 * 2 * 32) * row
+    assert giant == (31 * (3 + 3 + 1) * 32 + 2 * 32) * row
+    baby2, giant2 = bench.keyswitch_bytes(1 << 16, 24, 8, 16, 32, key_parts=2)
+    assert (baby2 - baby, giant2 - giant) == (15 * 3 * 32 * row, 31 * 3 * 32 * row)
 
 
 @pytest.mark.parametrize("lq,nb,ng", [(1, 1, 1), (8, 4, 4)])
@@ -65,17 +73,20 @@ def test_keyswitch_bytes_without_rotations(lq, nb, ng):
 def test_keyswitch_pass_rows():
     """One rotation at level 22 (23 Q limbs, K=8, 3 digits of 8, 8, 7 rows):
     inverse NTT of 23 limbs (92 rows), extension 23 -> 70 rows (93), forward
-    NTT of 70 limbs (280), key product 11 x 31 rows (341), inverse NTT of 16 P
-    limbs (64), extension 16 -> 46 rows (62), forward NTT of 46 limbs whose
-    last pass also reads x and c0 (92 + 161): 1,185 rows = 621,281,280 B."""
+    NTT of 70 limbs (280), key product 8 x 31 rows (248: 3 key b halves, 3
+    digits, 2 outputs), inverse NTT of 16 P limbs (64), extension 16 -> 46 rows
+    (62), forward NTT of 46 limbs whose last pass also reads x and c0
+    (92 + 161): 1,092 rows = 572,522,496 B."""
     rows = bench.keyswitch_pass_rows(22, 8)
-    assert list(rows.values()) == [92, 93, 280, 341, 64, 62, 253]
-    assert sum(rows.values()) * (1 << 16) * 8 == 621_281_280
+    assert list(rows.values()) == [92, 93, 280, 248, 64, 62, 253]
+    assert sum(rows.values()) * (1 << 16) * 8 == 572_522_496
     # the key product alone is the per-rotation figure of the key-switch roofline
-    assert rows["key product"] * (1 << 16) * 8 == 178_782_208
+    assert rows["key product"] * (1 << 16) * 8 == 130_023_424
+    # keys read whole: 3 more halves of 31 rows
+    assert bench.keyswitch_pass_rows(22, 8, key_parts=2)["key product"] == 341
     # the fold step ct + Rotate(ct): its last pass also reads both parts of ct
     folded = bench.keyswitch_pass_rows(22, 8, fold_add=True)
-    assert sum(folded.values()) == 1185 + 2 * 23
+    assert sum(folded.values()) == 1092 + 2 * 23
 
 
 def test_measured_step_traffic():
