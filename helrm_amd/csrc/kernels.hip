@@ -43,6 +43,49 @@ void launch_mul_const(u64* out, const u64* in, size_t bstride, int batch, RowMap
   hipLaunchKernelGGL(mul_const_kernel, dim3(N / 256, rm.nact(), batch), dim3(256), 0, st, out, in, bstride, rm, cw, cwp, mods, N);
 }
 
+__global__ void mul_const_v_kernel(u64* __restrict__ out, const u64* __restrict__ in, size_t bstride, RowMap rm, RowConst c,
+                                   const ModC* __restrict__ mods, int N) {
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
+  const int row = rm.row(blockIdx.y);
+  const int m = rm.mod(row);
+  const size_t o = (size_t)blockIdx.z * bstride + (size_t)row * N + x;
+  out[o] = shoup_mul(in[o], c.w[m], c.wp[m], mods[m].q);
+}
+void launch_mul_const_v(u64* out, const u64* in, size_t bstride, int batch, RowMap rm, const RowConst& c, const ModC* mods,
+                        int N, hipStream_t st) {
+  if (rm.nact() <= 0 || batch <= 0) return;
+  hipLaunchKernelGGL(mul_const_v_kernel, dim3(N / 256, rm.nact(), batch), dim3(256), 0, st, out, in, bstride, rm, c, mods, N);
+}
+
+// One thread per word of the tensor product: both operands are read once,
+// b is taken to Montgomery form in registers (b R = mont_mul(b, R^2)), and
+// the three products are written together.
+__global__ __launch_bounds__(256) void tensor_kernel(u64* __restrict__ d0, u64* __restrict__ d1, u64* __restrict__ d2,
+                                                     const u64* __restrict__ a0, const u64* __restrict__ a1,
+                                                     const u64* __restrict__ b0, const u64* __restrict__ b1,
+                                                     const u64* __restrict__ pw, const u64* __restrict__ pwp,
+                                                     const ModC* __restrict__ mods, int N) {
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
+  const int k = blockIdx.y;
+  const ModC mc = mods[k];
+  const size_t o = (size_t)k * N + x;
+  const u64 b0R = mont_mul(b0[o], mc.r2, mc.q, mc.qinv), b1R = mont_mul(b1[o], mc.r2, mc.q, mc.qinv);
+  const u64 va0 = a0[o], va1 = a1[o];
+  u64 r0 = mont_mul(va0, b0R, mc.q, mc.qinv);
+  u64 r1 = add_mod(mont_mul(va0, b1R, mc.q, mc.qinv), mont_mul(va1, b0R, mc.q, mc.qinv), mc.q);
+  if (pw) {
+    r0 = shoup_mul(r0, pw[k], pwp[k], mc.q);
+    r1 = shoup_mul(r1, pw[k], pwp[k], mc.q);
+  }
+  d0[o] = r0;
+  d1[o] = r1;
+  d2[o] = mont_mul(va1, b1R, mc.q, mc.qinv);
+}
+void launch_tensor(u64* d0, u64* d1, u64* d2, const u64* a0, const u64* a1, const u64* b0, const u64* b1, int l,
+                   const u64* pw, const u64* pwp, const ModC* mods, int N, hipStream_t st) {
+  hipLaunchKernelGGL(tensor_kernel, dim3(N / 256, l + 1, 1), dim3(256), 0, st, d0, d1, d2, a0, a1, b0, b1, pw, pwp, mods, N);
+}
+
 // out = a * bR * R^-1 (b stored in Montgomery form); optional accumulate
 __global__ void mont_mul_kernel(u64* __restrict__ out, const u64* __restrict__ a, size_t abstride,
                                 const u64* __restrict__ bR, size_t bbstride, size_t obstride, RowMap rm,
@@ -60,19 +103,20 @@ void launch_mont_mul(u64* out, size_t obstride, const u64* a, size_t abstride, c
   hipLaunchKernelGGL(mont_mul_kernel, dim3(N / 256, rm.nact(), batch), dim3(256), 0, st, out, a, abstride, bR, bbstride, obstride, rm, mods, N, acc ? 1 : 0);
 }
 
-// out[row] = in[row] +- c[modulus of row] (a constant in every NTT slot)
-__global__ void add_scalar_kernel(u64* __restrict__ out, const u64* __restrict__ in, RowMap rm, const u64* __restrict__ c,
-                                  const ModC* __restrict__ mods, int N, int sub) {
-  int x = blockIdx.x * blockDim.x + threadIdx.x;
-  int row = rm.row(blockIdx.y);
-  int m = rm.mod(row);
-  u64 q = mods[m].q;
-  size_t o = (size_t)row * N + x;
-  out[o] = sub ? sub_mod(in[o], c[m], q) : add_mod(in[o], c[m], q);
+// out[row] = in[row] +- c.w[modulus of row] (a constant in every NTT slot)
+__global__ void add_scalar_v_kernel(u64* __restrict__ out, const u64* __restrict__ in, RowMap rm, RowConst c,
+                                    const ModC* __restrict__ mods, int N, int sub) {
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
+  const int row = rm.row(blockIdx.y);
+  const int m = rm.mod(row);
+  const u64 q = mods[m].q;
+  const size_t o = (size_t)row * N + x;
+  out[o] = sub ? sub_mod(in[o], c.w[m], q) : add_mod(in[o], c.w[m], q);
 }
-void launch_add_scalar(u64* out, const u64* in, RowMap rm, const u64* c, const ModC* mods, int N, bool sub, hipStream_t st) {
+void launch_add_scalar_v(u64* out, const u64* in, RowMap rm, const RowConst& c, const ModC* mods, int N, bool sub,
+                         hipStream_t st) {
   if (rm.nact() <= 0) return;
-  hipLaunchKernelGGL(add_scalar_kernel, dim3(N / 256, rm.nact(), 1), dim3(256), 0, st, out, in, rm, c, mods, N, sub ? 1 : 0);
+  hipLaunchKernelGGL(add_scalar_v_kernel, dim3(N / 256, rm.nact(), 1), dim3(256), 0, st, out, in, rm, c, mods, N, sub ? 1 : 0);
 }
 
 // v -> v*R mod q (to Montgomery form) or v*R^-1 (from), in place
@@ -423,10 +467,13 @@ __global__ __launch_bounds__(256) void keymac_kernel(KeyMacArgs a) {
   hi1 = fold_hi4(hi1, mc.q);
   // add0 enters the high word (v*2^64 == v*R mod q), so the REDC below returns sum + add0
   if (a.add0 && k <= a.l) hi0 = add_mod(hi0, a.add0[(size_t)k * N + src], mc.q);
+  const u64 add1 = (a.add1 && k <= a.l) ? a.add1[(size_t)k * N + src] : 0;
+  if (!seeded) hi1 = add_mod(hi1, add1, mc.q);
   const size_t o = (size_t)b * a.out_bstride + (size_t)k * N + i;
   a.out0[o] = redc(lo0, hi0, mc.q, mc.qinv);
   const u64 r1 = redc(lo1, hi1, mc.q, mc.qinv);
-  a.out1[o] = seeded ? mont_mul(r1, mc.r2, mc.q, mc.qinv) : r1;
+  // regenerated a halves carry no R: the REDC left sum * R^-1, and add1 comes after the correction
+  a.out1[o] = seeded ? add_mod(mont_mul(r1, mc.r2, mc.q, mc.qinv), add1, mc.q) : r1;
 }
 void launch_keymac(const KeyMacArgs& a, int batch, hipStream_t st) {
   if (batch <= 0) return;

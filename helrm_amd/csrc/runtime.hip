@@ -1135,15 +1135,13 @@ u64 residue_i64(i128 k, u64 q) {
   return m ? q - m : 0;
 }
 // both parts of c (level l) times the integer k, in place
+// (the residues travel in the kernel arguments: the host does not wait)
 void mul_int_inplace(Cipher& c, i128 k) {
   Scheme& s = sch();
-  const int l = c.level, nm = s.L + s.K;
-  std::vector<u64> w(nm, 0), wp(nm, 0);
-  for (int i = 0; i <= l; i++) { w[i] = residue_i64(k, s.mod[i]); wp[i] = shoup(w[i], s.mod[i]); }
-  DU64 dw(nm), dwp(nm);
-  upload(dw.p, w.data(), nm); upload(dwp.p, wp.data(), nm);
-  launch_mul_const(c.d.p, c.d.p, (size_t)(l + 1) * s.N, 2, rows_q(l), dw.p, dwp.p, s.d_mods.p, s.N, s.st);
-  sync();  // the constant tables are freed on return
+  const int l = c.level;
+  RowConst rc{};
+  for (int i = 0; i <= l; i++) { rc.w[i] = residue_i64(k, s.mod[i]); rc.wp[i] = shoup(rc.w[i], s.mod[i]); }
+  launch_mul_const_v(c.d.p, c.d.p, (size_t)(l + 1) * s.N, 2, rows_q(l), rc, s.d_mods.p, s.N, s.st);
 }
 // Mul(ct, float64): integer-valued constants multiply as integers (scale
 // unchanged); others are scaled by q_l and rounded, and the scale grows by q_l
@@ -1160,14 +1158,11 @@ void mul_float_inplace(Cipher& c, double v) {
 // Add(ct, float64): round(v * scale) added to (subtracted from) every NTT slot of part 0
 void add_const_inplace(Cipher& c, double v, bool sub) {
   Scheme& s = sch();
-  const int l = c.level, nm = s.L + s.K;
+  const int l = c.level;
   const i128 k = scaled_constant(v, c.scale);
-  std::vector<u64> kq(nm, 0);
-  for (int i = 0; i <= l; i++) kq[i] = residue_i64(k, s.mod[i]);
-  DU64 dk(nm);
-  upload(dk.p, kq.data(), nm);
-  launch_add_scalar(c.d.p, c.d.p, rows_q(l), dk.p, s.d_mods.p, s.N, sub, s.st);
-  sync();
+  RowConst rc{};
+  for (int i = 0; i <= l; i++) rc.w[i] = residue_i64(k, s.mod[i]);
+  launch_add_scalar_v(c.d.p, c.d.p, rows_q(l), rc, s.d_mods.p, s.N, sub, s.st);
 }
 // Mul(ct, pt): both parts times the plaintext at level min(ct, pt); scales multiply
 std::unique_ptr<Cipher> mul_plain_ct(const Cipher& ct, const Plain& pt) {
@@ -1182,30 +1177,29 @@ std::unique_ptr<Cipher> mul_plain_ct(const Cipher& ct, const Plain& pt) {
   return out;
 }
 // MulRelin(a, b): tensor (a0 b0, a0 b1 + a1 b0, a1 b1) at level min, then the
-// third part key switched with the relinearization key and added
-std::unique_ptr<Cipher> mul_relin_ct(const Cipher& a, const Cipher& b) {
+// third part key switched with the relinearization key and added.
+// rescale: return Rescale(MulRelin(a, b)) (one modulus), word for word: the
+// tensor's first two parts enter the key switch's Q rows multiplied by P
+// (ModDown(x + P d) = ModDown(x) + d exactly: [P d]_P = 0), and the ModDown
+// is fused with the rescale (mod_down_rescale), so the rescale's own inverse
+// and forward transforms are not run.
+std::unique_ptr<Cipher> mul_relin_ct(const Cipher& a, const Cipher& b, bool rescale) {
   Scheme& s = sch();
   REQUIRE(s.rlk, "relinearization key not generated");
   const int l = std::min(a.level, b.level), N = s.N, K = s.K, nqp = l + 1 + K, dn = (l + 1 + K - 1) / K;
+  REQUIRE(!rescale || l >= 1, "cannot rescale: ciphertext already at level 0");
   const size_t ps = (size_t)(l + 1) * N;
-  const u64 *a0 = a.d.p, *a1 = a.d.p + (size_t)(a.level + 1) * N;
-  const u64 *b0 = b.d.p, *b1 = b.d.p + (size_t)(b.level + 1) * N;
-  DU64 bR(2 * ps), d2(ps);
-  copy_rows(bR.p, ps, b.d.p, (size_t)(b.level + 1) * N, ps, 2);
-  launch_mont_convert(bR.p, ps, 2, rows_q(l), s.d_mods.p, N, true, s.st);
-  auto out = new_ct(l, a.scale * b.scale); out->logslots = a.logslots;
-  u64 *o0 = out->d.p, *o1 = out->d.p + ps;
-  launch_mont_mul(o0, 0, a0, 0, bR.p, 0, 1, rows_q(l), s.d_mods.p, N, false, s.st);
-  launch_mont_mul(o1, 0, a0, 0, bR.p + ps, 0, 1, rows_q(l), s.d_mods.p, N, false, s.st);
-  launch_mont_mul(o1, 0, a1, 0, bR.p, 0, 1, rows_q(l), s.d_mods.p, N, true, s.st);
-  launch_mont_mul(d2.p, 0, a1, 0, bR.p + ps, 0, 1, rows_q(l), s.d_mods.p, N, false, s.st);
-  (void)b0; (void)b1;
+  DU64 dt(3 * ps);
+  u64 *d0 = dt.p, *d1 = dt.p + ps, *d2 = dt.p + 2 * ps;
+  launch_tensor(d0, d1, d2, a.d.p, a.d.p + (size_t)(a.level + 1) * N, b.d.p, b.d.p + (size_t)(b.level + 1) * N, l,
+                rescale ? s.pmod_w.p : nullptr, rescale ? s.pmod_wp.p : nullptr, s.d_mods.p, N, s.st);
   DU64 digits((size_t)dn * nqp * N), dd((size_t)2 * nqp * N);
-  decompose_modup(l, d2.p, 0, 1, digits.p, false);
+  decompose_modup(l, d2, 0, 1, digits.p, false);
   KeyMacArgs k{};
   k.digits = digits.p; k.dig_bstride = 0; k.digits_per_batch = 0; k.key = nullptr; k.perm = nullptr;
-  k.key1 = s.rlk->p; k.perm1 = nullptr; k.add0 = nullptr;
-  k.own = d2.p; k.own_bstride = 0;
+  k.key1 = s.rlk->p; k.perm1 = nullptr;
+  k.add0 = rescale ? d0 : nullptr; k.add1 = rescale ? d1 : nullptr;
+  k.own = d2; k.own_bstride = 0;
   k.out0 = dd.p; k.out1 = dd.p + (size_t)nqp * N; k.out_bstride = 0; k.mods = s.d_mods.p;
   k.N = N; k.l = l; k.L = s.L; k.K = K; k.nqp = nqp; k.dn = dn;
   if (s.rlk_seeded) {
@@ -1213,8 +1207,14 @@ std::unique_ptr<Cipher> mul_relin_ct(const Cipher& a, const Cipher& b) {
     for (int d = 0; d < dn; d++) k.ka[d] = stream_key(ST_RLK_A((u64)d));
   }
   launch_keymac(k, 1, s.st);
+  if (rescale) {
+    auto out = new_ct(l - 1, a.scale * b.scale / (double)s.mod[l]); out->logslots = a.logslots;
+    mod_down_rescale(l, dd.p, (size_t)nqp * N, 2, out->d.p, (size_t)l * N);
+    return out;
+  }
+  auto out = new_ct(l, a.scale * b.scale); out->logslots = a.logslots;
   // out = ModDown(dd) + (d0, d1): the epilogue reads and writes each word in one thread
-  mod_down(l, dd.p, (size_t)nqp * N, 2, out->d.p, ps, out->d.p, ps, 2, nullptr);
+  mod_down(l, dd.p, (size_t)nqp * N, 2, out->d.p, ps, d0, ps, 2, nullptr);
   return out;
 }
 std::unique_ptr<Cipher> rescale_ct(const Cipher& ct);
@@ -1257,16 +1257,14 @@ std::unique_ptr<Cipher> eval_poly_ct(const Cipher& x, std::vector<double> coef, 
   }
   const double s2 = x.scale * x.scale / ql;
   const double sB = so * (double)s.mod[l - 1] / s2;
-  auto sq = mul_relin_ct(x, x);
-  auto X2 = rescale_ct(*sq);
+  auto X2 = mul_relin_ct(x, x, true);
   X2->scale = s2;
   auto tb = copy_ct(x);
   mul_int_inplace(*tb, scaled_constant(d == 3 ? coef[3] : 0.0, sB * ql / x.scale));
   auto B = rescale_ct(*tb);
   B->scale = sB;
   add_const_inplace(*B, coef[2], false);
-  auto PB = mul_relin_ct(*X2, *B);
-  auto out = rescale_ct(*PB);
+  auto out = mul_relin_ct(*X2, *B, true);
   out->scale = so;
   auto A2 = dropped_copy(*A, l - 2);
   add_const_inplace(*A2, coef[0], false);
@@ -2093,15 +2091,14 @@ void mul_i_inplace(Cipher& c) {
   Scheme& s = sch();
   const size_t ps = (size_t)(c.level + 1) * s.N;
   launch_mul_i(c.d.p, c.d.p, ps, 2, rows_q(c.level), s.iu.p, s.iup.p, s.niu.p, s.niup.p, s.d_mods.p, s.N, s.st);
-  sync();
 }
 int MulImaginaryUnit(int ct) { return guard([&] { mul_i_inplace(get_ct(ct)); return ct; }); }
 int MulImaginaryUnitNew(int ct) { return guard([&] { auto c = copy_ct(get_ct(ct)); mul_i_inplace(*c); return push_ct(std::move(c)); }); }
 int Negate(int ct) { return guard([&] { auto c = copy_ct(get_ct(ct)); mul_float_inplace(*c, -1.0); return push_ct(std::move(c)); }); }
 int MulRelinCiphertext(int a, int b) {
-  return guard([&] { Cipher& c = get_ct(a); auto r = mul_relin_ct(c, get_ct(b)); c = std::move(*r); return a; });
+  return guard([&] { Cipher& c = get_ct(a); auto r = mul_relin_ct(c, get_ct(b), false); c = std::move(*r); return a; });
 }
-int MulRelinCiphertextNew(int a, int b) { return guard([&] { return push_ct(mul_relin_ct(get_ct(a), get_ct(b))); }); }
+int MulRelinCiphertextNew(int a, int b) { return guard([&] { return push_ct(mul_relin_ct(get_ct(a), get_ct(b), false)); }); }
 
 // ---- polynomial evaluator ----
 int NewPolynomialEvaluator(void) { return guard([&] { sch(); return 0; }); }
