@@ -615,6 +615,14 @@ def main():
             "achieved_GBs": rb / (r_ms / 1000.0) / 1e9, "frac": rb / (r_ms / 1000.0) / 1e9 / HBM_PEAK_GBS,
             "pass_bytes_per_rotation": pb, "pass_GBs": pb / (r_ms / 1000.0) / 1e9,
             "pass_frac": pb / (r_ms / 1000.0) / 1e9 / HBM_PEAK_GBS}
+        # the floor the rotation's 11 dependent launches sit on: an empty
+        # dependent launch, and plain copies of the Q rows and of the
+        # extended QP rows (LaunchProbe, same stream)
+        lp_q, lp_x = lib.launch_probe(lf + 1), lib.launch_probe(dn * nqp - (lf + 1))
+        kernel_rooflines["keyswitch_rotation"]["launch_probe"] = {
+            "empty_launch_us": lp_q["empty_launch_us"], "copy_q_rows_us": lp_q["copy_us"],
+            "copy_q_rows_TBs": lp_q["copy_TBs"], "copy_extended_rows_us": lp_x["copy_us"],
+            "copy_extended_rows_TBs": lp_x["copy_TBs"], "q_rows": lf + 1, "extended_rows": dn * nqp - (lf + 1)}
 
     cpu = None
     if not args.no_cpu_baseline and cfg["kind"] == "dlrm":

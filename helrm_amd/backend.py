@@ -269,6 +269,7 @@ _SIGNATURES = {
     "MulAccDevice": ([_c.c_void_p, _c.c_void_p, _c.c_void_p, _I, _I], _I),
     "GetStream": ([], _c.c_void_p),
     "ValuPeakProbe": ([_c.POINTER(_c.c_double), _I], _I),
+    "LaunchProbe": ([_I, _c.POINTER(_c.c_double), _I], _I),
     "KernelTimingEnable": ([_I], _I),
     "KernelTimingGet": ([_c.c_char_p, _c.POINTER(_c.c_long), _c.POINTER(_c.c_double)], _I),
     "GetMemoryStats": ([_PU64, _PU64, _PU64], _I),
@@ -448,6 +449,12 @@ class HipLibrary:
         self.ValuPeakProbe(out, 5)
         return {"wave_instr_per_s": out[0], "cus": int(out[1]), "wave_instr_per_clk_per_cu": out[2],
                 "v_mad_u64_u32_per_s": out[3], "v_add3_u32_per_s": out[4]}
+
+    def launch_probe(self, limbs):
+        """Dependent-launch latency and the copy time of `limbs` rows (LaunchProbe)."""
+        out = (ctypes.c_double * 3)()
+        self.LaunchProbe(limbs, out, 3)
+        return {"empty_launch_us": out[0], "copy_us": out[1], "copy_TBs": out[2]}
 
     def memory_stats(self):
         a, b, c = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()

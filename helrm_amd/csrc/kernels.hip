@@ -764,6 +764,28 @@ void launch_rescale_spread(u64* t, const u64* u, int l, u64 half, const ModC* mo
   hipLaunchKernelGGL(rescale_spread_kernel, dim3(N / 256, l, 2), dim3(256), 0, st, t, u, l, half, mods, N);
 }
 
+__global__ void rescale_pair_spread_kernel(u64* __restrict__ t, const u64* __restrict__ u, int l, u64 half, RescalePair rp,
+                                           u64* __restrict__ ks, const ModC* __restrict__ mods, int N) {
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
+  const int i = blockIdx.y, b = blockIdx.z, g = b >> 1, p = b & 1;
+  const u64 ql = mods[l].q;
+  const u64 v = shoup_mul(u[(size_t)p * N + x], rp.kl[g], rp.klp[g], ql);
+  const u64 w = add_mod(v, half, ql);
+  const ModC mc = mods[i];
+  const u64 wr = mont_mul(w, mc.rmod, mc.q, mc.qinv);  // w mod q_i
+  const u64 hr = mont_mul(half, mc.rmod, mc.q, mc.qinv);
+  t[((size_t)b * l + i) * N + x] = sub_mod(wr, hr, mc.q);
+  if (x == 0 && p == 0) {
+    ks[(size_t)(0 * 2 + g) * l + i] = rp.k[g][i];
+    ks[(size_t)(1 * 2 + g) * l + i] = rp.kp[g][i];
+    ks[(size_t)(2 * 2 + g) * l + i] = rp.c[g][i];
+  }
+}
+void launch_rescale_pair_spread(u64* t, const u64* u, int l, u64 half, const RescalePair& rp, u64* ks, const ModC* mods,
+                                int N, hipStream_t st) {
+  hipLaunchKernelGGL(rescale_pair_spread_kernel, dim3(N / 256, l, 4), dim3(256), 0, st, t, u, l, half, rp, ks, mods, N);
+}
+
 // ModDown followed by a rescale, in the coefficient domain of the extension.
 // ext[p] holds [x]_P extended to rows q_0..q_l (coefficient domain) and
 // xl[p] row l of x (coefficient domain).  Row l of the ModDown result is
@@ -891,6 +913,14 @@ __global__ __launch_bounds__(256) void valu_probe_kernel(u64* __restrict__ out, 
 #pragma unroll
   for (int i = 0; i < 8; i++) s += a[i] + b[i];
   out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+// Launch-latency probe: a kernel that does nothing (its store is never taken
+// for the flags the host passes), to time a chain of dependent launches.
+__global__ __launch_bounds__(256) void empty_probe_kernel(u64* out, int flag) {
+  if (flag == 0x7fffffff && threadIdx.x == 0) out[blockIdx.x] = 1;
+}
+void launch_empty_probe(u64* out, int blocks, int flag, hipStream_t st) {
+  hipLaunchKernelGGL(empty_probe_kernel, dim3(blocks), dim3(256), 0, st, out, flag);
 }
 void launch_valu_probe(int op, u64* out, int blocks, uint32_t seed, int iters, hipStream_t st) {
   if (op == 0) hipLaunchKernelGGL((valu_probe_kernel<0>), dim3(blocks), dim3(256), 0, st, out, seed, iters);

@@ -239,6 +239,10 @@ struct ModDownEpi {
   const uint32_t* perm_inv;             // nullptr: identity
   const u64 *pinv, *pinvp;              // [mod] P^-1 mod q and its Shoup companion
   const u64* acc; size_t c_bstride;     // nullptr, or added at the output position (out != acc)
+  // scaled pair (launch_ntt_rescale_pair): batch entry b = 2 g + p reads part
+  // p of x, multiplies it by ks's K_g of its row, adds C_g to part 0 and
+  // writes group g to out (g = 0) or out2 (g = 1); ks == nullptr: off
+  const u64* ks; int ks_rows; u64* out2;
 };
 
 struct NttArgs {
@@ -414,9 +418,10 @@ __device__ __forceinline__ void row_fwd_tail(const NttArgs& a, const u64* srow, 
     // ModDown epilogue: limb (batch b, Q row) of the extension
     const int b = lr.pad, row = (int)((lr.off - (int64_t)b * (int64_t)a.bstride) >> a.logN);
     const size_t rowoff = ((size_t)row << a.logN) + (size_t)r * C;
-    const u64* xr = a.e.x + (size_t)b * a.e.x_bstride + rowoff;
+    const int g = a.e.ks ? b >> 1 : 0, part = a.e.ks ? b & 1 : b;
+    const u64* xr = a.e.x + (size_t)part * a.e.x_bstride + rowoff;
     const u64* ar = (a.e.add && b < a.e.add_batches) ? a.e.add + (size_t)b * a.e.a_bstride + rowoff : nullptr;
-    u64* orow = a.e.out + (size_t)b * a.e.o_bstride + ((size_t)row << a.logN);
+    u64* orow = (g ? a.e.out2 : a.e.out) + (size_t)part * a.e.o_bstride + ((size_t)row << a.logN);
     const u64 pi = a.e.pinv[m], pip = a.e.pinvp[m];
     // every load of the epilogue is issued before the first use, so the
     // latencies overlap instead of adding up word by word
@@ -444,6 +449,16 @@ __device__ __forceinline__ void row_fwd_tail(const NttArgs& a, const u64* srow, 
       const u64* crow = a.e.acc + (size_t)b * a.e.c_bstride + ((size_t)row << a.logN);
 #pragma unroll
       for (int i = 0; i < 16; i++) av[i] = add_mod(av[i], crow[dst[i]], q);
+    }
+    if (a.e.ks) {
+      const int R = a.e.ks_rows;
+      const u64 kw = a.e.ks[(size_t)g * R + row], kwp = a.e.ks[(size_t)(2 + g) * R + row];
+      const u64 cadd = part == 0 ? a.e.ks[(size_t)(4 + g) * R + row] : 0;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        xv[i] = shoup_mul(xv[i], kw, kwp, q);
+        av[i] = add_mod(av[i], cadd, q);
+      }
     }
 #pragma unroll
     for (int i = 0; i < 16; i++) {
@@ -796,9 +811,10 @@ __device__ __forceinline__ void row8_fwd_tail(const NttArgs& a, const u64* srow,
   if (EPI) {
     const int b = lr.pad, row = (int)((lr.off - (int64_t)b * (int64_t)a.bstride) >> a.logN);
     const size_t rowoff = ((size_t)row << a.logN) + (size_t)r * C;
-    const u64* xr = a.e.x + (size_t)b * a.e.x_bstride + rowoff;
+    const int g = a.e.ks ? b >> 1 : 0, part = a.e.ks ? b & 1 : b;
+    const u64* xr = a.e.x + (size_t)part * a.e.x_bstride + rowoff;
     const u64* ar = (a.e.add && b < a.e.add_batches) ? a.e.add + (size_t)b * a.e.a_bstride + rowoff : nullptr;
-    u64* orow = a.e.out + (size_t)b * a.e.o_bstride + ((size_t)row << a.logN);
+    u64* orow = (g ? a.e.out2 : a.e.out) + (size_t)part * a.e.o_bstride + ((size_t)row << a.logN);
     const u64 pi = a.e.pinv[m], pip = a.e.pinvp[m];
     u64 xv[8], av[8];
     uint32_t dst[8];
@@ -822,6 +838,16 @@ __device__ __forceinline__ void row8_fwd_tail(const NttArgs& a, const u64* srow,
       const u64* crow = a.e.acc + (size_t)b * a.e.c_bstride + ((size_t)row << a.logN);
 #pragma unroll
       for (int i = 0; i < 8; i++) av[i] = add_mod(av[i], crow[dst[i]], q);
+    }
+    if (a.e.ks) {
+      const int R = a.e.ks_rows;
+      const u64 kw = a.e.ks[(size_t)g * R + row], kwp = a.e.ks[(size_t)(2 + g) * R + row];
+      const u64 cadd = part == 0 ? a.e.ks[(size_t)(4 + g) * R + row] : 0;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        xv[i] = shoup_mul(xv[i], kw, kwp, q);
+        av[i] = add_mod(av[i], cadd, q);
+      }
     }
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -1127,8 +1153,24 @@ void launch_ntt_moddown(u64* ext, size_t ext_bstride, int batch, int l, int logN
   a.tw = reinterpret_cast<const uint4*>(tw.tw);
   a.twr = reinterpret_cast<const uint4*>(tw.twr);
   a.epi = 1;
-  a.e = ModDownEpi{x, x_bstride, out, o_bstride, add, a_bstride, add_batches, perm_inv, pinv, pinvp, acc, c_bstride};
+  a.e = ModDownEpi{x, x_bstride, out, o_bstride, add, a_bstride, add_batches, perm_inv, pinv, pinvp, acc, c_bstride,
+                   nullptr, 0, nullptr};
   ntt_launch(a, (l + 1) * batch, true, st);
+}
+void launch_ntt_rescale_pair(u64* t, size_t t_bstride, int l, int logN, const u64* x, size_t x_bstride, u64* out0,
+                             u64* out1, size_t o_bstride, const u64* ks, const u64* rsinv, const u64* rsinvp,
+                             const NttTables& tw, hipStream_t st) {
+  const RowMap rm{l, l, 0, 0, 0, 0};
+  NttArgs a{};
+  a.list = nullptr;
+  a.src = t; a.sstride = t_bstride; a.data = t; a.bstride = t_bstride; a.rm = rm; a.rows = l; a.batch = 4;
+  a.mods = tw.mods;
+  a.ninv = tw.ninv; a.ninvp = tw.ninvp; a.fpc = tw.fpc; a.logN = logN;
+  a.tw = reinterpret_cast<const uint4*>(tw.tw);
+  a.twr = reinterpret_cast<const uint4*>(tw.twr);
+  a.epi = 1;
+  a.e = ModDownEpi{x, x_bstride, out0, o_bstride, nullptr, 0, 0, nullptr, rsinv, rsinvp, nullptr, 0, ks, l, out1};
+  ntt_launch(a, l * 4, true, st);
 }
 
 void launch_ntt_list(u64* data, const void* list, int nlimbs, int logN, bool forward, const NttTables& tw, hipStream_t st) {

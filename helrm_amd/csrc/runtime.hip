@@ -1219,12 +1219,36 @@ std::unique_ptr<Cipher> mul_relin_ct(const Cipher& a, const Cipher& b, bool resc
 }
 std::unique_ptr<Cipher> rescale_ct(const Cipher& ct);
 void add_inplace(Cipher& a, const Cipher& b, bool sub);
-// keep rows 0..nl of both parts (Lattigo DropLevel: the scale is unchanged)
-std::unique_ptr<Cipher> dropped_copy(const Cipher& c, int nl) {
+// Rescale(K_g * x) + C_g (C_g added to part 0, at the output's scale) for two
+// integers K_0, K_1 in one pass, word for word what mul_int_inplace,
+// rescale_ct and add_const_inplace compute one after the other: the inverse
+// transform of x's row l is shared (the rescale's spread takes K_g,l times
+// it), and the forward transform's epilogue multiplies x by K_g,i itself.
+std::pair<std::unique_ptr<Cipher>, std::unique_ptr<Cipher>> rescale_scaled_pair(const Cipher& x, i128 k0, double c0,
+                                                                                 double sc0, i128 k1, double c1, double sc1) {
   Scheme& s = sch();
-  auto out = new_ct(nl, c.scale); out->logslots = c.logslots;
-  copy_rows(out->d.p, (size_t)(nl + 1) * s.N, c.d.p, (size_t)(c.level + 1) * s.N, (size_t)(nl + 1) * s.N, 2);
-  return out;
+  const int l = x.level, N = s.N;
+  REQUIRE(l >= 1, "cannot rescale: ciphertext already at level 0");
+  REQUIRE(l <= HCK_MAXQ, "rescale pair: too many limbs");
+  RescalePair rp{};
+  const i128 ks[2] = {k0, k1};
+  const double cs[2] = {c0, c1}, scs[2] = {sc0, sc1};
+  for (int g = 0; g < 2; g++) {
+    rp.kl[g] = residue_i64(ks[g], s.mod[l]); rp.klp[g] = shoup(rp.kl[g], s.mod[l]);
+    const i128 kc = scaled_constant(cs[g], scs[g]);
+    for (int i = 0; i < l; i++) {
+      rp.k[g][i] = residue_i64(ks[g], s.mod[i]); rp.kp[g][i] = shoup(rp.k[g][i], s.mod[i]);
+      rp.c[g][i] = residue_i64(kc, s.mod[i]);
+    }
+  }
+  DU64 u((size_t)2 * N), t((size_t)4 * l * N), kd((size_t)6 * l);
+  ntt_oop(x.d.p + (size_t)l * N, (size_t)(l + 1) * N, u.p, N, 2, RowMap{1, 1, l, 0, 0, 0}, false);
+  launch_rescale_pair_spread(t.p, u.p, l, s.mod[l] >> 1, rp, kd.p, s.d_mods.p, N, s.st);
+  auto a = new_ct(l - 1, x.scale / (double)s.mod[l]); a->logslots = x.logslots;
+  auto b = new_ct(l - 1, x.scale / (double)s.mod[l]); b->logslots = x.logslots;
+  launch_ntt_rescale_pair(t.p, (size_t)l * N, l, s.logN, x.d.p, (size_t)(l + 1) * N, a->d.p, b->d.p, (size_t)l * N, kd.p,
+                          s.rs_inv.p + (size_t)l * s.L, s.rs_invp.p + (size_t)l * s.L, s.tw, s.st);
+  return {std::move(a), std::move(b)};
 }
 // Monomial polynomial of degree <= 3 at depth ceil(log2(d + 1)), output scale
 // `so` (the same composition as the restatement's orc_eval_poly):
@@ -1247,27 +1271,28 @@ std::unique_ptr<Cipher> eval_poly_ct(const Cipher& x, std::vector<double> coef, 
   }
   REQUIRE(l >= (d == 1 ? 1 : 2), "not enough levels left for the polynomial");
   const double ql = (double)s.mod[l];
-  auto t = copy_ct(x);
-  mul_int_inplace(*t, scaled_constant(coef[1], so * ql / x.scale));
-  auto A = rescale_ct(*t);
-  A->scale = so;
+  const i128 k1 = scaled_constant(coef[1], so * ql / x.scale);
   if (d == 1) {
+    auto t = copy_ct(x);
+    mul_int_inplace(*t, k1);
+    auto A = rescale_ct(*t);
+    A->scale = so;
     add_const_inplace(*A, coef[0], false);
     return A;
   }
   const double s2 = x.scale * x.scale / ql;
   const double sB = so * (double)s.mod[l - 1] / s2;
+  // A + c0 and B = Rescale(X * K3) + c2 in one rescale pass (A's rows above
+  // l - 2 are not read: the final sum is at level l - 2)
+  auto AB = rescale_scaled_pair(x, k1, coef[0], so, scaled_constant(d == 3 ? coef[3] : 0.0, sB * ql / x.scale), coef[2], sB);
+  auto& A2 = AB.first;
+  auto& B = AB.second;
+  A2->scale = so;
+  B->scale = sB;
   auto X2 = mul_relin_ct(x, x, true);
   X2->scale = s2;
-  auto tb = copy_ct(x);
-  mul_int_inplace(*tb, scaled_constant(d == 3 ? coef[3] : 0.0, sB * ql / x.scale));
-  auto B = rescale_ct(*tb);
-  B->scale = sB;
-  add_const_inplace(*B, coef[2], false);
   auto out = mul_relin_ct(*X2, *B, true);
   out->scale = so;
-  auto A2 = dropped_copy(*A, l - 2);
-  add_const_inplace(*A2, coef[0], false);
   add_inplace(*out, *A2, false);
   return out;
 }
@@ -2600,6 +2625,38 @@ void* GetStream(void) { return S ? (void*)S->st : nullptr; }
 // whole GPU: out[0] = the peak (the faster of the two probes), out[1] =
 // compute units, out[2] = the peak per compute unit and clock at the
 // device's peak clock, out[3] = v_mad_u64_u32 alone, out[4] = v_add3_u32.
+int LaunchProbe(int limbs, double* out, int len) {
+  return guard([&] {
+    Scheme& s = sch();
+    REQUIRE(out && len >= 3, "LaunchProbe needs 3 outputs");
+    REQUIRE(limbs >= 1 && limbs <= 256, "LaunchProbe: 1 to 256 limbs");
+    const int reps = 200;
+    const size_t words = (size_t)limbs * s.N;
+    DU64 a(words), b(words), o(4096);
+    HCHECK(hipMemsetAsync(a.p, 0, words * 8, s.st));
+    HCHECK(hipMemsetAsync(b.p, 0, words * 8, s.st));
+    hipEvent_t e0, e1;
+    HCHECK(hipEventCreate(&e0)); HCHECK(hipEventCreate(&e1));
+    auto time = [&](auto&& body) {
+      for (int r = 0; r < reps; r++) body(r);  // warm-up
+      HCHECK(hipEventRecord(e0, s.st));
+      for (int r = 0; r < reps; r++) body(r);
+      HCHECK(hipEventRecord(e1, s.st));
+      HCHECK(hipEventSynchronize(e1));
+      float ms = 0;
+      HCHECK(hipEventElapsedTime(&ms, e0, e1));
+      return (double)ms * 1e3 / reps;
+    };
+    out[0] = time([&](int r) { launch_empty_probe(o.p, 1024, r, s.st); });
+    out[1] = time([&](int r) {
+      if (r & 1) launch_copy(a.p, 0, b.p, 0, words, 1, s.st);
+      else launch_copy(b.p, 0, a.p, 0, words, 1, s.st);
+    });
+    out[2] = 2.0 * words * 8 / (out[1] * 1e-6) / 1e12;
+    (void)hipEventDestroy(e0); (void)hipEventDestroy(e1);
+    return 0;
+  });
+}
 int ValuPeakProbe(double* out, int len) {
   return guard([&] {
     Scheme& s = sch();

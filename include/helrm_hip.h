@@ -251,6 +251,11 @@ int JoinStream(int idx);
  * units, out[2] = the peak per compute unit per clock (peak clock), out[3] =
  * v_mad_u64_u32 alone, out[4] = v_add3_u32 alone. */
 int ValuPeakProbe(double* out, int len);
+/* [ext] launch-latency probe (measurement only), HIP events over 200
+ * dependent launches on the current stream: out[0] = microseconds per launch
+ * of an empty kernel of 1,024 workgroups, out[1] = microseconds per copy of
+ * `limbs` rows of N words (read and written), out[2] = that copy's TB/s. */
+int LaunchProbe(int limbs, double* out, int len);
 int KernelTimingEnable(int on);                                   /* HIP events around named launches */
 int KernelTimingGet(const char* name, long* count, double* total_ms);
 int GetMemoryStats(uint64_t* live, uint64_t* cached, uint64_t* peak);

@@ -36,3 +36,20 @@ def test_device_buffer_after_delete_scheme_refused(hip_lib):
     dec = np.asarray(hip_lib.Decode(hip_lib.Decrypt(ct)))
     np.testing.assert_allclose(dec[:16], np.linspace(-1, 1, 16), atol=1e-4)
     hip_lib.DeleteScheme()
+
+
+def test_measurement_probes(hip_lib):
+    """The measurement entry points bench.py reports: the launch-latency probe
+    (an empty dependent launch costs microseconds; a copy's rate is positive
+    and below the HBM peak; out-of-range sizes are refused) and the VALU
+    issue-rate probe."""
+    q, p = make_params(16, [50, 50], [61])
+    new_hip_scheme(hip_lib, 16, q, p, 40, 64, 3)
+    r = hip_lib.launch_probe(4)
+    assert 0.1 < r["empty_launch_us"] < 100
+    assert r["copy_us"] > 0 and 0 < r["copy_TBs"] < 8.0
+    with pytest.raises(HipError, match="LaunchProbe"):
+        hip_lib.launch_probe(0)
+    v = hip_lib.valu_peak()
+    assert v["cus"] > 0 and v["wave_instr_per_s"] > 0
+    hip_lib.DeleteScheme()
