@@ -275,7 +275,10 @@ __global__ __launch_bounds__(256) void bconv_lds_kernel(const u64* __restrict__ 
   const BConvJob& J = jobs.j[d];
   const BConvTable* __restrict__ tab = J.tab;
   const int ns = J.ns;
-  const int lane = threadIdx.x & (BCL_X - 1), w = threadIdx.x / BCL_X;
+  // w is the wave's index: made wave-uniform for the compiler, so that the
+  // row loop's table words and modulus constants are scalar loads (as
+  // per-lane loads every row would wait on a memory round trip)
+  const int lane = threadIdx.x & (BCL_X - 1), w = __builtin_amdgcn_readfirstlane(threadIdx.x / BCL_X);
   const int x = blockIdx.x * BCL_X + lane;
   const u64* inb = in + (size_t)b * in_bstride + (size_t)J.src_row * N;
   u64* outb = out + (size_t)b * out_bstride + J.out_off;
