@@ -57,6 +57,57 @@ void launch_mul_const_v(u64* out, const u64* in, size_t bstride, int batch, RowM
   hipLaunchKernelGGL(mul_const_v_kernel, dim3(N / 256, rm.nact(), batch), dim3(256), 0, st, out, in, bstride, rm, c, mods, N);
 }
 
+// One thread per output dword of every (diagonal, row).  A packed row's
+// dword d of chunk c holds bits [32 d, 32 d + 32) of the chunk's 64 fields:
+// from field j = 32 d / 52 upward (and field j + 1 where field j ends inside
+// the dword); a plain row's dwords are its words' halves.
+__global__ __launch_bounds__(256) void pack_diags_kernel(uint32_t* __restrict__ dst, size_t dst_stride,
+                                                        const u64* __restrict__ src, size_t src_stride,
+                                                        const uint32_t* __restrict__ rowdesc, int N) {
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int k = blockIdx.y, p = blockIdx.z;
+  const uint32_t off = rowdesc[2 * k], bits = rowdesc[2 * k + 1];
+  const u64* w = src + (size_t)p * src_stride + (size_t)k * N;
+  uint32_t* o = dst + (size_t)p * dst_stride + off;
+  if (bits == 0) {
+    if (t < (size_t)2 * N) o[t] = (uint32_t)(w[t >> 1] >> (32 * (t & 1)));
+    return;
+  }
+  if (t >= (size_t)(N / 64) * PK_CHUNK) return;
+  const int c = (int)(t / PK_CHUNK), d = (int)(t % PK_CHUNK);
+  const int bit0 = 32 * d, j = bit0 / PK_BITS, sh = bit0 - PK_BITS * j;
+  const u64* wc = w + (size_t)c * 64;
+  u64 v = wc[j] >> sh;
+  if (sh + 32 > PK_BITS && j + 1 < 64) v |= wc[j + 1] << (PK_BITS - sh);
+  o[t] = (uint32_t)v;
+}
+void launch_pack_diags(uint32_t* dst, size_t dst_stride, const u64* src, size_t src_stride, int np, const uint32_t* rowdesc,
+                       int nrows, int N, hipStream_t st) {
+  if (np <= 0 || nrows <= 0) return;
+  hipLaunchKernelGGL(pack_diags_kernel, dim3((2 * N + 255) / 256, nrows, np), dim3(256), 0, st, dst, dst_stride, src, src_stride,
+                     rowdesc, N);
+}
+// Word x of a packed row: chunk x / 64, field j = x % 64 at bit 52 j: its
+// three dwords (the third only read when the field crosses two: shift > 12,
+// never for the chunk's last field, whose index is clamped inside the chunk).
+__device__ __forceinline__ u64 pk_field(const uint32_t* chunk, int j) {
+  const int bit = PK_BITS * j, dw = bit >> 5, sh = bit & 31;
+  const uint32_t d0 = chunk[dw], d1 = chunk[dw + 1], d2 = chunk[min(dw + 2, PK_CHUNK - 1)];
+  return (u64)__builtin_amdgcn_alignbit(d1, d0, sh) |
+         ((u64)(__builtin_amdgcn_alignbit(d2, d1, sh) & ((1u << (PK_BITS - 32)) - 1)) << 32);
+}
+__global__ __launch_bounds__(256) void unpack_diag_kernel(u64* __restrict__ dst, const uint32_t* __restrict__ src,
+                                                         const uint32_t* __restrict__ rowdesc, int N) {
+  const int x = blockIdx.x * blockDim.x + threadIdx.x, k = blockIdx.y;
+  const uint32_t off = rowdesc[2 * k], bits = rowdesc[2 * k + 1];
+  const uint32_t* r = src + off;
+  dst[(size_t)k * N + x] = bits ? pk_field(r + (size_t)(x >> 6) * PK_CHUNK, x & 63)
+                                : ((u64)r[2 * (size_t)x + 1] << 32) | r[2 * (size_t)x];
+}
+void launch_unpack_diag(u64* dst, const uint32_t* src, const uint32_t* rowdesc, int nrows, int N, hipStream_t st) {
+  hipLaunchKernelGGL(unpack_diag_kernel, dim3(N / 256, nrows, 1), dim3(256), 0, st, dst, src, rowdesc, N);
+}
+
 // One thread per word of the tensor product: both operands are read once,
 // b is taken to Montgomery form in registers (b R = mont_mul(b, R^2)), and
 // the three products are written together.
@@ -705,8 +756,98 @@ __global__ __launch_bounds__(256) void diag_mac_kernel(DiagMacArgs a) {
     mac_group<NB, ACC>(a, dA, tA, s0, s1, mc, Tb + (size_t)g * a.T_gstride);
   }
 }
+// The dense 16-baby diagonal MAC over diagonals stored in the packed layout.
+// Each wave fetches its 64 coefficients' chunk of 8 diagonals at a time
+// (half a giant group) straight into LDS with global_load_lds_dwordx4 -- a
+// packed row's chunk is 104 dwords (26 lanes x 16 B), a plain row's 128 (32
+// lanes) -- the next half's while the current one is multiplied, so no
+// registers are held by loads in flight, and unpacks its own word from LDS.
+// A packed row reads 104 instead of 128 dwords per 64 words.
+constexpr int MAC_HALF = 8, MAC_SLOT = 128;
+typedef uint32_t MacLds[2][MAC_HALF][MAC_SLOT];  // one wave's two half-group buffers
+// The group loop of one row (PK: stored packed).  Wait counts: vector memory
+// operations complete in issue order; a half's 8 chunks are in LDS once at
+// most the operations issued after them are outstanding: the next half's 8
+// loads, plus the previous group's two accumulator stores when they came in
+// between (first half of every group but the first).
+template <bool PK>
+__device__ __forceinline__ void mac_d16_rows(const DiagMacArgs& a, const u64 (&s0)[16], const u64 (&s1)[16], const ModC& mc,
+                                             u64* Tb, const uint32_t* wbase, MacLds& lds, int lane) {
+  constexpr int SLOT = PK ? PK_CHUNK : MAC_SLOT;  // dwords of one 64-word chunk
+  const size_t ds = 2 * a.diag_stride;            // dwords from one diagonal to the next
+  // half h = 2 g + i: diagonals 8 i .. 8 i + 7 of group g into buffer h & 1
+  auto issue = [&](int h) {
+    if (lane < SLOT / 4) {
+      const uint32_t* src = wbase + (size_t)(h * MAC_HALF) * ds + 4 * lane;
+#pragma unroll
+      for (int b = 0; b < MAC_HALF; b++)
+        __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)b * ds),
+                                         (__attribute__((address_space(3))) void*)&lds[h & 1][b][0], 16, 0, 0);
+    }
+  };
+  issue(2 * a.g0);
+  for (int g = a.g0; g < a.g1; g++) {
+    Acc128 A0, A1;
+    acc_zero(A0); acc_zero(A1);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int h = 2 * g + i;
+      const bool more = i == 0 || g + 1 < a.g1;
+      if (more) issue(h + 1);
+      if (!more) __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));                       // vmcnt(0)
+      else if (i == 0 && g != a.g0) __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8) | 10);  // vmcnt(10)
+      else __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8) | 8);                         // vmcnt(8)
+#pragma unroll
+      for (int b = 0; b < MAC_HALF; b++) {
+        const uint32_t* c = &lds[h & 1][b][0];
+        const u64 d = PK ? pk_field(c, lane) : ((u64)c[2 * lane + 1] << 32) | c[2 * lane];
+        acc_mac(A0, d, s0[MAC_HALF * i + b]);
+        acc_mac(A1, d, s1[MAC_HALF * i + b]);
+      }
+    }
+    // 16 products of words < 2^62: the high word folded below q, one REDC
+    u64 lo0, hi0, lo1, hi1;
+    acc_value(A0, lo0, hi0);
+    acc_value(A1, lo1, hi1);
+    u64* T = Tb + (size_t)g * a.T_gstride;
+    __builtin_nontemporal_store(redc(lo0, fold_hi4(hi0, mc.q), mc.q, mc.qinv), &T[0]);
+    __builtin_nontemporal_store(redc(lo1, fold_hi4(hi1, mc.q), mc.q, mc.qinv), &T[a.T_pstride]);
+  }
+}
+__global__ __launch_bounds__(256) void diag_mac_d16_kernel(DiagMacArgs a) {
+  constexpr int NB = 16;
+  __shared__ MacLds lds[4];
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
+  const int k = blockIdx.y;
+  const int N = a.N;
+  const int kl = k <= a.l ? k : a.L + (k - a.l - 1);
+  const ModC mc = a.mods[kl];
+  const int krow = k <= a.l ? k : a.lt_level + 1 + (k - a.l - 1);  // row inside a diagonal
+  u64 s0[NB], s1[NB];
+#pragma unroll
+  for (int b = 0; b < NB; b++) {
+    s0[b] = 0; s1[b] = 0;
+    if (a.baby_is_zero[b]) {
+      if (k <= a.l) { s0[b] = a.pc[(size_t)k * N + x]; s1[b] = a.pc[a.pc_pstride + (size_t)k * N + x]; }
+    } else {
+      baby_rotation_at(a, a.baby_slot[b], k, kl, x, mc, s0[b], s1[b]);
+    }
+  }
+  u64* Tb = a.T + (size_t)k * N + x;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // this wave's chunk of the row: 64 coefficients from blockIdx.x * 256 + 64 w
+  const uint32_t* rbase = reinterpret_cast<const uint32_t*>(a.diag) + a.pkrow[2 * krow];
+  const size_t c = (size_t)blockIdx.x * 4 + w;
+  if (a.pkrow[2 * krow + 1]) mac_d16_rows<true>(a, s0, s1, mc, Tb, rbase + c * PK_CHUNK, lds[w], lane);
+  else mac_d16_rows<false>(a, s0, s1, mc, Tb, rbase + c * MAC_SLOT, lds[w], lane);
+}
 void launch_diag_mac(const DiagMacArgs& a, hipStream_t st) {
   if (a.g1 <= a.g0) return;
+  if (a.pkrow) {
+    // a transform stored packed (dense, 16 baby steps)
+    hipLaunchKernelGGL(diag_mac_d16_kernel, dim3(a.N / 256, a.nqp, 1), dim3(256), 0, st, a);
+    return;
+  }
   dim3 grid(a.N / 256, a.nqp, 1);
   const bool dense = a.dense && a.nb_chunk == 16 && a.b0 + 16 <= a.nbaby;
   if (a.b0 == 0) {

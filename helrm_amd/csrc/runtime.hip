@@ -311,7 +311,14 @@ struct LinTrans {
   std::vector<int> giant;                // giant rotation per group
   std::vector<std::vector<int>> baby;    // sorted babies per group
   std::vector<int> plain_idx;            // diagonal index of each stored plaintext
-  DU64 diags;                            // [np][level+1+K][N], Montgomery form
+  DU64 diags;                            // [np][level+1+K][N], Montgomery form (packed: see below)
+  // dense 16-baby transforms store their diagonals packed (rows of moduli
+  // below 2^52 as 52-bit fields, PK_CHUNK dwords per 64 words): per row its
+  // dword offset and 52 or 0 (plain), and the dwords of one diagonal
+  bool packed = false;
+  std::vector<uint32_t> pkrow;
+  DevArray<uint32_t> d_pkrow;
+  size_t pk_stride = 0;
   std::vector<char> resident;            // per stored plaintext: loaded (SerializeDiagonal / Remove drop it)
   DevArray<int> d_gpi, d_bzero, d_bslot;  // [ng][nbaby] plaintext index (absent: the zero plaintext); per-baby flags
   std::vector<int> gpi, bzero, bslot;     // host copies, checked before every diagonal-MAC launch
@@ -802,8 +809,12 @@ void special_fft(const Scheme& s, std::vector<double>& re, std::vector<double>& 
 // + ((k + src[p].rot) mod slots)] (zero past nvals), its residues go to rows
 // rm of out + p * out_pstride, then the forward NTT.  Batches of up to 64
 // plaintexts share one work buffer.
+// chunk_done: nullptr -> the np plaintexts go to out (out_pstride apart);
+// else out holds one chunk of up to 64 plaintexts, handed to chunk_done(c0, n)
+// after each chunk is encoded (before the next overwrites it)
 void encode_device(const float* h_data, size_t ndata, const std::vector<EncodeSrc>& src, int nvals, double scale, RowMap rm,
-                   u64* out, size_t out_pstride, bool complex_in = false) {
+                   u64* out, size_t out_pstride, bool complex_in = false,
+                   const std::function<void(int, int)>& chunk_done = nullptr) {
   Scheme& s = sch();
   const int N = s.N, slots = N / 2;
   DevArray<float> dd(std::max<size_t>(ndata, 1));
@@ -813,10 +824,11 @@ void encode_device(const float* h_data, size_t ndata, const std::vector<EncodeSr
   DevArray<double> re((size_t)chunk * slots), im((size_t)chunk * slots);
   for (int c0 = 0; c0 < np; c0 += chunk) {
     const int nb = std::min(chunk, np - c0);
-    u64* o = out + (size_t)c0 * out_pstride;
+    u64* o = chunk_done ? out : out + (size_t)c0 * out_pstride;
     launch_encode_fft(o, out_pstride, rm, dd.p, ds.p + c0, nb, nvals, scale, re.p, im.p, slots, s.d_rotgroup.p, s.d_rre.p,
                       s.d_rim.p, s.d_mods.p, s.logN, s.st, complex_in);
     ntt(o, out_pstride, nb, rm, true);
+    if (chunk_done) chunk_done(c0, nb);
   }
   sync();
 }
@@ -1397,6 +1409,52 @@ void check_mac_tables(const LinTrans& t) {
   }
 }
 
+// u64 words one stored diagonal takes
+size_t lt_diag_words(const LinTrans& t) {
+  Scheme& s = sch();
+  return t.packed ? t.pk_stride / 2 : (size_t)(t.level + 1 + s.K) * s.N;
+}
+// the packed layout of a dense 16-baby transform's diagonals
+void lt_pack_layout(LinTrans& t) {
+  Scheme& s = sch();
+  const int nqp = t.level + 1 + s.K, N = s.N;
+  t.pkrow.assign((size_t)2 * nqp, 0);
+  size_t off = 0;
+  for (int k = 0; k < nqp; k++) {
+    const u64 q = s.mod[qp_mod(t.level, k)];
+    const bool pk = q < (1ull << PK_BITS) && N % 256 == 0;
+    t.pkrow[2 * k] = (uint32_t)off;
+    t.pkrow[2 * k + 1] = pk ? PK_BITS : 0;
+    off += pk ? (size_t)(N / 64) * PK_CHUNK : (size_t)2 * N;
+  }
+  REQUIRE(off < (1ull << 32), "packed diagonal too large");
+  t.pk_stride = off;  // every row a multiple of 4 dwords: rows and diagonals stay 16-byte aligned
+  t.packed = true;
+  t.d_pkrow = DevArray<uint32_t>(t.pkrow.size());
+  upload(t.d_pkrow.p, t.pkrow.data(), t.pkrow.size());
+}
+// storage of np diagonals + the all-zero plaintext after them
+void lt_alloc_diags(LinTrans& t, int np) {
+  Scheme& s = sch();
+  const size_t w = lt_diag_words(t);
+  t.diags = DU64((size_t)(np + 1) * w);
+  HCHECK(hipMemsetAsync(t.diags.p + (size_t)np * w, 0, w * 8, s.st));
+}
+// diagonal p of t as plain rows [nqp][N] in dst (device); store the same back
+void lt_diag_get(const LinTrans& t, size_t p, u64* dst) {
+  Scheme& s = sch();
+  const size_t w = lt_diag_words(t);
+  if (!t.packed) { d2d(dst, t.diags.p + p * w, w * 8); return; }
+  launch_unpack_diag(dst, reinterpret_cast<const uint32_t*>(t.diags.p + p * w), t.d_pkrow.p, t.level + 1 + s.K, s.N, s.st);
+}
+void lt_diag_put(LinTrans& t, size_t p, const u64* src, int np = 1) {
+  Scheme& s = sch();
+  const size_t w = lt_diag_words(t), plain = (size_t)(t.level + 1 + s.K) * s.N;
+  if (!t.packed) { d2d(t.diags.p + p * w, src, (size_t)np * w * 8); return; }
+  launch_pack_diags(reinterpret_cast<uint32_t*>(t.diags.p + p * w), t.pk_stride, src, plain, np, t.d_pkrow.p, t.level + 1 + s.K,
+                    s.N, s.st);
+}
+
 int generate_lt(const int* idx, int nidx, const float* data, int ndata, int level, float ratio, bool load_mode) {
   Scheme& s = sch();
   const int N = s.N, slots = N / 2, K = s.K;
@@ -1432,21 +1490,6 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
   }
   const int np = (int)order.size(), nqp_lt = level + 1 + K;
   for (auto& o : order) t->plain_idx.push_back(o.first);
-  if (load_mode) {
-    // io_mode "load" (lineartransform.go:75-84): empty diagonal slots, filled by LoadPlaintextDiagonal
-    t->resident.assign(np, 0);
-  } else {
-    // one extra all-zero plaintext after the np diagonals: absent (group, baby) pairs point at it
-    t->diags = DU64((size_t)(np + 1) * nqp_lt * N);
-    HCHECK(hipMemsetAsync(t->diags.p + (size_t)np * nqp_lt * N, 0, (size_t)nqp_lt * N * 8, s.st));
-    RowMap rm{nqp_lt, level + 1, 0, s.L, 0, 0};
-    // special FFT, fixed point, residues in QP and NTT on the device, then the Montgomery conversion
-    std::vector<EncodeSrc> src(np);
-    for (int p = 0; p < np; p++) src[p] = EncodeSrc{order[p].second, rotv[p]};
-    encode_device(data, (size_t)ndata, src, slots, t->scale, rm, t->diags.p, (size_t)nqp_lt * N);
-    launch_mont_convert(t->diags.p, (size_t)nqp_lt * N, np, rm, s.d_mods.p, N, true, s.st);
-    t->resident.assign(np, 1);
-  }
   if (!t->naive) {
     const int ng = (int)t->giant.size(), nb = (int)t->rot2.size();
     std::vector<int> gpi((size_t)ng * nb, np), bzero(nb, 0), bslot(nb, 0);
@@ -1465,6 +1508,33 @@ int generate_lt(const int* idx, int nidx, const float* data, int ndata, int leve
     t->d_gpi = DevArray<int>(t->gpi.size()); upload(t->d_gpi.p, t->gpi.data(), t->gpi.size());
     t->d_bzero = DevArray<int>(nb); upload(t->d_bzero.p, t->bzero.data(), nb);
     t->d_bslot = DevArray<int>(nb); upload(t->d_bslot.p, t->bslot.data(), nb);
+    // the diagonal MAC's dense 16-baby kernel reads packed diagonals
+    if (t->dense && nb == 16) lt_pack_layout(*t);
+  }
+  if (load_mode) {
+    // io_mode "load" (lineartransform.go:75-84): empty diagonal slots, filled by LoadPlaintextDiagonal
+    t->resident.assign(np, 0);
+  } else {
+    // one extra all-zero plaintext after the np diagonals: absent (group, baby) pairs point at it
+    lt_alloc_diags(*t, np);
+    RowMap rm{nqp_lt, level + 1, 0, s.L, 0, 0};
+    // special FFT, fixed point, residues in QP and NTT on the device, then the
+    // Montgomery conversion; packed transforms encode through a plain staging
+    // buffer of up to 64 diagonals at a time
+    const size_t plain = (size_t)nqp_lt * N;
+    std::vector<EncodeSrc> src(np);
+    for (int p = 0; p < np; p++) src[p] = EncodeSrc{order[p].second, rotv[p]};
+    if (!t->packed) {
+      encode_device(data, (size_t)ndata, src, slots, t->scale, rm, t->diags.p, plain);
+      launch_mont_convert(t->diags.p, plain, np, rm, s.d_mods.p, N, true, s.st);
+    } else {
+      DU64 stage((size_t)std::min(np, 64) * plain);
+      encode_device(data, (size_t)ndata, src, slots, t->scale, rm, stage.p, plain, false, [&](int c0, int n) {
+        launch_mont_convert(stage.p, plain, n, rm, s.d_mods.p, N, true, s.st);
+        lt_diag_put(*t, (size_t)c0, stage.p, n);
+      });
+    }
+    t->resident.assign(np, 1);
   }
   sync();
   int id = s.lt_ids.take();
@@ -1531,7 +1601,8 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct, bool r
   // 3. fused diagonal MAC -> T[g][2][nqp][N]
   DU64 T((size_t)ng * 2 * qp);
   DiagMacArgs dm{};
-  dm.diag = t.diags.p; dm.diag_stride = (size_t)(t.level + 1 + K) * N;
+  dm.diag = t.diags.p; dm.diag_stride = lt_diag_words(t);
+  dm.pkrow = t.packed ? t.d_pkrow.p : nullptr;
   dm.digits = digits.p; dm.bkey = t.d_bkey.p; dm.bperm = t.d_bperm.p; dm.own = c1; dm.dn = dn;
   dm.bka = babies_seeded ? t.d_bka.p : nullptr;
   dm.pc = pc.p; dm.pc_pstride = (size_t)(l + 1) * N;
@@ -1542,6 +1613,7 @@ std::unique_ptr<Cipher> eval_lt_bsgs(const LinTrans& t, const Cipher& ct, bool r
   dm.g0 = 0; dm.g1 = ng;
   check_mac_tables(t);
   REQUIRE(t.diags.p && t.diags.n >= (t.plain_idx.size() + 1) * dm.diag_stride, "linear transform: diagonal storage missing");
+  REQUIRE(t.packed == (t.dense && nb == 16), "linear transform: packed diagonals go with the dense 16-baby kernel");
   for (int b0 = 0; b0 < nb; b0 += 32) {
     dm.b0 = b0; dm.nb_chunk = std::min(32, nb - b0);
     timed("diag_mac", [&] { launch_diag_mac(dm, s.st); });
@@ -2313,7 +2385,9 @@ ArrayResultByte SerializeDiagonal(int transformID, int diagIdx) {
     const size_t p = it - t.plain_idx.begin();
     REQUIRE(t.resident[p], "diagonal not loaded");
     std::vector<u64> h((size_t)nqp * N);
-    download(h.data(), t.diags.p + p * nqp * N, h.size());
+    DU64 tmp((size_t)nqp * N);
+    lt_diag_get(t, p, tmp.p);
+    download(h.data(), tmp.p, h.size());
     Wire w; w.qp(h.data(), t.level + 1, s.K, N);
     r = bytes_result(w.b);
     // as the reference, the serialized diagonal leaves the transform
@@ -2339,12 +2413,11 @@ int LoadPlaintextDiagonal(const unsigned char* data, unsigned long len, int tran
     in.poly(h.data(), t.level + 1, N, mods, 0);
     in.poly(h.data() + (size_t)(t.level + 1) * N, s.K, N, mods, t.level + 1);
     in.end();
-    if (!t.diags.p) {
-      // storage was released with the last diagonal: np plaintexts + the all-zero one
-      t.diags = DU64((size_t)(np + 1) * nqp * N);
-      HCHECK(hipMemsetAsync(t.diags.p + (size_t)np * nqp * N, 0, (size_t)nqp * N * 8, s.st));
-    }
-    upload(t.diags.p + p * nqp * N, h.data(), h.size());
+    // storage was released with the last diagonal: np plaintexts + the all-zero one
+    if (!t.diags.p) lt_alloc_diags(t, np);
+    DU64 tmp((size_t)nqp * N);
+    upload(tmp.p, h.data(), h.size());
+    lt_diag_put(t, p, tmp.p);
     t.resident[p] = 1;
     return 0;
   });
@@ -2508,7 +2581,7 @@ int ExportLinearTransformDiagonal(int ltID, int diag, uint64_t* buf, size_t len)
     REQUIRE(it != t.plain_idx.end(), "diagonal not stored");
     size_t p = it - t.plain_idx.begin(), n = (size_t)(t.level + 1 + s.K) * s.N;
     REQUIRE(len >= n, "buffer too small");
-    DU64 tmp(n); d2d(tmp.p, t.diags.p + p * n, n * 8);
+    DU64 tmp(n); lt_diag_get(t, p, tmp.p);
     launch_mont_convert(tmp.p, 0, 1, RowMap{t.level + 1 + s.K, t.level + 1, 0, s.L, 0, 0}, s.d_mods.p, s.N, false, s.st);
     download(buf, tmp.p, n);
     return (int)(n / s.N);
