@@ -39,8 +39,12 @@ def mac_unit_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, w=8):
 KEY_PARTS = 1
 
 
+# a diagonal row stored packed (modulus below 2^52) holds 64 words in 104 of 128 dwords
+PACKED_ROW_FRACTION = 104 / 128
+
+
 def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=8, chunks=1, fused_babies=True,
-                      key_parts=KEY_PARTS):
+                      key_parts=KEY_PARTS, packed_rows=0):
     """Per-PCMM and per-diag-MAC-launch algorithmic HBM bytes (every word once).
 
     PCMM: the diagonals, the read parts of each of the R rotation keys, the
@@ -49,16 +53,19 @@ def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=
     and P*c (2 Q polys, baby step 0) read, one QP accumulator pair per giant
     group of the launch written, and the n1-1 hoisted baby rotations --
     computed in the kernel's prologue from their keys (dnum*key_parts QP polys each)
+    and with packed_rows of the (L+K) diagonal rows stored packed (dense
+    16-baby transforms: the rows of moduli below 2^52)
     and the decomposed input (dnum QP polys, once) when fused_babies, else
     read (2 QP polys each).  mac_unit_bytes is the per-unit definition the
     roofline is quoted on."""
     R = (n1 - 1) + (n2 - 1) + f
-    pcmm = D * (L + K) * N * w + R * dnum * key_parts * (L + K) * N * w + 2 * L * N * w + 2 * (L - 1) * N * w
+    diag_rows = (L + K) - packed_rows * (1 - PACKED_ROW_FRACTION)
+    pcmm = int(D * diag_rows * N * w) + R * dnum * key_parts * (L + K) * N * w + 2 * L * N * w + 2 * (L - 1) * N * w
     if fused_babies:
         babies = (n1 - 1) * dnum * key_parts * (L + K) * N * w + (dnum * (L + K) * N * w if n1 > 1 else 0)
     else:
         babies = (n1 - 1) * 2 * (L + K) * N * w
-    diag_mac = (D * (L + K) * N * w + n2 * 2 * (L + K) * N * w) // chunks + babies + 2 * L * N * w
+    diag_mac = int(D * diag_rows * N * w + n2 * 2 * (L + K) * N * w) // chunks + babies + 2 * L * N * w
     return pcmm, diag_mac
 
 
@@ -261,8 +268,11 @@ def lt_roofline_bytes(lib, layer, N, K, w=8):
     tid = list(layer.transform_ids.values())[0]
     lti = lib.lt_info(tid)
     Lq = layer.level + 1
+    # dense 16-baby transforms keep the rows of moduli below 2^52 packed
+    dense16 = lti["baby"] == 16 and lti["plaintexts"] == lti["baby"] * lti["giant"]
+    packed = sum(1 for qq in lib.GetModuliChain()[:Lq] if qq < (1 << 52)) if dense16 else 0
     return algorithmic_bytes(N=N, L=Lq, K=K, D=lti["plaintexts"], n1=lti["baby"], n2=lti["giant"],
-                             f=layer.output_rotations, dnum=(Lq + K - 1) // K, w=w), lti
+                             f=layer.output_rotations, dnum=(Lq + K - 1) // K, w=w, packed_rows=packed), lti
 
 
 def cpu_model():
@@ -575,12 +585,13 @@ def main():
     roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": (achieved / HBM_PEAK_GBS) if achieved else None,
                 "traffic": read_traffic("diag_mac") if args.workload == "pcmm26" else None,
-                "kernel": "diag_mac_kernel", "algorithmic_bytes_per_launch": unit_per_launch,
+                "kernel": "diag_mac_d16_kernel", "algorithmic_bytes_per_launch": unit_per_launch,
                 "launches_per_step": launches,
                 "definition": "D*(L+K)*N*w diagonals + 2*n1*(L+K)*N*w + 2*n2*(L+K)*N*w baby- and giant-step QP polynomials",
                 "kernel_count": {"algorithmic_bytes_per_launch": mac_per_launch, "achieved": achieved_k,
                                  "frac": (achieved_k / HBM_PEAK_GBS) if achieved_k else None,
-                                 "definition": ("diagonals, the b halves of the hoisted baby rotations' keys (the a halves "
+                                 "definition": ("diagonals (rows of moduli below 2^52 packed, 104 of 128 dwords), the b "
+                                                "halves of the hoisted baby rotations' keys (the a halves "
                                                 "regenerated from their seed) and the decomposed input (the "
                                                 "rotations computed in the prologue), P*c, one QP accumulator "
                                                 "pair per giant group")}}

@@ -36,6 +36,10 @@ def test_pcmm26_algorithmic_bytes():
     pcmm2, mac2 = bench.algorithmic_bytes(key_parts=2)
     assert pcmm2 - pcmm == 52 * 3 * nqp * N * w
     assert mac2 == 11_249_123_328
+    # the 23 rows of 50-bit moduli stored packed: 104 of 128 dwords per 64 words
+    pcmm3, mac3 = bench.algorithmic_bytes(packed_rows=23)
+    assert pcmm - pcmm3 == mac - mac3 == 512 * 23 * (N // 64) * (128 - 104) * 4
+    assert mac3 == 9_336_520_704
     _, unfused = bench.algorithmic_bytes(fused_babies=False)
     assert unfused == 10_192_158_720
     assert unfused == 512 * nqp * N * w + 15 * 2 * nqp * N * w + 2 * 24 * N * w + 32 * 2 * nqp * N * w

@@ -166,3 +166,71 @@ def test_diagonal_save_load_round_trip(hip_lib, primes):
     out2 = hip_lib.export_ciphertext(hip_lib.EvaluateLinearTransform(tid, ct))
     assert_equal_u64(out2, out1, "transform after save / remove / load")
     hip_lib.DeleteScheme()
+
+
+def _wire_poly(rows):
+    """ring.Poly in the library's wire format (the layout parse_wire_poly reads)."""
+    parts = [np.array([rows.shape[0]], dtype="<u8").tobytes()]
+    for r in rows:
+        parts.append(np.array([rows.shape[1]], dtype="<u8").tobytes())
+        parts.append(np.ascontiguousarray(r, dtype="<u8").tobytes())
+    return b"".join(parts)
+
+
+def test_packed_diagonal_storage_edges(hip_lib):
+    """A dense 16-baby transform keeps its diagonals packed on the device
+    (rows of moduli below 2^52 as 52-bit fields, the 60- and 61-bit rows as
+    plain words).  Diagonals made of edge words -- every word q - 1, zeros,
+    alternating 0 / q - 1, single high bits, a ramp -- are loaded, then read
+    back through serialization and export byte for byte, and the transform
+    still evaluates bit-exactly as before once its own diagonals are back."""
+    logn = 11
+    N, S = 1 << logn, 1 << (logn - 1)
+    q, p = make_params(logn, [60, 50, 50, 50, 50], [61])
+    L, K = len(q), len(p)
+    level = L - 1
+    mods = list(q) + list(p)
+    assert max(q[1:]) < (1 << 52) <= q[0] and p[0] >= (1 << 52)
+    print("[serialize] packed diagonal edges", flush=True)
+    new_hip_scheme(hip_lib, logn, q, p, 40, 64, 17)
+    rng = np.random.default_rng(21)
+    idx = list(range(256))
+    data = rng.uniform(-1, 1, (len(idx), S)).astype(np.float32)
+    tid = hip_lib.GenerateLinearTransform(idx, data.reshape(-1).tolist(), level, 2.0, "none")
+    info = hip_lib.lt_info(tid)
+    assert info["baby"] == 16 and info["giant"] * 16 == info["plaintexts"], info  # the packed (dense 16-baby) layout
+    for ge in hip_lib.GetLinearTransformRotationKeys(tid):
+        hip_lib.GenerateLinearTransformRotationKey(ge)
+    vals = rng.uniform(-1, 1, S).astype(np.float32)
+    ct = hip_lib.Encrypt(hip_lib.Encode(vals.tolist(), level, 1 << 40))
+    out1 = hip_lib.export_ciphertext(hip_lib.EvaluateLinearTransform(tid, ct))
+    own = {}
+    for d in (0, 7, 255):
+        blob, ptr = hip_lib.SerializeDiagonal(tid, d)
+        hip_lib.FreeCArray(ptr)
+        own[d] = bytes(blob)
+    i = np.arange(N, dtype=np.uint64)
+    patterns = {
+        "all_q-1": lambda qq: np.full(N, qq - 1, dtype=np.uint64),
+        "zeros": lambda qq: np.zeros(N, dtype=np.uint64),
+        "alternating": lambda qq: np.where(i % 2 == 1, np.uint64(qq - 1), np.uint64(0)),
+        "high_bits": lambda qq: np.uint64(1) << (i % np.uint64(int(qq).bit_length() - 1)),
+        "ramp": lambda qq: (i * np.uint64(0x9E3779B97F4A7C15 % int(qq))) % np.uint64(qq),
+    }
+    for name, f in patterns.items():
+        rows = np.stack([f(int(m)) for m in mods[:level + 1] + list(p)])
+        assert all((rows[r] < np.uint64(mods[r] if r <= level else p[r - level - 1])).all() for r in range(rows.shape[0]))
+        blob = _wire_poly(rows[:level + 1]) + _wire_poly(rows[level + 1:])
+        for d in (0, 7, 255):
+            assert hip_lib.LoadPlaintextDiagonal(blob, tid, d) == 0
+            got = hip_lib.export_lt_diagonal(tid, d, level)
+            assert_equal_u64(np.asarray(got).reshape(-1, N), from_montgomery(rows, mods[:level + 1] + list(p)),
+                             f"export {name} diagonal {d}")
+            back, ptr = hip_lib.SerializeDiagonal(tid, d)
+            hip_lib.FreeCArray(ptr)
+            assert bytes(back) == blob, f"{name}: diagonal {d} bytes after the packed round trip"
+    for d in (0, 7, 255):
+        assert hip_lib.LoadPlaintextDiagonal(own[d], tid, d) == 0
+    out2 = hip_lib.export_ciphertext(hip_lib.EvaluateLinearTransform(tid, ct))
+    assert_equal_u64(out2, out1, "transform with its own diagonals back")
+    hip_lib.DeleteScheme()
