@@ -1194,16 +1194,7 @@ static int find_best_bsgs_ratio(const int* diags, int nd, int maxN, int logMaxRa
 }
 static int lt_find(const orc_lt* t, int di) { for (int i = 0; i < t->nplain; i++) if (t->plain_idx[i] == di) return i; return -1; }
 
-static orc_lt* lt_new_impl(orc_ctx* c, const int* idx, int nidx, const float* data, int level, float bsgs_ratio, int max_groups);
 orc_lt* orc_lt_new(orc_ctx* c, const int* idx, int nidx, const float* data, int level, float bsgs_ratio) {
-    return lt_new_impl(c, idx, nidx, data, level, bsgs_ratio, -1);
-}
-/* Bounded CPU-baseline sample: the full BSGS structure, but only the
- * plaintexts of giant groups [0, max_groups) are encoded. */
-orc_lt* orc_lt_new_groups(orc_ctx* c, const int* idx, int nidx, const float* data, int level, float bsgs_ratio, int max_groups) {
-    return lt_new_impl(c, idx, nidx, data, level, bsgs_ratio, max_groups);
-}
-static orc_lt* lt_new_impl(orc_ctx* c, const int* idx, int nidx, const float* data, int level, float bsgs_ratio, int max_groups) {
     int N = c->N, slots = N / 2, K = c->K, nqp = level + 1 + K;
     orc_lt* t = (orc_lt*)xcalloc(sizeof(orc_lt));
     t->level = level; t->slots = slots;
@@ -1240,7 +1231,6 @@ static orc_lt* lt_new_impl(orc_ctx* c, const int* idx, int nidx, const float* da
          * then the encodings, independent of each other, in parallel */
         int* srcs = (int*)xmalloc(sizeof(int) * (nidx + 1)); int* rotp = (int*)xmalloc(sizeof(int) * (nidx + 1));
         for (int g = 0; g < t->ngiant; g++) {
-            if (max_groups >= 0 && g >= max_groups) break;
             int j = t->giant[g]; int rot = (-j) & (slots - 1);
             for (int bi = 0; bi < t->nbaby[g]; bi++) {
                 int di = j + t->baby[g][bi], src = -1;

@@ -115,8 +115,6 @@ void orc_basis_extend(const orc_ctx* c, const int* src, int ns, const int* dst,
 /* ---- linear transform (BSGS diagonal evaluation) ------------------------ */
 orc_lt* orc_lt_new(orc_ctx* c, const int* idx, int nidx, const float* data,
                    int level, float bsgs_ratio);
-orc_lt* orc_lt_new_groups(orc_ctx* c, const int* idx, int nidx, const float* data,
-                          int level, float bsgs_ratio, int max_groups);
 void    orc_lt_free(orc_lt* t);
 int     orc_lt_n1(const orc_lt* t);
 int     orc_lt_level(const orc_lt* t);

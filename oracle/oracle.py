@@ -76,7 +76,6 @@ def lib():
             "orc_decompose_modup": ([vp, ctypes.c_int, u64p, u64p], None),
             "orc_basis_extend": ([vp, intp, ctypes.c_int, intp, ctypes.c_int, u64p, u64p], None),
             "orc_lt_new": ([vp, intp, ctypes.c_int, fp, ctypes.c_int, ctypes.c_float], vp),
-            "orc_lt_new_groups": ([vp, intp, ctypes.c_int, fp, ctypes.c_int, ctypes.c_float, ctypes.c_int], vp),
             "orc_lt_free": ([vp], None),
             "orc_lt_n1": ([vp], ctypes.c_int),
             "orc_lt_level": ([vp], ctypes.c_int),
@@ -395,14 +394,6 @@ class Oracle:
         d = np.ascontiguousarray(np.asarray(data, dtype=np.float32).reshape(-1))
         ia = (ctypes.c_int * len(idx))(*idx)
         t = lib().orc_lt_new(self.ctx, ia, len(idx), _p(d, fp), level, ctypes.c_float(bsgs_ratio))
-        self.lts.append(t)
-        return t
-
-    def lt_new_groups(self, idx, data, level, bsgs_ratio, max_groups):
-        idx = list(idx)
-        d = np.ascontiguousarray(np.asarray(data, dtype=np.float32).reshape(-1))
-        ia = (ctypes.c_int * len(idx))(*idx)
-        t = lib().orc_lt_new_groups(self.ctx, ia, len(idx), _p(d, fp), level, ctypes.c_float(bsgs_ratio), int(max_groups))
         self.lts.append(t)
         return t
 

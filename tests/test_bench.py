@@ -96,6 +96,7 @@ def test_keyswitch_pass_rows():
 def test_measured_step_traffic():
     """The whole-PCMM traffic of the committed PMC summary, as a rate at a step time."""
     r = bench.measured_step_traffic("pcmm26", 7.0)
-    assert r["measured_traffic_bytes"] > 30e9
+    # the key switches' passes move more than the algorithmic bytes
+    assert r["measured_traffic_bytes"] > 2 * bench.algorithmic_bytes(packed_rows=23)[0]
     assert abs(r["measured_traffic_GBs"] - r["measured_traffic_bytes"] / 7e-3 / 1e9) < 1e-6
     assert bench.measured_step_traffic("dlrm", 7.0) == {}
