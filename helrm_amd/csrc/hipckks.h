@@ -189,6 +189,65 @@ __device__ __forceinline__ void acc61_value(const Acc61& A, u64& lo, u64& hi) {
   lo = A.s0 + t;
   hi = A.s2 + A.c0 + (s1 >> 32) + (s1c << 32) + (lo < t ? 1 : 0);
 }
+// REDC(value of A) - sub mod q for an Acc61 whose value is below q * 2^64
+// (8 products of words below 2^61 and a column bound kept by the caller), sub
+// < q: the columns are combined, reduced and corrected in 32-bit carry
+// chains (about 33 VALU instructions where the 64-bit form takes ~47):
+//   s1 = s1a + s1b (carry s1c); lo = s0 + s1 * 2^32 (carry c1);
+//   hi = s2 + s1 / 2^32 + s1c * 2^32 + c0 + c1;
+//   m = lo * qinv mod 2^64 (qinv = -q^-1); t = hi + mulhi(m, q) + (lo != 0);
+//   r = t >= q ? t - q : t;  result = r - sub (+ q if it borrows).
+__device__ __forceinline__ u64 acc61_redc_sub(const Acc61& A, u64 q, u64 qinv, u64 sub) {
+  uint32_t lol, loh, hil, hih;
+  {
+    uint32_t s1l, s1h;
+    u64 k0, k1, k2, k3, s1c, c1;
+    asm("v_add_co_u32_e64 %[s1l], %[k0], %[al], %[bl]\n\t"
+        "v_addc_co_u32_e64 %[s1h], %[s1c], %[ah], %[bh], %[k0]\n\t"
+        "v_add_co_u32_e64 %[loh], %[c1], %[s0h], %[s1l]\n\t"
+        "v_add_co_u32_e64 %[hil], %[k1], %[s2l], %[s1h]\n\t"
+        "v_addc_co_u32_e64 %[hih], %[k1], %[s2h], 0, %[k1]\n\t"
+        "v_addc_co_u32_e64 %[hih], %[k1], %[hih], 0, %[s1c]\n\t"
+        "v_add_co_u32_e64 %[hil], %[k2], %[hil], %[c0]\n\t"
+        "v_addc_co_u32_e64 %[hih], %[k2], %[hih], 0, %[k2]\n\t"
+        "v_addc_co_u32_e64 %[hil], %[k3], %[hil], 0, %[c1]\n\t"
+        "v_addc_co_u32_e64 %[hih], %[k3], %[hih], 0, %[k3]"
+        : [s1l] "=&v"(s1l), [s1h] "=&v"(s1h), [loh] "=&v"(loh), [hil] "=&v"(hil), [hih] "=&v"(hih),
+          [k0] "=&s"(k0), [k1] "=&s"(k1), [k2] "=&s"(k2), [k3] "=&s"(k3), [s1c] "=&s"(s1c), [c1] "=&s"(c1)
+        : [al] "v"((uint32_t)A.s1a), [ah] "v"((uint32_t)(A.s1a >> 32)), [bl] "v"((uint32_t)A.s1b),
+          [bh] "v"((uint32_t)(A.s1b >> 32)), [s0h] "v"((uint32_t)(A.s0 >> 32)), [s2l] "v"((uint32_t)A.s2),
+          [s2h] "v"((uint32_t)(A.s2 >> 32)), [c0] "v"(A.c0));
+    lol = (uint32_t)A.s0;
+  }
+  const u64 lo = ((u64)loh << 32) | lol;
+  // m = lo * qinv mod 2^64
+  const uint32_t ql = (uint32_t)q, qh = (uint32_t)(q >> 32), il = (uint32_t)qinv, ih = (uint32_t)(qinv >> 32);
+  const u64 p0 = (u64)lol * il;
+  const uint32_t mh = (uint32_t)(p0 >> 32) + lol * ih + loh * il;
+  const u64 m = ((u64)mh << 32) | (uint32_t)p0;
+  const u64 mq = mulhi64(m, q);
+  uint32_t tl, th, rl, rh, dl, dh;
+  u64 cz, k4, b0, b1;
+  // t = hi + mq + (lo != 0); r = t - q unless that borrows; d = r - sub, + q if that borrows
+  asm("v_cmp_ne_u64_e64 %[cz], 0, %[lo]\n\t"
+      "v_addc_co_u32_e64 %[tl], %[k4], %[hil], %[mql], %[cz]\n\t"
+      "v_addc_co_u32_e64 %[th], %[k4], %[hih], %[mqh], %[k4]\n\t"
+      "v_sub_co_u32_e64 %[rl], %[b0], %[tl], %[ql]\n\t"
+      "v_subb_co_u32_e64 %[rh], %[b0], %[th], %[qh], %[b0]\n\t"
+      "v_cndmask_b32_e64 %[rl], %[rl], %[tl], %[b0]\n\t"
+      "v_cndmask_b32_e64 %[rh], %[rh], %[th], %[b0]\n\t"
+      "v_sub_co_u32_e64 %[dl], %[b1], %[rl], %[sl]\n\t"
+      "v_subb_co_u32_e64 %[dh], %[b1], %[rh], %[sh], %[b1]\n\t"
+      "v_cndmask_b32_e64 %[tl], 0, %[ql], %[b1]\n\t"
+      "v_cndmask_b32_e64 %[th], 0, %[qh], %[b1]\n\t"
+      "v_add_co_u32_e64 %[dl], %[k4], %[dl], %[tl]\n\t"
+      "v_addc_co_u32_e64 %[dh], %[k4], %[dh], %[th], %[k4]"
+      : [tl] "=&v"(tl), [th] "=&v"(th), [rl] "=&v"(rl), [rh] "=&v"(rh), [dl] "=&v"(dl), [dh] "=&v"(dh),
+        [cz] "=&s"(cz), [k4] "=&s"(k4), [b0] "=&s"(b0), [b1] "=&s"(b1)
+      : [lo] "v"(lo), [hil] "v"(hil), [hih] "v"(hih), [mql] "v"((uint32_t)mq), [mqh] "v"((uint32_t)(mq >> 32)),
+        [ql] "v"(ql), [qh] "v"(qh), [sl] "v"((uint32_t)sub), [sh] "v"((uint32_t)(sub >> 32)));
+  return ((u64)dh << 32) | dl;
+}
 // the 128-bit value (lo, hi) of an accumulator
 __device__ __forceinline__ void acc_value(const Acc128& A, u64& lo, u64& hi) {
   const u64 t = A.s1 << 32;

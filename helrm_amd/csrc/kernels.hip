@@ -288,9 +288,7 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
         else if (i == 4) acc61_first_half_s(A, y[i], h[i]);
         else acc61_mac_s<1>(A, y[i], h[i]);
       }
-      u64 lo, hi;
-      acc61_value(A, lo, hi);
-      res = redc(lo, hi, mc.q, mc.qinv);
+      res = acc61_redc_sub(A, mc.q, mc.qinv, svs[(r - r0) * (ns + 1) + v]);
     } else {
       u128 acc = 0;
 #pragma unroll
@@ -305,8 +303,8 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
         acc += ((u128)fold_hi4(hi, mc.q) << 64) | lo;
       }
       res = redc((u64)acc, fold_hi4((u64)(acc >> 64), mc.q), mc.q, mc.qinv);
+      res = sub_mod(res, svs[(r - r0) * (ns + 1) + v], mc.q);
     }
-    res = sub_mod(res, svs[(r - r0) * (ns + 1) + v], mc.q);
     outb[(size_t)row * N + x] = res;
   }
 }
@@ -381,10 +379,7 @@ __global__ __launch_bounds__(256) void bconv_lds_kernel(const u64* __restrict__ 
       else if (i == 4) acc61_first_half_s(A, y[i], h[i]);
       else acc61_mac_s<1>(A, y[i], h[i]);
     }
-    u64 lo, hi;
-    acc61_value(A, lo, hi);
-    const u64 res = redc(lo, hi, mc.q, mc.qinv);
-    outb[(size_t)row * N + x] = sub_mod(res, svs[r * (ns + 1) + v], mc.q);
+    outb[(size_t)row * N + x] = acc61_redc_sub(A, mc.q, mc.qinv, svs[r * (ns + 1) + v]);
   }
 }
 void launch_bconv(const u64* in, size_t in_bstride, BConvJobs jobs, u64* out, size_t out_bstride, int batch,
