@@ -437,6 +437,38 @@ def copy_calibration(mib):
                       "copy_GBs": 2 * n * 8 / (ms / 1000.0) / 1e9}), flush=True)
 
 
+def hbm_ceiling(gib_list=(1, 4)):
+    """The streaming rates plain torch kernels reach on this GPU, for reading
+    the roofline fractions against what a copy achieves: a device copy (read +
+    write), a fill (write only) and a sum (read only) of 1 and 4 GiB of
+    int64, 5 launches each after one untimed, HIP events on torch's stream.
+    One JSON line per size."""
+    import torch
+
+    def per_launch_s(f, reps=5):
+        f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps / 1000.0
+
+    for gib in gib_list:
+        n = gib * (1 << 30) // 8
+        a = torch.ones(n, dtype=torch.int64, device="cuda")
+        b = torch.empty_like(a)
+        cp = per_launch_s(lambda: b.copy_(a))
+        fl = per_launch_s(lambda: b.fill_(3))
+        sm = per_launch_s(lambda: torch.sum(a))
+        print(json.dumps({"hbm_ceiling_GiB": gib, "copy_rw_GBs": 2 * n * 8 / cp / 1e9,
+                          "fill_w_GBs": n * 8 / fl / 1e9, "sum_r_GBs": n * 8 / sm / 1e9}), flush=True)
+        del a, b
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -462,9 +494,14 @@ def main():
                          "(embedding PCMM workloads; 0: skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (PMC counter calibration) and exit")
+    ap.add_argument("--hbm-ceiling", action="store_true",
+                    help="only measure the copy / fill / sum rates of plain torch kernels over 1 and 4 GiB and exit")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.hbm_ceiling:
+        hbm_ceiling()
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -248,6 +248,22 @@ __device__ __forceinline__ u64 acc61_redc_sub(const Acc61& A, u64 q, u64 qinv, u
         [ql] "v"(ql), [qh] "v"(qh), [sl] "v"((uint32_t)sub), [sh] "v"((uint32_t)(sub >> 32)));
   return ((u64)dh << 32) | dl;
 }
+// One destination word of a basis extension from at most 8 sources:
+// REDC(sum_i y(i) * h[i]) - sub mod q, y(i) < 2^61 (zero past the job's
+// sources) and h[i] < q the row's table words (Montgomery form, read for all
+// 8 i: the table holds spare words past its last row).
+template <class Y>
+__device__ __forceinline__ u64 bconv_word8(Y y, const u64* __restrict__ h, u64 q, u64 qinv, u64 sub) {
+  Acc61 A;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    if (i == 0) acc61_first_s(A, y(i), h[i]);
+    else if (i < 4) acc61_mac_s<0>(A, y(i), h[i]);
+    else if (i == 4) acc61_first_half_s(A, y(i), h[i]);
+    else acc61_mac_s<1>(A, y(i), h[i]);
+  }
+  return acc61_redc_sub(A, q, qinv, sub);
+}
 // the 128-bit value (lo, hi) of an accumulator
 __device__ __forceinline__ void acc_value(const Acc128& A, u64& lo, u64& hi) {
   const u64 t = A.s1 << 32;

@@ -279,16 +279,8 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
     u64 res;
     if (MAXS <= 8) {
       // y[i] < q_i < 2^61 and h[i] < q < 2^61: 8 products sum below 2^64 q,
-      // so hi < q as the REDC needs
-      Acc61 A;
-#pragma unroll
-      for (int i = 0; i < MAXS; i++) {  // y[i] = 0 past ns
-        if (i == 0) acc61_first_s(A, y[i], h[i]);
-        else if (i < 4) acc61_mac_s<0>(A, y[i], h[i]);
-        else if (i == 4) acc61_first_half_s(A, y[i], h[i]);
-        else acc61_mac_s<1>(A, y[i], h[i]);
-      }
-      res = acc61_redc_sub(A, mc.q, mc.qinv, svs[(r - r0) * (ns + 1) + v]);
+      // so hi < q as the REDC needs (y[i] = 0 past ns)
+      res = bconv_word8([&](int i) { return y[i]; }, h, mc.q, mc.qinv, svs[(r - r0) * (ns + 1) + v]);
     } else {
       u128 acc = 0;
 #pragma unroll
@@ -371,15 +363,7 @@ __global__ __launch_bounds__(256) void bconv_lds_kernel(const u64* __restrict__ 
     const int m = rm.mod(row);
     const ModC mc = mods[m];
     const u64* __restrict__ h = hat + (size_t)m * ns;
-    Acc61 A;
-#pragma unroll
-    for (int i = 0; i < MAXS; i++) {  // y[i] = 0 past ns
-      if (i == 0) acc61_first_s(A, y[i], h[i]);
-      else if (i < 4) acc61_mac_s<0>(A, y[i], h[i]);
-      else if (i == 4) acc61_first_half_s(A, y[i], h[i]);
-      else acc61_mac_s<1>(A, y[i], h[i]);
-    }
-    outb[(size_t)row * N + x] = acc61_redc_sub(A, mc.q, mc.qinv, svs[r * (ns + 1) + v]);
+    outb[(size_t)row * N + x] = bconv_word8([&](int i) { return y[i]; }, h, mc.q, mc.qinv, svs[r * (ns + 1) + v]);
   }
 }
 void launch_bconv(const u64* in, size_t in_bstride, BConvJobs jobs, u64* out, size_t out_bstride, int batch,
