@@ -69,6 +69,17 @@ def algorithmic_bytes(N=1 << 16, L=24, K=8, D=512, n1=16, n2=32, f=6, dnum=3, w=
     return pcmm, diag_mac
 
 
+def keyswitch_rotation_bytes(level, K, N=1 << 16, w=8, key_parts=KEY_PARTS):
+    """Algorithmic bytes of one single key switch (a rotation) at `level`:
+    the key (dnum digits x key_parts halves), the dnum decomposed digits and
+    the two output parts, each a QP polynomial of level + 1 + K rows.
+    key_parts=2 is the per-unit definition (whole keys read); the library
+    reads only the b halves of the keys it generated (KEY_PARTS)."""
+    nqp = level + 1 + K
+    dn = (nqp - 1) // K
+    return (dn * key_parts + dn + 2) * nqp * N * w
+
+
 def keyswitch_pass_rows(level, K, fold_add=False, key_parts=KEY_PARTS):
     """Rows of N words that one single key switch at `level` moves, pass by
     pass (a transform is 2 passes, each reading and writing its limb);
@@ -650,17 +661,19 @@ def main():
     # the single-ciphertext key switch: the fold's rotations (one key switch
     # each at the transform's output level, the fold's add inside its last
     # pass) against the per-rotation bytes
-    # key dnum*KEY_PARTS*(l+1+K)*N*w + digits dnum*(l+1+K)*N*w + output 2*(l+1+K)*N*w
     if kt["rotate"]["launches"] and len(layers) == 1:
         lf = layers[0].level - 1  # the fold runs on the rescaled transform output
         nqp, dn = lf + 1 + K, (lf + 1 + K - 1) // K
-        rb = (dn * KEY_PARTS + dn + 2) * nqp * N * 8
+        rb = keyswitch_rotation_bytes(lf, K, N)
         r_ms = kt["rotate"]["avg_ms"]
         pb = sum(keyswitch_pass_rows(lf, K, fold_add=True).values()) * N * 8
+        # the per-unit definition counts whole keys (both halves read)
+        ub = keyswitch_rotation_bytes(lf, K, N, key_parts=2)
         kernel_rooflines["keyswitch_rotation"] = {
             "level": lf, "algorithmic_bytes_per_rotation": rb, "avg_ms": r_ms,
             "rotations_per_step": kt["rotate"]["launches"] / nprof,
             "achieved_GBs": rb / (r_ms / 1000.0) / 1e9, "frac": rb / (r_ms / 1000.0) / 1e9 / HBM_PEAK_GBS,
+            "per_unit_bytes_per_rotation": ub, "per_unit_frac": ub / (r_ms / 1000.0) / 1e9 / HBM_PEAK_GBS,
             "pass_bytes_per_rotation": pb, "pass_GBs": pb / (r_ms / 1000.0) / 1e9,
             "pass_frac": pb / (r_ms / 1000.0) / 1e9 / HBM_PEAK_GBS}
         # the floor the rotation's 11 dependent launches sit on: an empty

@@ -74,6 +74,17 @@ def test_keyswitch_bytes_without_rotations(lq, nb, ng):
         assert baby == ((lq + 7) // 8) * (lq + 8) * (1 << 13) * 8 + lq * (1 << 13) * 8
 
 
+def test_keyswitch_rotation_bytes():
+    """One rotation at level 22 of the 24-limb chain (23 Q + 8 P rows of 2^16
+    words, 3 digits): whole keys 3 x 2 x 31 rows, digits 3 x 31, output
+    2 x 31 = 341 rows of 512 KiB = 178,782,208 B by the per-unit definition;
+    with the b halves only (a halves regenerated), 248 rows."""
+    assert bench.keyswitch_rotation_bytes(22, 8, key_parts=2) == 341 * (1 << 16) * 8 == 178_782_208
+    assert bench.keyswitch_rotation_bytes(22, 8, key_parts=1) == 248 * (1 << 16) * 8 == 130_023_424
+    # a smaller chain: level 3, K = 1 -> 5 QP rows, 4 digits
+    assert bench.keyswitch_rotation_bytes(3, 1, N=1 << 13, key_parts=2) == (4 * 2 + 4 + 2) * 5 * (1 << 13) * 8
+
+
 def test_keyswitch_pass_rows():
     """One rotation at level 22 (23 Q limbs, K=8, 3 digits of 8, 8, 7 rows):
     inverse NTT of 23 limbs (92 rows), extension 23 -> 70 rows (93), forward
