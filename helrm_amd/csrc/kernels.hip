@@ -308,6 +308,10 @@ __global__ __launch_bounds__(256) void bconv_kernel(const u64* __restrict__ in, 
 // every fourth destination row -- four times the waves for the same work.
 // The overflow count sums y_i / s_i in source order, as the one-thread form.
 constexpr int BCL_X = 64;
+// launches of fewer one-coefficient-per-thread workgroups than this take the shared-source form
+#ifndef BCL_MAX_BLOCKS
+#define BCL_MAX_BLOCKS 2048
+#endif
 __global__ __launch_bounds__(256) void bconv_lds_kernel(const u64* __restrict__ in, size_t in_bstride, BConvJobs jobs,
                                                        u64* __restrict__ out, size_t out_bstride,
                                                        const ModC* __restrict__ mods, int N) {
@@ -378,7 +382,7 @@ void launch_bconv(const u64* in, size_t in_bstride, BConvJobs jobs, u64* out, si
   // all destination rows in one thread unless that leaves too few workgroups
   const int cols = N / 256;
   // a launch of at most a few waves per SIMD: the shared-source form
-  if (nsmax <= 8 && N % BCL_X == 0 && (long)cols * batch * jobs.n < 2048) {
+  if (nsmax <= 8 && N % BCL_X == 0 && (long)cols * batch * jobs.n < BCL_MAX_BLOCKS) {
     hipLaunchKernelGGL(bconv_lds_kernel, dim3(N / BCL_X, 1, batch * jobs.n), dim3(256), 0, st, in, in_bstride, jobs, out,
                        out_bstride, mods, N);
     return;
