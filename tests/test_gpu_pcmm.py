@@ -4,15 +4,16 @@ transform -> rescale -> hybrid fold -> bias -> decrypt -> decode.
 
 * single_table, pcmm26_n13 and the ragged selector: the output ciphertext is
   bit-exact with the same flow run on the CPU restatement (oracle/);
-* pcmm26 (N=2^16): bit-exact with the oracle's words through committed
-  per-row SHA-256 digests (tests/golden/make_fullsize_digests.py).
+* pcmm26 and pcmm26 + sparse_to_top (N=2^16): bit-exact with the oracle's
+  words through committed per-row SHA-256 digests
+  (tests/golden/make_fullsize_digests.py).
 * every config: decrypted embeddings within 2^-20 of the fp32 plaintext
   lookup (tolerance from the task statement).
 """
 import numpy as np
 import pytest
 
-from helpers import assert_equal_u64, check_fullsize_layer, fullsize_digests, oracle_linear, oracle_pcmm
+from helpers import assert_equal_u64, assert_rows_match, check_fullsize_layer, fullsize_digests, oracle_linear, oracle_pcmm
 from oracle import oracle as O
 from helrm_amd.workloads import PCMMWorkload, SparseToTopWorkload
 
@@ -190,13 +191,33 @@ def test_sparse_to_top_bitexact_vs_oracle(hip_lib):
     hip_lib.DeleteScheme()
 
 
-def test_sparse_to_top_full_size_decrypts(hip_lib):
+def test_sparse_to_top_full_size_bitexact(hip_lib):
+    """HELRM.sparse then HELRM.sparse_to_top at N=2^16 (dlrm.py:226-230): the
+    PCMM output and the repack output match the oracle's words row for row
+    (SHA-256 digests written by tests/golden/make_fullsize_digests.py); the
+    416 embeddings decrypt at slots [16, 432) within 2^-20 and slots [0, 16)
+    stay empty."""
+    d = fullsize_digests("pcmm26_top")
     print("[pcmm] pcmm26_top (N=2^16): building", flush=True)
     w = SparseToTopWorkload(hip_lib, "pcmm26_top", seed=3, key_seed=17).setup()
     info = w.shape_info()
     print(f"[pcmm] pcmm26_top: {info}", flush=True)
     assert info["repack"]["diagonals"] == 1 and info["repack"]["output_rotations"] == 6
-    out = w.run()
+    assert hip_lib.GetModuliChain() == d["q"] and hip_lib.GetAuxModuliChain() == d["p"]
+    assert sorted(int(i) for i in w.repack.diagonals[(0, 0)].keys()) == d["repack_diagonals"]
+    assert w.repack.output_rotations == d["repack_rotations"]
+    emb = w.layer.forward(w.ct_in)
+    eid = emb.ids[0]
+    assert hip_lib.GetCiphertextLevel(eid) == d["pcmm_out"]["level"]
+    assert hip_lib.GetCiphertextScaleDouble(eid) == d["pcmm_out"]["scale"]
+    assert_rows_match(hip_lib.export_ciphertext(eid), d["pcmm_out"]["rows"], "pcmm26_top PCMM output")
+    out = w.repack.forward(emb)
+    emb.free()
+    oid = out.ids[0]
+    assert hip_lib.GetCiphertextLevel(oid) == d["out"]["level"]
+    assert hip_lib.GetCiphertextScaleDouble(oid) == d["out"]["scale"]
+    assert_rows_match(hip_lib.export_ciphertext(oid), d["out"]["rows"], "pcmm26_top repack output")
+    print("[pcmm] pcmm26_top: PCMM and repack outputs bit-exact", flush=True)
     y = w.decrypt_output(out)
     err = np.abs(y - w.expected).max()
     print(f"[pcmm] pcmm26_top: max |decrypted - expected| = {err:.3e}", flush=True)
