@@ -7,6 +7,8 @@ transform -> rescale -> hybrid fold -> bias -> decrypt -> decode.
 * pcmm26 and pcmm26 + sparse_to_top (N=2^16): bit-exact with the oracle's
   words through committed per-row SHA-256 digests
   (tests/golden/make_fullsize_digests.py).
+* queries issued on the library's two HIP streams: word for word what the
+  same queries give one at a time;
 * every config: decrypted embeddings within 2^-20 of the fp32 plaintext
   lookup (tolerance from the task statement).
 """
@@ -156,6 +158,44 @@ def test_pcmm26_bitexact_vs_oracle(hip_lib):
     # the fold leaves the output periodic with period 512: slot j+512 decrypts to row j as well
     full = np.asarray(w.scheme.decode(w.scheme.decrypt(out.__class__(w.scheme, out.ids, 2 * 512))))
     assert np.abs(full[512:512 + 416] - w.expected).max() < TOL
+    hip_lib.DeleteScheme()
+
+
+def test_pcmm_two_streams_bitexact(hip_lib):
+    """Queries issued back to back on the library's two HIP streams (query i
+    on stream i % 2, as bench.py's in-flight measurement issues them), at
+    N=2^13: every output equals the same query run alone, word for word, and
+    the first equals the restatement's PCMM -- the two streams' buffer caches
+    and shared tables never mix one query's work into another's."""
+    name = "pcmm26_n13"
+    print(f"[pcmm] {name}: two streams", flush=True)
+    w = PCMMWorkload(hip_lib, name, seed=3, key_seed=17).setup()
+    cts = [w.ct_in] + [w.make_query(1000 + k)[0] for k in range(2)]
+    ref = []
+    for ct in cts:
+        o = w.forward(ct)
+        ref.append(hip_lib.export_ciphertext(o.ids[0]))
+        o.free()
+    outs = []
+    for i in range(8):
+        hip_lib.SetStream(i % 2)
+        outs.append(w.forward(cts[i % len(cts)]))
+    hip_lib.SetStream(0)
+    hip_lib.JoinStream(1)
+    hip_lib.Synchronize()
+    for i, o in enumerate(outs):
+        assert_equal_u64(hip_lib.export_ciphertext(o.ids[0]), ref[i % len(cts)], f"{name} query {i} on stream {i % 2}")
+        o.free()
+    c = w.cfg
+    orc = O.Oracle(c["logn"], hip_lib.GetModuliChain(), hip_lib.GetAuxModuliChain(), h=c["h"], seed=17)
+    try:
+        want, _, _ = oracle_pcmm(orc, w.layer.diagonals[(0, 0)], w.layer.output_rotations, w.layer.level, w.selector,
+                                 c["logscale"], 0)
+    finally:
+        orc.close()
+    assert_equal_u64(ref[0], want, f"{name} serial output vs the restatement")
+    for ct in cts[1:]:
+        ct.free()
     hip_lib.DeleteScheme()
 
 
